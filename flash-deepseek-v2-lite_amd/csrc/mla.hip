@@ -1,0 +1,335 @@
+// Absorbed multi-head latent attention (MLA) for q_len = 1 over the compressed
+// cache: one 576-wide bf16 row per token (512 normalised latent + 64 rotated
+// k_pe), shared by all 16 heads.
+//
+//   prepare : kv-norm + RoPE(k_pe) -> cache row; RoPE(q_pe); q_lat = W_UK^T q_nope
+//   decode  : split-KV flash decoding; per workgroup one (row, split); 32-token
+//             tiles double-buffered in LDS; S^T = K Q^T and O^T += V^T P^T on
+//             v_mfma_f32_16x16x32_bf16 (16 heads = one MFMA dimension)
+//   combine : log-sum-exp merge of the splits, then W_UV (fused GEMV) or bf16 o_lat
+#include "common.h"
+
+namespace {
+constexpr int kHeads = 16;
+constexpr int kRow = 576;       // cache row (elements)
+constexpr int kLat = 512;       // latent part
+constexpr int kQkvA = 3648;     // q (16*192) | latent (512) | k_pe (64)
+constexpr int kTile = 32;       // tokens per LDS tile
+constexpr int kLdsRow = kRow + 8;  // padded LDS row (elements): 1168 bytes
+constexpr int kTileChunks = kTile * kRow / 8;  // 16-byte chunks per tile = 2304
+}  // namespace
+
+// RoPE on de-interleaved pairs: out[t] = e*cos[t] - o*sin[t], out[32+t] = o*cos[32+t] + e*sin[32+t]
+// (e, o = x[2t], x[2t+1]); lanes 0..31 each produce one pair.  fp32 math, one bf16 round.
+__device__ __forceinline__ void rope_pair(const bf16_t* x, const bf16_t* cs, const bf16_t* sn, bf16_t* out, int t) {
+  const float e = bf2f(x[2 * t]), o = bf2f(x[2 * t + 1]);
+  out[t] = f2bf(e * bf2f(cs[t]) - o * bf2f(sn[t]));
+  out[32 + t] = f2bf(o * bf2f(cs[32 + t]) + e * bf2f(sn[32 + t]));
+}
+
+template <bool ABSORB>
+__global__ __launch_bounds__(64) void mla_prepare_kernel(const bf16_t* __restrict__ qkva, int64_t qs, int rows,
+                                                         const int32_t* __restrict__ pos,
+                                                         const int64_t* __restrict__ base,
+                                                         const bf16_t* __restrict__ kvw, float eps,
+                                                         const bf16_t* __restrict__ cosT,
+                                                         const bf16_t* __restrict__ sinT, int max_pos,
+                                                         const bf16_t* __restrict__ w_uk, bf16_t* __restrict__ cache,
+                                                         bf16_t* __restrict__ qout) {
+  constexpr int RB = 16;
+  __shared__ float qn[RB][128];
+  const int b0 = blockIdx.x * RB, h = blockIdx.y, jb = blockIdx.z, lane = threadIdx.x;
+  const int nr = min(RB, rows - b0);
+  if (jb == 0) {
+    for (int r = 0; r < nr; ++r) {
+      const int b = b0 + r;
+      int p = pos[b];
+      p = p < 0 ? 0 : (p >= max_pos ? max_pos - 1 : p);
+      const bf16_t* q = qkva + b * qs;
+      const bf16_t* cs = cosT + (int64_t)p * 64;
+      const bf16_t* sn = sinT + (int64_t)p * 64;
+      if (lane < 32) rope_pair(q + h * 192 + 128, cs, sn, qout + ((int64_t)b * kHeads + h) * kRow + kLat, lane);
+      if (h == 0) {
+        float f[8], g[8];
+        unpack8(ldg16(q + 3072 + lane * 8), f);
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(f[i], f[i], ss);
+        ss = wave_sum(ss);
+        const float rs = rsqrtf(ss / static_cast<float>(kLat) + eps);
+        unpack8(ldg16(kvw + lane * 8), g);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) f[i] = g[i] * rbf(f[i] * rs);
+        bf16_t* crow = cache + (base[b] + pos[b]) * kRow;
+        *reinterpret_cast<uint4*>(crow + lane * 8) = pack8(f);
+        if (lane < 32) rope_pair(q + 3584, cs, sn, crow + kLat, lane);
+      }
+    }
+  }
+  if (!ABSORB) return;
+  for (int idx = lane; idx < nr * 128; idx += 64) {
+    const int r = idx >> 7, i = idx & 127;
+    qn[r][i] = bf2f(qkva[(b0 + r) * qs + h * 192 + i]);
+  }
+  __syncthreads();
+  float acc[RB][2];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) acc[r][0] = acc[r][1] = 0.f;
+  const bf16_t* wp = w_uk + (int64_t)h * 128 * kLat + jb * 128 + 2 * lane;
+#pragma unroll 8
+  for (int i = 0; i < 128; ++i) {
+    const uint32_t w2 = *reinterpret_cast<const uint32_t*>(wp + i * kLat);
+    const float w0 = __uint_as_float(w2 << 16), w1 = __uint_as_float(w2 & 0xffff0000u);
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      acc[r][0] = __builtin_fmaf(qn[r][i], w0, acc[r][0]);
+      acc[r][1] = __builtin_fmaf(qn[r][i], w1, acc[r][1]);
+    }
+  }
+  for (int r = 0; r < nr; ++r)
+    *reinterpret_cast<uint32_t*>(qout + ((int64_t)(b0 + r) * kHeads + h) * kRow + jb * 128 + 2 * lane) =
+        pack2(acc[r][0], acc[r][1]);
+}
+
+extern "C" int dsv2_mla_prepare(const void* qkva, int64_t qkva_stride, int rows, const int32_t* pos,
+                                const int64_t* base, const void* kv_norm_w, float eps, const void* rope_cos,
+                                const void* rope_sin, int max_pos, const void* w_uk, void* cache, void* q_out,
+                                void* stream) {
+  DSV2_REQUIRE(qkva && pos && base && kv_norm_w && rope_cos && rope_sin && cache && q_out, DSV2_E_NULL,
+               "mla_prepare: null pointer");
+  DSV2_REQUIRE(rows >= 0 && max_pos > 0 && qkva_stride >= kQkvA, DSV2_E_SHAPE, "mla_prepare: bad shape");
+  DSV2_REQUIRE(dsv2_aligned16(qkva) && qkva_stride % 8 == 0 && dsv2_aligned16(kv_norm_w) && dsv2_aligned16(cache) &&
+                   dsv2_aligned16(q_out) && (!w_uk || dsv2_aligned16(w_uk)),
+               DSV2_E_ALIGN, "mla_prepare: alignment");
+  if (rows == 0) return DSV2_OK;
+  const dim3 grid((rows + 15) / 16, kHeads, w_uk ? 4 : 1);
+  if (w_uk)
+    hipLaunchKernelGGL(mla_prepare_kernel<true>, grid, dim3(64), 0, (hipStream_t)stream, (const bf16_t*)qkva,
+                       qkva_stride, rows, pos, base, (const bf16_t*)kv_norm_w, eps, (const bf16_t*)rope_cos,
+                       (const bf16_t*)rope_sin, max_pos, (const bf16_t*)w_uk, (bf16_t*)cache, (bf16_t*)q_out);
+  else
+    hipLaunchKernelGGL(mla_prepare_kernel<false>, grid, dim3(64), 0, (hipStream_t)stream, (const bf16_t*)qkva,
+                       qkva_stride, rows, pos, base, (const bf16_t*)kv_norm_w, eps, (const bf16_t*)rope_cos,
+                       (const bf16_t*)rope_sin, max_pos, nullptr, (bf16_t*)cache, (bf16_t*)q_out);
+  return dsv2_launch_status("mla_prepare");
+}
+
+// ---------------------------------------------------------------------------
+// split-KV decode
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256, 2) void mla_decode_kernel(const bf16_t* __restrict__ q,
+                                                            const bf16_t* __restrict__ cache,
+                                                            const int64_t* __restrict__ base,
+                                                            const int32_t* __restrict__ pos, int split_tokens,
+                                                            int max_splits, float scale_log2,
+                                                            float* __restrict__ part_o, float* __restrict__ part_ml) {
+  __shared__ __attribute__((aligned(16))) bf16_t lds[2][kTile * kLdsRow];
+  const int s = blockIdx.x, b = blockIdx.y;
+  const int len = pos[b] + 1;
+  const int t_begin = s * split_tokens;
+  if (t_begin >= len) return;
+  const int t_end = min(len, t_begin + split_tokens);
+  const int ntiles = (t_end - t_begin + kTile - 1) / kTile;
+  const bf16_t* crow = cache + base[b] * kRow;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, li = lane & 15, kg = lane >> 4;
+
+  // Q^T fragments (B operand): head li, dims kk*32 + kg*8 .. +8
+  bf16x8_t qf[18];
+  {
+    const bf16_t* qh = q + ((int64_t)b * kHeads + li) * kRow + kg * 8;
+#pragma unroll
+    for (int kk = 0; kk < 18; ++kk) qf[kk] = as_bf16x8(ldg16(qh + kk * 32));
+  }
+
+  uint4 stage[9];
+  auto load_tile = [&](int t0) {
+#pragma unroll
+    for (int i = 0; i < 9; ++i) {
+      const int c = tid + 256 * i;
+      const int tok = c / 72, off = (c % 72) * 8;
+      const int tt = min(t0 + tok, t_end - 1);
+      stage[i] = ldg16(crow + (int64_t)tt * kRow + off);
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 9; ++i) {
+      const int c = tid + 256 * i;
+      const int tok = c / 72, off = (c % 72) * 8;
+      *reinterpret_cast<uint4*>(&lds[buf][tok * kLdsRow + off]) = stage[i];
+    }
+  };
+
+  load_tile(t_begin);
+  store_tile(0);
+  __syncthreads();
+
+  float m_run = -INFINITY, l_run = 0.f;
+  floatx4_t acc[8];
+#pragma unroll
+  for (int mb = 0; mb < 8; ++mb) acc[mb] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+
+  for (int it = 0; it < ntiles; ++it) {
+    const int buf = it & 1;
+    const int t0 = t_begin + it * kTile;
+    if (it + 1 < ntiles) load_tile(t0 + kTile);
+    const bf16_t* L = lds[buf];
+
+    // S^T = K Q^T for two 16-token blocks: sc[blk][e] = score(token blk*16 + 4kg + e, head li)
+    floatx4_t sc[2];
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) {
+      sc[blk] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+      const bf16_t* kr = L + (blk * 16 + li) * kLdsRow + kg * 8;
+#pragma unroll
+      for (int kk = 0; kk < 18; ++kk)
+        sc[blk] = mfma16x16x32(*reinterpret_cast<const bf16x8_t*>(kr + kk * 32), qf[kk], sc[blk]);
+    }
+    float p[8];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int tok = t0 + blk * 16 + 4 * kg + e;
+        const float v = tok < t_end ? sc[blk][e] * scale_log2 : -INFINITY;
+        p[blk * 4 + e] = v;
+        mx = fmaxf(mx, v);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = exp2f(m_run - m_new);
+    float rsum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      p[i] = exp2f(p[i] - m_new);
+      rsum += p[i];
+    }
+    rsum += __shfl_xor(rsum, 16, 64);
+    rsum += __shfl_xor(rsum, 32, 64);
+    l_run = l_run * alpha + rsum;
+    m_run = m_new;
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) acc[mb] *= alpha;
+
+    // P^T (B operand): head li, tokens {4kg+e} then {16+4kg+e}; V^T (A operand) uses the same token order
+    const bf16x8_t pb = as_bf16x8(pack8(p));
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) {
+      const int d = wv * 128 + mb * 16 + li;
+      const bf16_t* vc = L + d;
+      uint4 av;
+      av.x = (uint32_t)vc[(4 * kg + 0) * kLdsRow] | ((uint32_t)vc[(4 * kg + 1) * kLdsRow] << 16);
+      av.y = (uint32_t)vc[(4 * kg + 2) * kLdsRow] | ((uint32_t)vc[(4 * kg + 3) * kLdsRow] << 16);
+      av.z = (uint32_t)vc[(16 + 4 * kg + 0) * kLdsRow] | ((uint32_t)vc[(16 + 4 * kg + 1) * kLdsRow] << 16);
+      av.w = (uint32_t)vc[(16 + 4 * kg + 2) * kLdsRow] | ((uint32_t)vc[(16 + 4 * kg + 3) * kLdsRow] << 16);
+      acc[mb] = mfma16x16x32(as_bf16x8(av), pb, acc[mb]);
+    }
+    if (it + 1 < ntiles) {
+      // buf^1 was last read in iteration it-1, which every wave finished before the
+      // barrier that ended it; one barrier after the store publishes tile it+1.
+      store_tile(buf ^ 1);
+      __syncthreads();
+    }
+  }
+  // O^T layout: lane holds head li, dims wv*128 + mb*16 + 4kg + e
+  float* po = part_o + (((int64_t)b * max_splits + s) * kHeads + li) * kLat + wv * 128 + 4 * kg;
+#pragma unroll
+  for (int mb = 0; mb < 8; ++mb)
+    *reinterpret_cast<float4*>(po + mb * 16) = make_float4(acc[mb][0], acc[mb][1], acc[mb][2], acc[mb][3]);
+  if (wv == 0 && kg == 0) {
+    float* pm = part_ml + (((int64_t)b * max_splits + s) * kHeads + li) * 2;
+    pm[0] = m_run;
+    pm[1] = l_run;
+  }
+}
+
+extern "C" int dsv2_mla_decode(const void* q, const void* cache, const int64_t* base, const int32_t* pos, int rows,
+                               int split_tokens, int max_splits, float softmax_scale, float* part_o, float* part_ml,
+                               void* stream) {
+  DSV2_REQUIRE(q && cache && base && pos && part_o && part_ml, DSV2_E_NULL, "mla_decode: null pointer");
+  DSV2_REQUIRE(rows >= 0 && rows <= 65535 && split_tokens > 0 && split_tokens % kTile == 0 && max_splits > 0 &&
+                   max_splits <= 64,
+               DSV2_E_SHAPE, "mla_decode: bad shape (split_tokens %% 32, 1 <= max_splits <= 64)");
+  DSV2_REQUIRE(dsv2_aligned16(q) && dsv2_aligned16(cache) && dsv2_aligned16(part_o), DSV2_E_ALIGN,
+               "mla_decode: alignment");
+  if (rows == 0) return DSV2_OK;
+  const float scale_log2 = softmax_scale * 1.4426950408889634f;
+  hipLaunchKernelGGL(mla_decode_kernel, dim3(max_splits, rows), dim3(256), 0, (hipStream_t)stream,
+                     (const bf16_t*)q, (const bf16_t*)cache, base, pos, split_tokens, max_splits, scale_log2, part_o,
+                     part_ml);
+  return dsv2_launch_status("mla_decode");
+}
+
+// ---------------------------------------------------------------------------
+// combine (+ W_UV)
+// ---------------------------------------------------------------------------
+template <bool UV>
+__global__ __launch_bounds__(256) void mla_combine_kernel(const float* __restrict__ part_o,
+                                                          const float* __restrict__ part_ml,
+                                                          const int32_t* __restrict__ pos, int split_tokens,
+                                                          int max_splits, const bf16_t* __restrict__ w_uv,
+                                                          bf16_t* __restrict__ out, int64_t os) {
+  __shared__ float olat[kLat];
+  __shared__ float wsp[64];
+  const int b = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int len = pos[b] + 1;
+  const int ns = min((len + split_tokens - 1) / split_tokens, max_splits);
+  if (wv == 0) {
+    const float* pm = part_ml + ((int64_t)b * max_splits * kHeads + h) * 2;
+    const float m = lane < ns ? pm[(int64_t)lane * kHeads * 2] : -INFINITY;
+    const float M = wave_max(m);
+    const float w = lane < ns ? exp2f(m - M) : 0.f;
+    const float l = lane < ns ? pm[(int64_t)lane * kHeads * 2 + 1] : 0.f;
+    const float Lsum = wave_sum(w * l);
+    wsp[lane] = w / Lsum;
+  }
+  __syncthreads();
+  float o0 = 0.f, o1 = 0.f;
+  const float* po = part_o + ((int64_t)b * max_splits * kHeads + h) * kLat + 2 * tid;
+  for (int s = 0; s < ns; ++s) {
+    const float2 v = *reinterpret_cast<const float2*>(po + (int64_t)s * kHeads * kLat);
+    o0 = __builtin_fmaf(wsp[s], v.x, o0);
+    o1 = __builtin_fmaf(wsp[s], v.y, o1);
+  }
+  if (!UV) {
+    *reinterpret_cast<uint32_t*>(out + b * os + h * kLat + 2 * tid) = pack2(o0, o1);
+    return;
+  }
+  olat[2 * tid] = o0;
+  olat[2 * tid + 1] = o1;
+  __syncthreads();
+  float xo[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) xo[e] = olat[lane * 8 + e];
+  const bf16_t* wp = w_uv + ((int64_t)h * 128 + wv * 32) * kLat + lane * 8;
+  float r[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) r[i] = dot8(ldg16(wp + i * kLat), xo);
+#pragma unroll
+  for (int i = 0; i < 32; ++i) r[i] = wave_sum(r[i]);
+  if (lane == 0) {
+    bf16_t* o = out + b * os + h * 128 + wv * 32;
+#pragma unroll
+    for (int i = 0; i < 32; i += 2) *reinterpret_cast<uint32_t*>(o + i) = pack2(r[i], r[i + 1]);
+  }
+}
+
+extern "C" int dsv2_mla_combine(const float* part_o, const float* part_ml, const int32_t* pos, int rows,
+                                int split_tokens, int max_splits, const void* w_uv, void* out, int64_t out_stride,
+                                void* stream) {
+  DSV2_REQUIRE(part_o && part_ml && pos && out, DSV2_E_NULL, "mla_combine: null pointer");
+  DSV2_REQUIRE(rows >= 0 && rows <= 65535 && split_tokens > 0 && max_splits > 0 && max_splits <= 64, DSV2_E_SHAPE,
+               "mla_combine: bad shape");
+  DSV2_REQUIRE(out_stride % 8 == 0 && dsv2_aligned16(out) && (!w_uv || dsv2_aligned16(w_uv)), DSV2_E_ALIGN,
+               "mla_combine: alignment");
+  if (rows == 0) return DSV2_OK;
+  if (w_uv)
+    hipLaunchKernelGGL(mla_combine_kernel<true>, dim3(rows, kHeads), dim3(256), 0, (hipStream_t)stream, part_o,
+                       part_ml, pos, split_tokens, max_splits, (const bf16_t*)w_uv, (bf16_t*)out, out_stride);
+  else
+    hipLaunchKernelGGL(mla_combine_kernel<false>, dim3(rows, kHeads), dim3(256), 0, (hipStream_t)stream, part_o,
+                       part_ml, pos, split_tokens, max_splits, nullptr, (bf16_t*)out, out_stride);
+  return dsv2_launch_status("mla_combine");
+}

@@ -1,0 +1,428 @@
+// MoE for DeepSeek-V2-Lite (64 routed experts, top-6, inter 1408, 2 shared experts):
+// router (+ fused post-attention RMSNorm), small-family route-local GEMV kernels,
+// batch-family deterministic bucketing and the final weighted combine.
+#include "common.h"
+
+namespace {
+constexpr int kH = 2048;
+constexpr int kE = 64;
+constexpr int kTopK = 6;
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// router: one workgroup per token.  xn = RMSNorm(h); logits = fp32(xn).fp32(W_r)
+// (bf16 x bf16 products are exact in fp32); softmax; top-6 by repeated max with
+// ties to the lower index.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void router_kernel(const bf16_t* __restrict__ h, int64_t hs,
+                                                     const bf16_t* __restrict__ nw, float eps,
+                                                     const bf16_t* __restrict__ wr, float scaling,
+                                                     bf16_t* __restrict__ xn_out, const float* __restrict__ logits_in,
+                                                     int32_t* __restrict__ ids32, int64_t* __restrict__ ids64,
+                                                     float* __restrict__ wts) {
+  __shared__ float xs[kH];
+  __shared__ float lg[kE];
+  __shared__ float red[4];
+  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  if (!logits_in) {
+    float f[8], g[8];
+    unpack8(ldg16(h + b * hs + tid * 8), f);
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(f[i], f[i], ss);
+    ss = block_sum<4>(ss, red);
+    const float rs = rsqrtf(ss / static_cast<float>(kH) + eps);
+    unpack8(ldg16(nw + tid * 8), g);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      f[i] = rbf(g[i] * rbf(f[i] * rs));
+      xs[tid * 8 + i] = f[i];
+    }
+    if (xn_out) *reinterpret_cast<uint4*>(xn_out + (int64_t)b * kH + tid * 8) = pack8(f);
+    __syncthreads();
+    float xl[32];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xl[j * 8 + i] = xs[(lane + 64 * j) * 8 + i];
+    for (int e16 = 0; e16 < 16; ++e16) {
+      const int e = wv * 16 + e16;
+      const bf16_t* we = wr + (int64_t)e * kH;
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc += dot8(ldg16(we + (lane + 64 * j) * 8), xl + j * 8);
+      acc = wave_sum(acc);
+      if (lane == 0) lg[e] = acc;
+    }
+    __syncthreads();
+  } else {
+    if (tid < kE) lg[tid] = logits_in[(int64_t)b * kE + tid];
+    __syncthreads();
+  }
+  if (wv == 0) {
+    const float x = lg[lane];
+    const float mx = wave_max(x);
+    const float ex = expf(x - mx);
+    const float sm = wave_sum(ex);
+    float v = ex / sm;
+    for (int s = 0; s < kTopK; ++s) {
+      float bv = v;
+      int bi = lane;
+      wave_argmax(bv, bi);
+      if (lane == 0) {
+        if (ids32) ids32[b * kTopK + s] = bi;
+        if (ids64) ids64[b * kTopK + s] = bi;
+        wts[b * kTopK + s] = bv * scaling;
+      }
+      if (lane == bi) v = -INFINITY;
+    }
+  }
+}
+
+extern "C" int dsv2_router_topk6(const void* h, int64_t h_stride, const void* norm_w, float eps, const void* w_router,
+                                 float scaling, int rows, void* xn_out, int32_t* ids32, int64_t* ids64, float* weights,
+                                 void* stream) {
+  DSV2_REQUIRE(h && norm_w && w_router && weights && (ids32 || ids64), DSV2_E_NULL, "router: null pointer");
+  DSV2_REQUIRE(rows >= 0 && rows <= 0x7fffffff / kTopK, DSV2_E_SHAPE, "router: bad rows");
+  DSV2_REQUIRE(dsv2_aligned16(h) && h_stride % 8 == 0 && dsv2_aligned16(norm_w) && dsv2_aligned16(w_router) &&
+                   (!xn_out || dsv2_aligned16(xn_out)),
+               DSV2_E_ALIGN, "router: alignment");
+  if (rows == 0) return DSV2_OK;
+  hipLaunchKernelGGL(router_kernel, dim3(rows), dim3(256), 0, (hipStream_t)stream, (const bf16_t*)h, h_stride,
+                     (const bf16_t*)norm_w, eps, (const bf16_t*)w_router, scaling, (bf16_t*)xn_out, nullptr, ids32,
+                     ids64, weights);
+  return dsv2_launch_status("router");
+}
+
+extern "C" int dsv2_router_topk6_from_logits(const float* logits, int rows, float scaling, int32_t* ids32,
+                                             int64_t* ids64, float* weights, void* stream) {
+  DSV2_REQUIRE(logits && weights && (ids32 || ids64), DSV2_E_NULL, "router_from_logits: null pointer");
+  DSV2_REQUIRE(rows >= 0, DSV2_E_SHAPE, "router_from_logits: bad rows");
+  if (rows == 0) return DSV2_OK;
+  hipLaunchKernelGGL(router_kernel, dim3(rows), dim3(256), 0, (hipStream_t)stream, nullptr, 0, nullptr, 0.f, nullptr,
+                     scaling, nullptr, logits, ids32, ids64, weights);
+  return dsv2_launch_status("router_from_logits");
+}
+
+// ---------------------------------------------------------------------------
+// small family: route-local gate_up + SwiGLU.  grid (inter/(4*RPW), rows*NR)
+// route r*NR+s: s < 6 -> routed expert ids[r,s]; s = 6, 7 -> shared-expert half.
+// ---------------------------------------------------------------------------
+template <int RPW>
+__global__ __launch_bounds__(256) void route_gateup_kernel(const bf16_t* __restrict__ xn,
+                                                           const int32_t* __restrict__ ids, int nr,
+                                                           const bf16_t* __restrict__ wgu,
+                                                           const bf16_t* __restrict__ shgu, int inter,
+                                                           bf16_t* __restrict__ hbuf) {
+  const int route = blockIdx.y;
+  const int b = route / nr, s = route % nr;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int i0 = (blockIdx.x * 4 + wv) * RPW;
+  if (i0 >= inter) return;
+  const bf16_t *gp, *up;
+  if (s < kTopK) {
+    const int e = min(max(ids[b * kTopK + s], 0), kE - 1);
+    gp = wgu + (int64_t)e * 2 * inter * kH;
+    up = gp + (int64_t)inter * kH;
+  } else {
+    const int half = s - kTopK;
+    gp = shgu + (int64_t)half * inter * kH;
+    up = shgu + (int64_t)(2 * inter + half * inter) * kH;
+  }
+  gp += (int64_t)i0 * kH;
+  up += (int64_t)i0 * kH;
+  float xf[32];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) unpack8(ldg16(xn + (int64_t)b * kH + (lane + 64 * j) * 8), xf + j * 8);
+  uint4 wg[RPW][4], wu[RPW][4];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      wg[r][j] = ldg16(gp + (int64_t)r * kH + (lane + 64 * j) * 8);
+      wu[r][j] = ldg16(up + (int64_t)r * kH + (lane + 64 * j) * 8);
+    }
+  float ag[RPW], au[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    ag[r] = au[r] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      ag[r] += dot8(wg[r][j], xf + j * 8);
+      au[r] += dot8(wu[r][j], xf + j * 8);
+    }
+    ag[r] = wave_sum(ag[r]);
+    au[r] = wave_sum(au[r]);
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) hbuf[(int64_t)route * inter + i0 + r] = f2bf(swiglu_bf(ag[r], au[r]));
+  }
+}
+
+extern "C" int dsv2_moe_route_gateup(const void* xn, int rows, const int32_t* ids, const void* w_gate_up,
+                                     const void* sh_gate_up, int inter, void* hbuf, void* stream) {
+  DSV2_REQUIRE(xn && ids && w_gate_up && hbuf, DSV2_E_NULL, "moe_route_gateup: null pointer");
+  const int nr = sh_gate_up ? kTopK + 2 : kTopK;
+  DSV2_REQUIRE(rows >= 0 && (int64_t)rows * nr <= 65535 && inter > 0 && inter % 8 == 0, DSV2_E_SHAPE,
+               "moe_route_gateup: bad shape");
+  DSV2_REQUIRE(dsv2_aligned16(xn) && dsv2_aligned16(w_gate_up) && (!sh_gate_up || dsv2_aligned16(sh_gate_up)),
+               DSV2_E_ALIGN, "moe_route_gateup: alignment");
+  if (rows == 0) return DSV2_OK;
+  constexpr int RPW = 2;
+  hipLaunchKernelGGL(route_gateup_kernel<RPW>, dim3((inter + 4 * RPW - 1) / (4 * RPW), rows * nr), dim3(256), 0,
+                     (hipStream_t)stream, (const bf16_t*)xn, ids, nr, (const bf16_t*)w_gate_up,
+                     (const bf16_t*)sh_gate_up, inter, (bf16_t*)hbuf);
+  return dsv2_launch_status("moe_route_gateup");
+}
+
+// ---------------------------------------------------------------------------
+// small family: down projection of every route of a token + weighted top-6 sum
+// (+ shared halves, + residual), deterministic (no atomics). grid (2048/(4*RPW), rows)
+// ---------------------------------------------------------------------------
+template <int NR, int RPW>
+__global__ __launch_bounds__(256) void route_down_kernel(const bf16_t* __restrict__ hbuf,
+                                                         const int32_t* __restrict__ ids,
+                                                         const float* __restrict__ wts,
+                                                         const bf16_t* __restrict__ wd,
+                                                         const bf16_t* __restrict__ shd, int inter,
+                                                         const bf16_t* __restrict__ res, bf16_t* __restrict__ out) {
+  const int b = blockIdx.y;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int j0 = (blockIdx.x * 4 + wv) * RPW;
+  if (j0 >= kH) return;
+  const bf16_t* wrow[NR];
+  int64_t wstride[NR];
+#pragma unroll
+  for (int s = 0; s < NR; ++s) {
+    if (s < kTopK) {
+      wrow[s] = wd + (int64_t)min(max(ids[b * kTopK + s], 0), kE - 1) * kH * inter + (int64_t)j0 * inter;
+      wstride[s] = inter;
+    } else {
+      wrow[s] = shd + (int64_t)(s - kTopK) * inter + (int64_t)j0 * 2 * inter;
+      wstride[s] = 2 * inter;
+    }
+  }
+  const bf16_t* hb = hbuf + (int64_t)b * NR * inter;
+  float acc[NR][RPW];
+#pragma unroll
+  for (int s = 0; s < NR; ++s)
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) acc[s][r] = 0.f;
+  const int nch = inter >> 3;
+  for (int c = lane; c < nch; c += 64) {
+    uint4 w[NR][RPW];
+#pragma unroll
+    for (int s = 0; s < NR; ++s)
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) w[s][r] = ldg16(wrow[s] + r * wstride[s] + c * 8);
+#pragma unroll
+    for (int s = 0; s < NR; ++s) {
+      float hx[8];
+      unpack8(ldg16(hb + (int64_t)s * inter + c * 8), hx);
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) acc[s][r] += dot8(w[s][r], hx);
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < NR; ++s)
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) acc[s][r] = wave_sum(acc[s][r]);
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      float routed = 0.f;
+#pragma unroll
+      for (int s = 0; s < kTopK; ++s) routed += wts[b * kTopK + s] * rbf(acc[s][r]);
+      float y = rbf(routed);
+      if (NR > kTopK) y = rbf(y + rbf(acc[kTopK][r] + acc[kTopK + 1][r]));
+      if (res) y = rbf(bf2f(res[(int64_t)b * kH + j0 + r]) + y);
+      out[(int64_t)b * kH + j0 + r] = f2bf(y);
+    }
+  }
+}
+
+extern "C" int dsv2_moe_route_down(const void* hbuf, int rows, const int32_t* ids, const float* weights,
+                                   const void* w_down, const void* sh_down, int inter, const void* residual, void* out,
+                                   void* stream) {
+  DSV2_REQUIRE(hbuf && ids && weights && w_down && out, DSV2_E_NULL, "moe_route_down: null pointer");
+  DSV2_REQUIRE(rows >= 0 && rows <= 65535 && inter > 0 && inter % 8 == 0, DSV2_E_SHAPE, "moe_route_down: bad shape");
+  DSV2_REQUIRE(dsv2_aligned16(hbuf) && dsv2_aligned16(w_down) && (!sh_down || dsv2_aligned16(sh_down)),
+               DSV2_E_ALIGN, "moe_route_down: alignment");
+  if (rows == 0) return DSV2_OK;
+  constexpr int RPW = 2;
+  const dim3 grid(kH / (4 * RPW), rows);
+  if (sh_down)
+    hipLaunchKernelGGL((route_down_kernel<kTopK + 2, RPW>), grid, dim3(256), 0, (hipStream_t)stream,
+                       (const bf16_t*)hbuf, ids, weights, (const bf16_t*)w_down, (const bf16_t*)sh_down, inter,
+                       (const bf16_t*)residual, (bf16_t*)out);
+  else
+    hipLaunchKernelGGL((route_down_kernel<kTopK, RPW>), grid, dim3(256), 0, (hipStream_t)stream, (const bf16_t*)hbuf,
+                       ids, weights, (const bf16_t*)w_down, nullptr, inter, (const bf16_t*)residual, (bf16_t*)out);
+  return dsv2_launch_status("moe_route_down");
+}
+
+// ---------------------------------------------------------------------------
+// batch family bucketing: one workgroup of 16 waves.  Routes are processed in
+// 64-route chunks; a route's slot = expert start + routes of the same expert in
+// earlier chunks + earlier lanes of its own chunk, so the order is stable in the
+// route index and the result is deterministic (no atomics).
+// ---------------------------------------------------------------------------
+constexpr int kMaxRoutes = 8192;
+constexpr int kMaxChunks = kMaxRoutes / 64;
+
+__global__ __launch_bounds__(1024) void bucket_kernel(const int32_t* __restrict__ ids, int R, int tile_tokens,
+                                                      int32_t* __restrict__ sorted_routes,
+                                                      int32_t* __restrict__ route_pos, int32_t* __restrict__ tiles,
+                                                      int32_t* __restrict__ num_tiles) {
+  __shared__ uint16_t hist[kMaxChunks][kE];  // 16 KB: per-chunk counts, then exclusive prefix over chunks
+  __shared__ uint8_t rank[kMaxRoutes];
+  __shared__ uint8_t expert[kMaxRoutes];
+  __shared__ int start[kE], tstart[kE], total[kE];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int nchunks = (R + 63) / 64;
+  for (int i = tid; i < nchunks * kE; i += 1024) hist[i / kE][i % kE] = 0;
+  __syncthreads();
+  for (int c = wv; c < nchunks; c += 16) {
+    const int r = c * 64 + lane;
+    const int e = r < R ? min(max(ids[r], 0), kE - 1) : -1;
+    int before = 0, after = 0;
+    for (int j = 0; j < 64; ++j) {
+      const int ej = __shfl(e, j, 64);
+      before += (j < lane && ej == e) ? 1 : 0;
+      after += (j > lane && ej == e) ? 1 : 0;
+    }
+    if (r < R) {
+      rank[r] = (uint8_t)before;
+      expert[r] = (uint8_t)e;
+      if (after == 0) hist[c][e] = (uint16_t)(before + 1);
+    }
+  }
+  __syncthreads();
+  if (tid < kE) {
+    int run = 0;
+    for (int c = 0; c < nchunks; ++c) {
+      const int t = hist[c][tid];
+      hist[c][tid] = (uint16_t)run;
+      run += t;
+    }
+    total[tid] = run;
+  }
+  __syncthreads();
+  if (wv == 0) {
+    const int tot = total[lane];
+    const int nt = (tot + tile_tokens - 1) / tile_tokens;
+    int incl = tot, tincl = nt;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int a = __shfl_up(incl, o, 64), bt = __shfl_up(tincl, o, 64);
+      if (lane >= o) {
+        incl += a;
+        tincl += bt;
+      }
+    }
+    start[lane] = incl - tot;
+    tstart[lane] = tincl - nt;
+    if (lane == 63) num_tiles[0] = tincl;
+  }
+  __syncthreads();
+  for (int r = tid; r < R; r += 1024) {
+    const int e = expert[r];
+    const int p = start[e] + hist[r >> 6][e] + rank[r];
+    sorted_routes[p] = r;
+    route_pos[r] = p;
+  }
+  for (int e = wv; e < kE; e += 16) {
+    const int tot = total[e];
+    const int nt = (tot + tile_tokens - 1) / tile_tokens;
+    for (int i = lane; i < nt; i += 64) {
+      int4 t;
+      t.x = e;
+      t.y = start[e] + i * tile_tokens;
+      t.z = min(tile_tokens, tot - i * tile_tokens);
+      t.w = 0;
+      reinterpret_cast<int4*>(tiles)[tstart[e] + i] = t;
+    }
+  }
+}
+
+extern "C" int dsv2_moe_bucket(const int32_t* ids, int rows, int tile_tokens, int32_t* sorted_routes,
+                               int32_t* route_pos, int32_t* tiles, int32_t* num_tiles, void* stream) {
+  DSV2_REQUIRE(ids && sorted_routes && route_pos && tiles && num_tiles, DSV2_E_NULL, "moe_bucket: null pointer");
+  DSV2_REQUIRE(rows >= 0 && rows * kTopK <= kMaxRoutes && tile_tokens >= 1 && tile_tokens <= 64, DSV2_E_SHAPE,
+               "moe_bucket: rows*6 must be <= %d (got %d)", kMaxRoutes, rows * kTopK);
+  DSV2_REQUIRE(dsv2_aligned16(tiles), DSV2_E_ALIGN, "moe_bucket: tiles must be 16-byte aligned");
+  hipLaunchKernelGGL(bucket_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, ids, rows * kTopK, tile_tokens,
+                     sorted_routes, route_pos, tiles, num_tiles);
+  return dsv2_launch_status("moe_bucket");
+}
+
+// ---------------------------------------------------------------------------
+// combine: one workgroup per token (256 threads x 8 elements)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void moe_combine_kernel(const bf16_t* __restrict__ ys,
+                                                          const int32_t* __restrict__ route_pos,
+                                                          const float* __restrict__ wts,
+                                                          const bf16_t* __restrict__ shared,
+                                                          const bf16_t* __restrict__ res, bf16_t* __restrict__ out,
+                                                          const bf16_t* __restrict__ nw, float eps,
+                                                          bf16_t* __restrict__ xn) {
+  __shared__ float red[4];
+  const int b = blockIdx.x, tid = threadIdx.x;
+  float acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+#pragma unroll
+  for (int s = 0; s < kTopK; ++s) {
+    const int p = route_pos[b * kTopK + s];
+    const float w = wts[b * kTopK + s];
+    float f[8];
+    unpack8(ldg16(ys + (int64_t)p * kH + tid * 8), f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] += w * f[i];
+  }
+  float y[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) y[i] = rbf(acc[i]);
+  if (shared) {
+    float f[8];
+    unpack8(ldg16(shared + (int64_t)b * kH + tid * 8), f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = rbf(y[i] + f[i]);
+  }
+  if (res) {
+    float f[8];
+    unpack8(ldg16(res + (int64_t)b * kH + tid * 8), f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = rbf(f[i] + y[i]);
+  }
+  *reinterpret_cast<uint4*>(out + (int64_t)b * kH + tid * 8) = pack8(y);
+  if (nw) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(y[i], y[i], ss);
+    ss = block_sum<4>(ss, red);
+    const float rs = rsqrtf(ss / static_cast<float>(kH) + eps);
+    float g[8];
+    unpack8(ldg16(nw + tid * 8), g);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = g[i] * rbf(y[i] * rs);
+    *reinterpret_cast<uint4*>(xn + (int64_t)b * kH + tid * 8) = pack8(y);
+  }
+}
+
+extern "C" int dsv2_moe_combine(const void* ysorted, const int32_t* route_pos, const float* weights, int rows,
+                                const void* shared, const void* residual, void* out, const void* next_norm_w, float eps,
+                                void* xn_out, void* stream) {
+  DSV2_REQUIRE(ysorted && route_pos && weights && out && (!next_norm_w || xn_out), DSV2_E_NULL,
+               "moe_combine: null pointer");
+  DSV2_REQUIRE(rows >= 0, DSV2_E_SHAPE, "moe_combine: bad rows");
+  DSV2_REQUIRE(dsv2_aligned16(ysorted) && dsv2_aligned16(out) && (!shared || dsv2_aligned16(shared)) &&
+                   (!residual || dsv2_aligned16(residual)) && (!xn_out || dsv2_aligned16(xn_out)),
+               DSV2_E_ALIGN, "moe_combine: alignment");
+  if (rows == 0) return DSV2_OK;
+  hipLaunchKernelGGL(moe_combine_kernel, dim3(rows), dim3(256), 0, (hipStream_t)stream, (const bf16_t*)ysorted,
+                     route_pos, weights, (const bf16_t*)shared, (const bf16_t*)residual, (bf16_t*)out,
+                     (const bf16_t*)next_norm_w, eps, (bf16_t*)xn_out);
+  return dsv2_launch_status("moe_combine");
+}

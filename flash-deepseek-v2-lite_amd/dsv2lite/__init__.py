@@ -1,0 +1,9 @@
+"""MI355X-native host runtime for the DeepSeek-V2-Lite decode step (HIP kernels via triton_kernels._hip)."""
+
+from .config import DSV2Config
+from .cache import CompressedKVCache
+from .weights import LayerWeights, ModelWeights, init_weights, pack_hf_layer
+from .engine import DecodeEngine, FAMILIES, plan_splits, moe_tile_tokens
+
+__all__ = ["DSV2Config", "CompressedKVCache", "LayerWeights", "ModelWeights", "init_weights", "pack_hf_layer",
+           "DecodeEngine", "FAMILIES", "plan_splits", "moe_tile_tokens"]

@@ -1,0 +1,53 @@
+"""Compressed MLA KV cache in HBM.
+
+Layout: one bf16 tensor [n_layers, total_tokens, 576]; sequence b owns rows
+[base[b], base[b] + capacity[b]) of every layer.  A row is the kv-normalised
+512-d latent followed by the 64-d rotated k_pe (1,152 bytes per token per
+layer, vs. 10,240 for the reference's expanded K/V cache, src/run.py:81-99).
+
+``pos[b]`` (int32, device) is the number of cached tokens of sequence b, i.e.
+the position of its next token; the decode step writes row base+pos and the
+argmax kernel advances pos.  Rows at or beyond pos are never read, so
+snapshot/restore of the prompt state (src/run.py:161-170, 212-217, 547-555) only
+saves and restores ``pos``.
+"""
+
+from __future__ import annotations
+
+import torch
+
+
+class CompressedKVCache:
+    def __init__(self, n_layers: int, capacities: list[int], device="cuda", row: int = 576):
+        if not capacities or min(capacities) <= 0:
+            raise ValueError("capacities must be positive")
+        self.n_layers = n_layers
+        self.capacities = list(int(c) for c in capacities)
+        bases = [0]
+        for c in self.capacities[:-1]:
+            bases.append(bases[-1] + c)
+        self.total = bases[-1] + self.capacities[-1]
+        self.row = row
+        self.data = torch.zeros(n_layers, self.total, row, dtype=torch.bfloat16, device=device)
+        self.base = torch.tensor(bases, dtype=torch.int64, device=device)
+        self.pos = torch.zeros(len(capacities), dtype=torch.int32, device=device)
+        self.max_capacity = max(self.capacities)
+
+    @property
+    def batch(self) -> int:
+        return len(self.capacities)
+
+    def layer(self, i: int) -> torch.Tensor:
+        return self.data[i]
+
+    def snapshot(self) -> torch.Tensor:
+        return self.pos.clone()
+
+    def restore(self, snap: torch.Tensor) -> None:
+        self.pos.copy_(snap)
+
+    def rows_of(self, b: int, layer: int, n: int | None = None) -> torch.Tensor:
+        """The cached rows of sequence b in a layer (host-synchronising; for checks)."""
+        n = int(self.pos[b].item()) if n is None else n
+        s = int(self.base[b].item())
+        return self.data[layer, s:s + n]

@@ -1,0 +1,300 @@
+"""The DeepSeek-V2-Lite q_len=1 decode step on HIP kernels, and its prefill.
+
+One ``step()`` enqueues the whole 27-layer step (embedding gather, per layer
+attention + MLP/MoE, final norm, lm_head, greedy argmax, position advance) on
+torch's current stream; ``capture()`` records it once into a hipGraph
+(torch.cuda.CUDAGraph) and ``replay()`` re-launches it.  Mirrors
+``_graph_decode_step`` / ``_run_graph_decode`` (src/run.py:558-688).
+
+Kernel families (``--kernel-family``, src/run.py:53-65):
+  small -- VALU GEMV with fused RMSNorm prologue and residual epilogue; fused
+           MLA prepare (RoPE + cache write + W_UK absorption) and fused
+           combine + W_UV; route-local MoE over 6 routed + 2 shared "half"
+           experts with a deterministic in-workgroup top-6 combine.
+  batch -- bf16 MFMA grouped GEMM for every projection (heads-batched W_UK /
+           W_UV), deterministic expert bucketing, expert-grouped gate_up+SwiGLU
+           and down on MFMA, fused combine + shared + residual + next RMSNorm.
+Both use the same split-KV absorbed-MLA decode kernel.  Prefill always uses
+the batch family with one row per prompt token.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from triton_kernels import _hip
+from triton_kernels._hip import LINEAR_OUT_F32, LINEAR_SWIGLU, call, ptr
+
+from .cache import CompressedKVCache
+from .config import DSV2Config
+from .rope import cos_sin_tables
+from .weights import ModelWeights
+
+BF16 = torch.bfloat16
+FAMILIES = ("small", "batch")
+
+
+def plan_splits(rows: int, max_ctx: int, target_wgs: int = 1024) -> tuple[int, int]:
+    """(split_tokens, max_splits) for the split-KV decode: about target_wgs workgroups,
+    split_tokens a multiple of 32, at most 64 splits per row."""
+    per_row = max(1, min(64, math.ceil(target_wgs / max(rows, 1))))
+    split = max(32, math.ceil(math.ceil(max_ctx / per_row) / 32) * 32)
+    split = max(split, math.ceil(max_ctx / 64 / 32) * 32)
+    return split, math.ceil(max_ctx / split)
+
+
+def moe_tile_tokens(rows: int, n_experts: int = 64, top_k: int = 6) -> int:
+    avg = rows * top_k / n_experts
+    return 16 if avg <= 6 else (32 if avg <= 16 else 64)
+
+
+class RowBuffers:
+    """Per-row work buffers for `rows` rows of one kernel family."""
+
+    def __init__(self, cfg: DSV2Config, rows: int, family: str, max_ctx: int, device):
+        self.rows = rows
+        self.family = family
+        e = lambda *s, dt=BF16: torch.empty(*s, dtype=dt, device=device)  # noqa: E731
+        H = cfg.hidden
+        self.h = e(rows, H)
+        self.xn = e(rows, H)
+        self.qkva = e(rows, cfg.qkva_dim)
+        self.q = e(rows, cfg.n_heads, cfg.cache_row)
+        self.split_tokens, self.max_splits = plan_splits(rows, max_ctx)
+        self.part_o = e(rows, self.max_splits, cfg.n_heads, cfg.kv_rank, dt=torch.float32)
+        self.part_ml = e(rows, self.max_splits, cfg.n_heads, 2, dt=torch.float32)
+        self.attn = e(rows, H)
+        self.ids32 = e(rows, cfg.top_k, dt=torch.int32)
+        self.wts = e(rows, cfg.top_k, dt=torch.float32)
+        self.mid = e(rows, cfg.dense_inter)
+        if family == "small":
+            self.hbuf = e(rows, cfg.top_k + 2, cfg.moe_inter)
+        else:
+            R = rows * cfg.top_k
+            self.olat = e(rows, cfg.n_heads, cfg.kv_rank)
+            self.tile_tokens = moe_tile_tokens(rows, cfg.n_experts, cfg.top_k)
+            self.max_tiles = math.ceil(R / self.tile_tokens) + cfg.n_experts
+            self.sorted = e(R, dt=torch.int32)
+            self.route_pos = e(R, dt=torch.int32)
+            self.tiles = e(self.max_tiles, 4, dt=torch.int32)
+            self.ntiles = e(1, dt=torch.int32)
+            self.hs = e(R, cfg.moe_inter)
+            self.ys = e(R, H)
+            self.shmid = e(rows, cfg.shared_inter)
+            self.shout = e(rows, H)
+
+
+class DecodeEngine:
+    def __init__(self, weights: ModelWeights, capacities: list[int], family: str = "small",
+                 max_prefill_rows: int = 1024, device="cuda"):
+        if family not in FAMILIES:
+            raise ValueError(f"Unknown kernel family: {family}")
+        cfg = weights.cfg
+        cfg.check_kernel_dims()
+        self.cfg = cfg
+        self.w = weights
+        self.family = family
+        self.device = torch.device(device)
+        self.B = len(capacities)
+        self.cache = CompressedKVCache(cfg.n_layers, capacities, device=device, row=cfg.cache_row)
+        self.max_pos = self.cache.max_capacity
+        self.cos, self.sin = cos_sin_tables(cfg, self.max_pos, device=device)
+        self.scale = cfg.softmax_scale
+        self.ids = torch.zeros(self.B, dtype=torch.int64, device=device)
+        self.logits = torch.empty(self.B, cfg.vocab, dtype=torch.float32, device=device)
+        self.buf = RowBuffers(cfg, self.B, family, self.max_pos, device)
+        self.max_prefill_rows = max_prefill_rows
+        self.graph = None
+        self._host_pos = [0] * self.B  # host mirror of cache.pos, for capacity checks only
+
+    # ------------------------------------------------------------------ layers
+    def _attention(self, L, li: int, b: RowBuffers, R: int, pos, base, family: str, st: int) -> None:
+        c = self.cfg
+        cache = self.cache.layer(li)
+        if family == "small":
+            call("dsv2_gemv_bf16", ptr(b.h), c.hidden, R, c.hidden, ptr(L.w_qkva), c.qkva_dim, ptr(L.ln_in), c.eps,
+                 None, 0, ptr(b.qkva), c.qkva_dim, 0, st)
+            call("dsv2_mla_prepare", ptr(b.qkva), c.qkva_dim, R, ptr(pos), ptr(base), ptr(L.kv_norm), c.eps,
+                 ptr(self.cos), ptr(self.sin), self.max_pos, ptr(L.w_uk), ptr(cache), ptr(b.q), st)
+        else:
+            call("dsv2_gemm_bf16", ptr(b.xn), c.hidden, 0, R, c.hidden, ptr(L.w_qkva), 0, c.qkva_dim, 1, None, 0,
+                 ptr(b.qkva), c.qkva_dim, 0, 0, st)
+            call("dsv2_mla_prepare", ptr(b.qkva), c.qkva_dim, R, ptr(pos), ptr(base), ptr(L.kv_norm), c.eps,
+                 ptr(self.cos), ptr(self.sin), self.max_pos, None, ptr(cache), ptr(b.q), st)
+            # q_lat[r, h, :512] = W_UK_h^T q_nope[r, h]: 16 head groups, K = 128
+            call("dsv2_gemm_bf16", ptr(b.qkva), c.qkva_dim, c.q_head, R, c.qk_nope, ptr(L.w_ukt),
+                 c.kv_rank * c.qk_nope, c.kv_rank, c.n_heads, None, 0, ptr(b.q), c.n_heads * c.cache_row,
+                 c.cache_row, 0, st)
+        call("dsv2_mla_decode", ptr(b.q), ptr(cache), ptr(base), ptr(pos), R, b.split_tokens, b.max_splits,
+             self.scale, ptr(b.part_o), ptr(b.part_ml), st)
+        if family == "small":
+            call("dsv2_mla_combine", ptr(b.part_o), ptr(b.part_ml), ptr(pos), R, b.split_tokens, b.max_splits,
+                 ptr(L.w_uv), ptr(b.attn), c.hidden, st)
+            call("dsv2_gemv_bf16", ptr(b.attn), c.hidden, R, c.hidden, ptr(L.w_o), c.hidden, None, 0.0, ptr(b.h),
+                 c.hidden, ptr(b.h), c.hidden, 0, st)
+        else:
+            call("dsv2_mla_combine", ptr(b.part_o), ptr(b.part_ml), ptr(pos), R, b.split_tokens, b.max_splits,
+                 None, ptr(b.olat), c.n_heads * c.kv_rank, st)
+            # attn[r, h*128 + i] = W_UV_h o_lat[r, h]: 16 head groups, K = 512
+            call("dsv2_gemm_bf16", ptr(b.olat), c.n_heads * c.kv_rank, c.kv_rank, R, c.kv_rank, ptr(L.w_uv),
+                 c.v_dim * c.kv_rank, c.v_dim, c.n_heads, None, 0, ptr(b.attn), c.hidden, c.v_dim, 0, st)
+            call("dsv2_gemm_bf16", ptr(b.attn), c.hidden, 0, R, c.hidden, ptr(L.w_o), 0, c.hidden, 1, ptr(b.h),
+                 c.hidden, ptr(b.h), c.hidden, 0, 0, st)
+
+    def _mlp(self, L, li: int, b: RowBuffers, R: int, family: str, next_norm, st: int) -> None:
+        c = self.cfg
+        H = c.hidden
+        if family == "small":
+            if L.moe:
+                call("dsv2_router_topk6", ptr(b.h), H, ptr(L.ln_post), c.eps, ptr(L.w_router), c.routed_scaling, R,
+                     ptr(b.xn), ptr(b.ids32), None, ptr(b.wts), st)
+                call("dsv2_moe_route_gateup", ptr(b.xn), R, ptr(b.ids32), ptr(L.w_gu), ptr(L.sh_gu), c.moe_inter,
+                     ptr(b.hbuf), st)
+                call("dsv2_moe_route_down", ptr(b.hbuf), R, ptr(b.ids32), ptr(b.wts), ptr(L.w_down), ptr(L.sh_down),
+                     c.moe_inter, ptr(b.h), ptr(b.h), st)
+            else:
+                call("dsv2_gemv_bf16", ptr(b.h), H, R, H, ptr(L.w_gu), c.dense_inter, ptr(L.ln_post), c.eps, None, 0,
+                     ptr(b.mid), c.dense_inter, LINEAR_SWIGLU, st)
+                call("dsv2_gemv_bf16", ptr(b.mid), c.dense_inter, R, c.dense_inter, ptr(L.w_down), H, None, 0.0,
+                     ptr(b.h), H, ptr(b.h), H, 0, st)
+            return
+        if L.moe:
+            call("dsv2_router_topk6", ptr(b.h), H, ptr(L.ln_post), c.eps, ptr(L.w_router), c.routed_scaling, R,
+                 ptr(b.xn), ptr(b.ids32), None, ptr(b.wts), st)
+            call("dsv2_moe_bucket", ptr(b.ids32), R, b.tile_tokens, ptr(b.sorted), ptr(b.route_pos), ptr(b.tiles),
+                 ptr(b.ntiles), st)
+            call("dsv2_moe_grouped_gateup", ptr(b.xn), ptr(b.sorted), ptr(b.tiles), ptr(b.ntiles), b.max_tiles,
+                 b.tile_tokens, ptr(L.w_gu), c.moe_inter, ptr(b.hs), st)
+            call("dsv2_moe_grouped_down", ptr(b.hs), ptr(b.tiles), ptr(b.ntiles), b.max_tiles, b.tile_tokens,
+                 ptr(L.w_down), c.moe_inter, ptr(b.ys), st)
+            call("dsv2_gemm_bf16", ptr(b.xn), H, 0, R, H, ptr(L.sh_gu), 0, c.shared_inter, 1, None, 0, ptr(b.shmid),
+                 c.shared_inter, 0, LINEAR_SWIGLU, st)
+            call("dsv2_gemm_bf16", ptr(b.shmid), c.shared_inter, 0, R, c.shared_inter, ptr(L.sh_down), 0, H, 1,
+                 None, 0, ptr(b.shout), H, 0, 0, st)
+            call("dsv2_moe_combine", ptr(b.ys), ptr(b.route_pos), ptr(b.wts), R, ptr(b.shout), ptr(b.h), ptr(b.h),
+                 ptr(next_norm), c.eps, ptr(b.xn), st)
+        else:
+            call("dsv2_rmsnorm_bf16", ptr(b.h), H, ptr(L.ln_post), ptr(b.xn), H, R, H, c.eps, st)
+            call("dsv2_gemm_bf16", ptr(b.xn), H, 0, R, H, ptr(L.w_gu), 0, c.dense_inter, 1, None, 0, ptr(b.mid),
+                 c.dense_inter, 0, LINEAR_SWIGLU, st)
+            call("dsv2_gemm_bf16", ptr(b.mid), c.dense_inter, 0, R, c.dense_inter, ptr(L.w_down), 0, H, 1, ptr(b.h),
+                 H, ptr(b.h), H, 0, 0, st)
+            call("dsv2_rmsnorm_bf16", ptr(b.h), H, ptr(next_norm), ptr(b.xn), H, R, H, c.eps, st)
+
+    def _layers(self, b: RowBuffers, R: int, ids: torch.Tensor, pos, base, family: str, st: int,
+                record: list | None = None) -> None:
+        c = self.cfg
+        call("dsv2_embed_gather_bf16", ptr(ids), ptr(self.w.embed), c.hidden, ptr(b.h), R, st)
+        if family == "batch":
+            call("dsv2_rmsnorm_bf16", ptr(b.h), c.hidden, ptr(self.w.layers[0].ln_in), ptr(b.xn), c.hidden, R,
+                 c.hidden, c.eps, st)
+        n = len(self.w.layers)
+        for li, L in enumerate(self.w.layers):
+            self._attention(L, li, b, R, pos, base, family, st)
+            if record is not None:
+                record.append(("attn", li, b.h[:R].clone()))
+            next_norm = self.w.layers[li + 1].ln_in if li + 1 < n else self.w.norm
+            self._mlp(L, li, b, R, family, next_norm, st)
+            if record is not None:
+                record.append(("layer", li, b.h[:R].clone()))
+                if L.moe:
+                    record.append(("router", li, b.ids32[:R].clone(), b.wts[:R].clone()))
+
+    def _head(self, b: RowBuffers, family: str, st: int, pos) -> None:
+        c = self.cfg
+        B = self.B
+        if family == "small":
+            call("dsv2_gemv_bf16", ptr(b.h), c.hidden, B, c.hidden, ptr(self.w.lm_head), c.vocab, ptr(self.w.norm),
+                 c.eps, None, 0, ptr(self.logits), c.vocab, LINEAR_OUT_F32, st)
+        else:  # b.xn already holds the final-normed hidden (fused into the last combine)
+            call("dsv2_gemm_bf16", ptr(b.xn), c.hidden, 0, B, c.hidden, ptr(self.w.lm_head), 0, c.vocab, 1, None, 0,
+                 ptr(self.logits), c.vocab, 0, LINEAR_OUT_F32, st)
+        call("dsv2_argmax_f32", ptr(self.logits), B, c.vocab, ptr(self.ids), ptr(pos), st)
+
+    # ------------------------------------------------------------------ public
+    def step(self, record: list | None = None) -> None:
+        """Enqueue one decode step for all rows: reads self.ids, writes self.logits and the
+        next ids into self.ids, advances cache.pos.  No host synchronisation."""
+        if max(p + 1 for p in self._host_pos) > self.max_pos:
+            raise RuntimeError("KV cache capacity exhausted")
+        st = _hip.stream_ptr(self.device)
+        self._layers(self.buf, self.B, self.ids, self.cache.pos, self.cache.base, self.family, st, record)
+        self._head(self.buf, self.family, st, self.cache.pos)
+        self._host_pos = [p + 1 for p in self._host_pos]
+
+    def prefill(self, prompts: list[torch.Tensor], record: list | None = None) -> torch.Tensor:
+        """Eager prefill of one prompt per row (batch-family kernels, one kernel row per
+        prompt token, chunks of <= max_prefill_rows rows in sequence order).  Writes the
+        compressed cache, sets cache.pos = prompt lengths and self.ids = greedy first
+        tokens (returned).  Mirrors _prefill_once (src/run.py:526-544)."""
+        if len(prompts) != self.B:
+            raise ValueError(f"need {self.B} prompts, got {len(prompts)}")
+        lens = [int(p.numel()) for p in prompts]
+        if min(lens) < 1:
+            raise ValueError("empty prompt")
+        for b, n in enumerate(lens):
+            if n >= self.cache.capacities[b]:
+                raise ValueError(f"prompt {b} of length {n} does not fit capacity {self.cache.capacities[b]}")
+        dev = self.device
+        seq = torch.cat([torch.full((n,), b, dtype=torch.int64) for b, n in enumerate(lens)])
+        posv = torch.cat([torch.arange(n, dtype=torch.int32) for n in lens])
+        ids_all = torch.cat([p.reshape(-1).to(torch.int64).cpu() for p in prompts])
+        base_all = self.cache.base.cpu()[seq]
+        total = seq.numel()
+        max_rows = min(self.max_prefill_rows, total)
+        pb = RowBuffers(self.cfg, max_rows, "batch", self.max_pos, dev)
+        last_h = torch.empty(self.B, self.cfg.hidden, dtype=BF16, device=dev)
+        last_xn = torch.empty_like(last_h)
+        st = _hip.stream_ptr(dev)
+        for s in range(0, total, max_rows):
+            e = min(total, s + max_rows)
+            R = e - s
+            ids_c = ids_all[s:e].to(dev)
+            pos_c = posv[s:e].to(dev)
+            base_c = base_all[s:e].to(dev)
+            self._layers(pb, R, ids_c, pos_c, base_c, "batch", st, record)
+            is_last = (posv[s:e] + 1) == torch.tensor(lens)[seq[s:e]]
+            rows = torch.nonzero(is_last).flatten()
+            if rows.numel():
+                which = seq[s:e][rows].to(dev)
+                last_h.index_copy_(0, which, pb.h[rows.to(dev)])
+                last_xn.index_copy_(0, which, pb.xn[rows.to(dev)])
+        # final norm is fused into the last layer's combine (pb.xn); lm_head + argmax
+        c = self.cfg
+        call("dsv2_gemm_bf16", ptr(last_xn), c.hidden, 0, self.B, c.hidden, ptr(self.w.lm_head), 0, c.vocab, 1, None,
+             0, ptr(self.logits), c.vocab, 0, LINEAR_OUT_F32, st)
+        call("dsv2_argmax_f32", ptr(self.logits), self.B, c.vocab, ptr(self.ids), None, st)
+        self.cache.pos.copy_(torch.tensor(lens, dtype=torch.int32))
+        self._host_pos = list(lens)
+        self.buf.h.copy_(last_h)
+        del pb
+        return self.ids
+
+    def snapshot(self) -> tuple[torch.Tensor, torch.Tensor, list[int]]:
+        return self.cache.snapshot(), self.ids.clone(), list(self._host_pos)
+
+    def restore(self, snap) -> None:
+        pos, ids, host = snap
+        self.cache.restore(pos)
+        self.ids.copy_(ids)
+        self._host_pos = list(host)
+
+    def capture(self) -> torch.cuda.CUDAGraph:
+        """Record one step() into a graph (positions/ids advance on every replay)."""
+        saved = list(self._host_pos)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.step()
+        self._host_pos = saved
+        self.graph = g
+        return g
+
+    def replay(self) -> None:
+        if self.graph is None:
+            raise RuntimeError("capture() first")
+        if max(p + 1 for p in self._host_pos) > self.max_pos:
+            raise RuntimeError("KV cache capacity exhausted")
+        self.graph.replay()
+        self._host_pos = [p + 1 for p in self._host_pos]

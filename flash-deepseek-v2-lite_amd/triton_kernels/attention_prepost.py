@@ -1,0 +1,74 @@
+"""Decode input preparation, cache write, residual add
+(reference: triton_kernels/attention_prepost.py:113-223)."""
+
+from __future__ import annotations
+
+import torch
+
+from . import _hip
+from ._checks import require_contiguous, require_cuda
+
+
+def copy_single_token_to_cache(src: torch.Tensor, dst: torch.Tensor, cache_position: torch.Tensor) -> None:
+    """dst[b, pos] = src[b] for each row b, pos = cache_position[0] (device scalar).
+
+    Accepts the reference's expanded layout ([B, H, 1, D] -> [B, H, S, D], per-head
+    rows) and the compressed-cache layout ([B, 1, D] -> [B, S, D])."""
+    require_cuda("copy_single_token_to_cache", src, dst, cache_position)
+    if src.dtype != dst.dtype:
+        raise ValueError("src and dst dtype must match")
+    if cache_position.numel() != 1:
+        raise ValueError("cache_position must be a CUDA tensor with one element")
+    require_contiguous("copy_single_token_to_cache", src, dst)
+    if src.ndim == 4 and dst.ndim == 4 and src.shape[2] == 1 and src.shape[:2] == dst.shape[:2] \
+            and src.shape[3] == dst.shape[3]:
+        rows = src.shape[0] * src.shape[1]
+        row_bytes = src.shape[3] * src.element_size()
+        src_bs, dst_bs = row_bytes, dst.shape[2] * row_bytes
+    elif src.ndim == 3 and dst.ndim == 3 and src.shape[1] == 1 and src.shape[0] == dst.shape[0] \
+            and src.shape[2] == dst.shape[2]:
+        rows = src.shape[0]
+        row_bytes = src.shape[2] * src.element_size()
+        src_bs, dst_bs = row_bytes, dst.shape[1] * row_bytes
+    else:
+        raise NotImplementedError("copy_single_token_to_cache supports [B,H,1,D]->[B,H,S,D] or [B,1,D]->[B,S,D]")
+    if row_bytes % 16:
+        raise ValueError("row size must be a multiple of 16 bytes")
+    pos = cache_position.reshape(1).to(torch.int64)
+    _hip.call("dsv2_copy_token_rows", src.data_ptr(), src_bs, dst.data_ptr(), dst_bs, row_bytes, pos.data_ptr(),
+              rows, _hip.stream_ptr(src.device))
+
+
+def prepare_decode_inputs_triton(cache_position: torch.Tensor, attention_mask: torch.Tensor,
+                                 position_ids: torch.Tensor, attention_mask_index: torch.Tensor) -> None:
+    """mask[b, j] = (j <= pos); position_ids[b] = pos (int64, in place)."""
+    require_cuda("prepare_decode_inputs_triton", cache_position, attention_mask, position_ids)
+    if cache_position.numel() != 1:
+        raise ValueError("cache_position must have one element")
+    if attention_mask.ndim != 2:
+        raise ValueError("attention_mask must have shape [batch, max_cache_len]")
+    if position_ids.ndim != 2 or position_ids.shape[0] != attention_mask.shape[0] or position_ids.shape[1] != 1:
+        raise ValueError("position_ids must have shape [batch, 1]")
+    if attention_mask_index.ndim != 1 or attention_mask_index.shape[0] != attention_mask.shape[1]:
+        raise ValueError("attention_mask_index must be 1D with length max_cache_len")
+    if attention_mask.dtype != torch.long or position_ids.dtype != torch.long or cache_position.dtype != torch.long:
+        raise ValueError("prepare_decode_inputs_triton requires int64 tensors")
+    require_contiguous("prepare_decode_inputs_triton", attention_mask, position_ids)
+    _hip.call("dsv2_prepare_decode_inputs", cache_position.data_ptr(), attention_mask.data_ptr(),
+              position_ids.data_ptr(), attention_mask.shape[0], attention_mask.shape[1],
+              _hip.stream_ptr(attention_mask.device))
+
+
+def residual_add_triton(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    require_cuda("residual_add_triton", a, b)
+    if a.shape != b.shape:
+        raise ValueError("a and b must have the same shape")
+    if a.dtype != torch.bfloat16 or b.dtype != a.dtype:
+        raise NotImplementedError("residual_add_triton supports bf16 with same dtype")
+    require_contiguous("residual_add_triton", a, b)
+    if a.numel() % 8:
+        raise ValueError("residual_add_triton needs numel % 8 == 0")
+    out = torch.empty_like(a)
+    _hip.call("dsv2_residual_add_bf16", a.data_ptr(), b.data_ptr(), out.data_ptr(), a.numel(),
+              _hip.stream_ptr(a.device))
+    return out

@@ -1,0 +1,211 @@
+/*
+ * dsv2lite.h -- C ABI of the MI355X (gfx950) DeepSeek-V2-Lite decode-step library
+ * (libdsv2lite_hip.so).
+ *
+ * Conventions (every entry point):
+ *   - device pointers are plain `void*` / typed pointers to HBM buffers owned by
+ *     the caller; bf16 tensors are passed as `void*` (2 bytes per element);
+ *   - `stream` is a hipStream_t passed as `void*` (the caller's current stream);
+ *   - no entry point allocates, synchronises or reads device memory on the host,
+ *     so every one of them may be recorded into a hipGraph;
+ *   - return 0 on success, a negative DSV2_E* code for a rejected argument, or a
+ *     positive hipError_t from the launch.  dsv2_last_error_message() gives the
+ *     text of the last failure on the calling thread.
+ *
+ * The reference (heiheiha798/Flash-DeepSeeek-V2-Lite) has no native FFI: its
+ * operator boundary is the Python `triton_kernels` package patched into the HF
+ * model by src/run.py:256-502.  Each entry point below cites the Python
+ * function (file:line in that repository) whose role it takes.
+ */
+#ifndef DSV2LITE_H_
+#define DSV2LITE_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DSV2_ABI_VERSION 1
+
+#define DSV2_OK 0
+#define DSV2_E_NULL (-1)      /* a required pointer is null            */
+#define DSV2_E_SHAPE (-2)     /* a size is out of the supported range  */
+#define DSV2_E_ALIGN (-3)     /* a pointer/stride is not 16B-aligned   */
+#define DSV2_E_FLAGS (-4)     /* unsupported flag combination          */
+
+/* flags of dsv2_gemv_bf16 / dsv2_gemm_bf16 */
+#define DSV2_LINEAR_SWIGLU 1  /* W holds [gate; up] (2N rows): y = bf16(silu(bf16 g)) * bf16 u */
+#define DSV2_LINEAR_OUT_F32 2 /* store fp32(bf16(acc)) instead of bf16 (logits)               */
+
+int dsv2_abi_version(void);
+const char* dsv2_last_error_message(void);
+
+/* ---- elementwise -------------------------------------------------------- */
+
+/* y[r,:] = w * bf16(x[r,:] * rsqrt(mean(x^2) + eps)), fp32 math, bf16 out.
+ * Replaces rmsnorm_triton (triton_kernels/rmsnorm.py:60-95). cols % 8 == 0, cols <= 8192. */
+int dsv2_rmsnorm_bf16(const void* x, int64_t x_stride, const void* w, void* y, int64_t y_stride,
+                      int rows, int cols, float eps, void* stream);
+
+/* out = bf16(fp32(a) + fp32(b)).  Replaces residual_add_triton
+ * (triton_kernels/attention_prepost.py:191-223).  n % 8 == 0. */
+int dsv2_residual_add_bf16(const void* a, const void* b, void* out, int64_t n, void* stream);
+
+/* out = bf16(g * sigmoid(g) * u) in fp32.  Replaces silu_mul_triton
+ * (triton_kernels/mlp_elementwise.py:24-45).  n % 8 == 0. */
+int dsv2_silu_mul_bf16(const void* gate, const void* up, void* out, int64_t n, void* stream);
+
+/* mask[b,j] = (j <= pos), position_ids[b] = pos with pos = cache_position[0], int64.
+ * Replaces prepare_decode_inputs_triton (triton_kernels/attention_prepost.py:152-188). */
+int dsv2_prepare_decode_inputs(const int64_t* cache_position, int64_t* attention_mask,
+                               int64_t* position_ids, int batch, int max_len, void* stream);
+
+/* dst[b, pos, :] = src[b, :] for b < batch, pos = cache_position[0]; row_bytes % 16 == 0.
+ * dst row b starts at dst + b*dst_batch_stride bytes, token rows are row_bytes apart.
+ * Replaces copy_single_token_to_cache (triton_kernels/attention_prepost.py:113-149). */
+int dsv2_copy_token_rows(const void* src, int64_t src_batch_stride, void* dst, int64_t dst_batch_stride,
+                         int64_t row_bytes, const int64_t* cache_position, int batch, void* stream);
+
+/* pos32[b] = cache_position[0]; base[b] = b * per_row_capacity (int64).  Turns the
+ * reference's shared scalar cache_position (src/run.py:196-202) into per-row arrays. */
+int dsv2_fill_positions(const int64_t* cache_position, int32_t* pos, int64_t* base,
+                        int64_t per_row_capacity, int batch, void* stream);
+
+/* out[r,:] = table[ids[r], :] (bf16 rows of `hidden`).  The embed_tokens gather of the
+ * HF model (run.py:577-584 feeds input_ids into the model). */
+int dsv2_embed_gather_bf16(const int64_t* ids, const void* table, int hidden, void* out, int rows,
+                           void* stream);
+
+/* next_ids[r] = first index of the max of logits[r, :vocab] (fp32); if pos != NULL,
+ * pos[r] += 1.  Replaces _greedy_decode + cache_position.add_(1) (src/run.py:252-253,585-588). */
+int dsv2_argmax_f32(const float* logits, int rows, int vocab, int64_t* next_ids, int32_t* pos,
+                    void* stream);
+
+/* ---- linears -------------------------------------------------------------- */
+
+/* y[r, n] = bf16( x'[r,:] . W[n,:] ) for r < rows, n < N, fp32 accumulation, where
+ * x' = x, or RMSNorm(x; norm_w, eps) when norm_w != NULL (fused prologue).  With
+ * residual != NULL: y = bf16(residual + bf16(acc)).  flags: DSV2_LINEAR_*.
+ * VALU GEMV for few rows (weights streamed once per 8 rows).  K % 8 == 0, N % 8 == 0.
+ * Replaces the small-family GEMVs (attention_decode_small.py:55-137, :858-929) and the
+ * torch F.linear calls of the dense / shared MLP and lm_head (src/run.py:341-352). */
+int dsv2_gemv_bf16(const void* x, int64_t x_stride, int rows, int K, const void* W, int N,
+                   const void* norm_w, float eps, const void* residual, int64_t res_stride, void* y,
+                   int64_t y_stride, int flags, void* stream);
+
+/* Grouped bf16 MFMA GEMM (v_mfma_f32_16x16x32_bf16), fp32 accumulation:
+ *   for group g < n_groups, row r < rows:
+ *     Y[g*y_gstride + r*y_stride + n] = x[g*x_gstride + r*x_stride, :] . W[g*w_gstride + n*K, :]
+ * Same flags/residual semantics as dsv2_gemv_bf16 (residual only with n_groups == 1).
+ * K % 32 == 0, N % 64 == 0.  Replaces _batched_linear_kernel
+ * (triton_kernels/attention_decode_batch.py:421-468) and cuBLAS F.linear at batch sizes. */
+int dsv2_gemm_bf16(const void* x, int64_t x_stride, int64_t x_gstride, int rows, int K, const void* W,
+                   int64_t w_gstride, int N, int n_groups, const void* residual, int64_t res_stride, void* y,
+                   int64_t y_stride, int64_t y_gstride, int flags, void* stream);
+
+/* ---- absorbed MLA -------------------------------------------------------- */
+
+/* Per row r (new token at cache slot base[r] + pos[r]):
+ *   c = RMSNorm(qkva[r, 3072:3584]; kv_norm_w) -> cache[slot, 0:512]
+ *   k_pe = RoPE(qkva[r, 3584:3648], pos)      -> cache[slot, 512:576]
+ *   q_out[r, h, 512:576] = RoPE(q_pe_h);  q_out[r, h, 0:512] = W_UK_h^T q_nope_h
+ *     (only when w_uk != NULL; the batch family runs the absorption as a grouped GEMM).
+ * RoPE rotates de-interleaved pairs with bf16 cos/sin tables [max_pos, 64].
+ * Replaces kv-norm + _batched_build_qkv_rope_kernel + _cache_write_q1_dual_kernel
+ * (attention_decode_batch.py:719-813; attention_decode_small.py:141-339). */
+int dsv2_mla_prepare(const void* qkva, int64_t qkva_stride, int rows, const int32_t* pos,
+                     const int64_t* base, const void* kv_norm_w, float eps, const void* rope_cos,
+                     const void* rope_sin, int max_pos, const void* w_uk, void* cache, void* q_out,
+                     void* stream);
+
+/* Split-KV absorbed-MLA decode over the compressed cache [*, 576] bf16.
+ * Row r attends cache rows base[r] .. base[r]+pos[r] (inclusive); split s covers
+ * tokens [s*split_tokens, (s+1)*split_tokens).  Writes unnormalised partial
+ * o_lat [rows, max_splits, 16, 512] fp32 and (m, l) [rows, max_splits, 16, 2]
+ * (m in log2 units).  split_tokens % 32 == 0.  Replaces _batched_decode_attention_q1_kernel
+ * (attention_decode_batch.py:241-342) / _decode_attention_q1_kernel (attention_decode_small.py:343-423). */
+int dsv2_mla_decode(const void* q, const void* cache, const int64_t* base, const int32_t* pos, int rows,
+                    int split_tokens, int max_splits, float softmax_scale, float* part_o, float* part_ml,
+                    void* stream);
+
+/* Merge the splits of dsv2_mla_decode.  With w_uv != NULL: out[r, h*128 + i] =
+ * bf16(sum_j W_UV[h, i, j] o_lat[r, h, j]) (bf16 [rows, 2048], row stride out_stride);
+ * with w_uv == NULL: out = bf16 o_lat [rows, 16, 512] for a grouped GEMM.
+ * Together with dsv2_mla_decode this replaces the attention core + v-combine
+ * (attention_decode_batch.py:240-401). */
+int dsv2_mla_combine(const float* part_o, const float* part_ml, const int32_t* pos, int rows,
+                     int split_tokens, int max_splits, const void* w_uv, void* out, int64_t out_stride,
+                     void* stream);
+
+/* ---- MoE ------------------------------------------------------------------ */
+
+/* Router: xn = RMSNorm(h; norm_w) (written to xn_out), logits = fp32(xn) . fp32(W_r)^T
+ * [64], softmax, top-6 by repeated max (ties -> lower index), weights = score * scaling.
+ * ids as int32 (ids32) and/or int64 (ids64).  Replaces _graph_gate_forward + the router
+ * kernel (src/run.py:257-275; triton_kernels/moe_router.py:9-86). */
+int dsv2_router_topk6(const void* h, int64_t h_stride, const void* norm_w, float eps, const void* w_router,
+                      float scaling, int rows, void* xn_out, int32_t* ids32, int64_t* ids64, float* weights,
+                      void* stream);
+
+/* Softmax + top-6 from given fp32 logits [rows, 64]: router_softmax_topk6_triton
+ * (triton_kernels/moe_router.py:63-86). */
+int dsv2_router_topk6_from_logits(const float* logits, int rows, float scaling, int32_t* ids32,
+                                  int64_t* ids64, float* weights, void* stream);
+
+/* Small family, route-local gate_up + SwiGLU: for row r, route s < n_routes:
+ *   hbuf[r, s, :inter] = bf16(silu(bf16 g)) * bf16 u  with expert e = ids[r, s] (s < 6) or
+ *   the shared expert half s-6 (s = 6, 7 when sh_gate_up != NULL: rows [(s-6)*inter, ...)
+ *   of gate and of up).  w_gate_up [64, 2*inter, 2048]; sh_gate_up [2*2*inter, 2048].
+ * Replaces _fused_gate_up_swiglu_kernel / _batched_fused_gate_up_swiglu_kernel
+ * (triton_kernels/moe_small_gemv.py:53-105, :195-253) with the gate/up rows paired correctly. */
+int dsv2_moe_route_gateup(const void* xn, int rows, const int32_t* ids, const void* w_gate_up,
+                          const void* sh_gate_up, int inter, void* hbuf, void* stream);
+
+/* Small family, route-local down + top-6 combine (+ shared, + residual):
+ *   d_s = bf16(hbuf[r,s,:] . Wd_s[j,:]);  routed = bf16(sum_{s<6} w[r,s] d_s)  (fp32, slot order)
+ *   shared = bf16(d_6 + d_7) (when sh_down != NULL);  y = bf16(routed + shared)
+ *   out[r, j] = residual ? bf16(residual[r, j] + y) : y.
+ * w_down [64, 2048, inter]; sh_down [2048, 2*inter].  Replaces _down_partial_kernel +
+ * _down_reduce_topk6_kernel (moe_small_gemv.py:109-191, :257-347). */
+int dsv2_moe_route_down(const void* hbuf, int rows, const int32_t* ids, const float* weights,
+                        const void* w_down, const void* sh_down, int inter, const void* residual, void* out,
+                        void* stream);
+
+/* Batch family bucketing (one workgroup, deterministic counting sort by expert):
+ *   sorted_routes[p] = route index r*6+s in expert order, stable in r;
+ *   route_pos[r*6+s] = p;  tiles[t] = {expert, first slot, count<=tile_tokens, 0} (int32x4);
+ *   num_tiles[0] = number of tiles (<= rows*6/tile_tokens + 64).  rows*6 <= 8192.
+ * Replaces _build_route_indices_kernel + _build_route_blocks_kernel (moe_batch.py:95-148). */
+int dsv2_moe_bucket(const int32_t* ids, int rows, int tile_tokens, int32_t* sorted_routes, int32_t* route_pos,
+                    int32_t* tiles, int32_t* num_tiles, void* stream);
+
+/* Expert-grouped gate_up + SwiGLU on bf16 MFMA over the tiles of dsv2_moe_bucket:
+ *   hsorted[p, :inter] for p in tile = SwiGLU(xn[sorted_routes[p]/6] . W_e^T).
+ * Grid is sized by max_tiles; tiles >= num_tiles[0] exit.  Replaces
+ * _grouped_gate_up_swiglu_kernel (moe_batch.py:152-234). */
+int dsv2_moe_grouped_gateup(const void* xn, const int32_t* sorted_routes, const int32_t* tiles,
+                            const int32_t* num_tiles, int max_tiles, int tile_tokens, const void* w_gate_up,
+                            int inter, void* hsorted, void* stream);
+
+/* Expert-grouped down projection: ysorted[p, :] = bf16(hsorted[p, :] . Wd_e^T).
+ * Replaces _grouped_down_partial_kernel (moe_batch.py:238-307) with a bf16 result
+ * (the expert output's own rounding point) instead of an fp32 partial. */
+int dsv2_moe_grouped_down(const void* hsorted, const int32_t* tiles, const int32_t* num_tiles, int max_tiles,
+                          int tile_tokens, const void* w_down, int inter, void* ysorted, void* stream);
+
+/* Combine: routed = bf16(sum_s w[r,s] ysorted[route_pos[r*6+s]]) (fp32, slot order);
+ * y = shared ? bf16(routed + shared[r]) : routed;  out[r] = residual ? bf16(residual[r] + y) : y.
+ * If next_norm_w != NULL also xn_out[r] = RMSNorm(out[r]; next_norm_w).
+ * Replaces _batched_down_reduce_topk6_kernel (moe_batch.py:56-92) + the shared add and
+ * residual add of the MoE layer (src/run.py:486). */
+int dsv2_moe_combine(const void* ysorted, const int32_t* route_pos, const float* weights, int rows,
+                     const void* shared, const void* residual, void* out, const void* next_norm_w, float eps,
+                     void* xn_out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSV2LITE_H_ */

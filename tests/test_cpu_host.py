@@ -1,0 +1,125 @@
+"""Host-side checks that run without a GPU: the C-ABI library loads and exports every
+symbol the header declares, wrappers reject what the reference rejects, and the
+product's host math (RoPE tables, softmax scale, split planning, cache layout)
+matches the oracle."""
+
+from __future__ import annotations
+
+import math
+import os
+import re
+
+import pytest
+import torch
+
+import oracle.dsv2_oracle as O
+from golden_utils import ROOT
+
+
+def _header_symbols():
+    txt = open(os.path.join(ROOT, "include", "dsv2lite.h")).read()
+    return sorted(set(re.findall(r"\b(dsv2_[a-z0-9_]+)\s*\(", txt)))
+
+
+def test_library_exports_every_header_symbol():
+    from triton_kernels import _hip
+
+    syms = _header_symbols()
+    assert len(syms) >= 20
+    for s in syms:
+        assert hasattr(_hip.lib, s), s
+    assert sorted(_hip.EXPORTS) == syms
+    assert _hip.lib.dsv2_abi_version() == _hip.ABI_VERSION
+
+
+def test_abi_rejects_bad_arguments_without_launching():
+    from triton_kernels import _hip
+
+    with pytest.raises(_hip.HipKernelError, match="null pointer"):
+        _hip.call("dsv2_rmsnorm_bf16", None, 0, None, None, 0, 1, 2048, 1e-6, None)
+    with pytest.raises(_hip.HipKernelError, match="bad shape"):
+        _hip.call("dsv2_gemv_bf16", 16, 2048, 1, 2047, 16, 64, None, 0.0, None, 0, 16, 64, 0, None)
+    with pytest.raises(_hip.HipKernelError, match="max_splits"):
+        _hip.call("dsv2_mla_decode", 16, 16, 16, 16, 1, 32, 65, 0.1, 16, 16, None)
+    with pytest.raises(_hip.HipKernelError, match="rows\\*6"):
+        _hip.call("dsv2_moe_bucket", 16, 2000, 32, 16, 16, 16, 16, None)
+
+
+def test_wrappers_reject_cpu_tensors_like_the_reference():
+    from triton_kernels.attention_prepost import residual_add_triton
+    from triton_kernels.mlp_elementwise import silu_mul_triton
+    from triton_kernels.moe_router import router_softmax_topk6_triton
+    from triton_kernels.rmsnorm import rmsnorm_triton
+
+    x = torch.zeros(2, 2048, dtype=torch.bfloat16)
+    with pytest.raises(NotImplementedError):
+        rmsnorm_triton(x, torch.ones(2048, dtype=torch.bfloat16), 1e-6)
+    with pytest.raises(NotImplementedError):
+        residual_add_triton(x, x)
+    with pytest.raises(NotImplementedError):
+        silu_mul_triton(x, x)
+    with pytest.raises(NotImplementedError):
+        router_softmax_topk6_triton(torch.zeros(1, 64), 1.0)
+
+
+def test_product_rope_and_scale_match_oracle():
+    from dsv2lite.config import DSV2Config
+    from dsv2lite.rope import cos_sin_tables, inv_freq
+
+    cfg = DSV2Config()
+    d = O.Dims()
+    assert torch.equal(inv_freq(cfg), O.yarn_inv_freq(d))
+    cos, sin = cos_sin_tables(cfg, 3000)
+    ocos, osin = O.yarn_cos_sin(d, 3000, mode="bf16")
+    assert torch.equal(cos.float(), ocos) and torch.equal(sin.float(), osin)
+    assert abs(cfg.softmax_scale - O.softmax_scale(d)) < 1e-12
+    assert cfg.qkva_dim == 3648 and cfg.cache_row == 576
+
+
+@pytest.mark.parametrize("rows,ctx", [(1, 10), (1, 236), (64, 1130), (256, 2160), (128, 8200), (1024, 2176),
+                                      (3, 100000)])
+def test_plan_splits(rows, ctx):
+    from dsv2lite.engine import plan_splits
+
+    split, ns = plan_splits(rows, ctx)
+    assert split % 32 == 0 and 1 <= ns <= 64
+    assert split * ns >= ctx and split * (ns - 1) < ctx
+
+
+def test_moe_tile_choice_and_cache_layout():
+    from dsv2lite.cache import CompressedKVCache
+    from dsv2lite.engine import moe_tile_tokens
+
+    assert moe_tile_tokens(1) == 16 and moe_tile_tokens(64) == 16 and moe_tile_tokens(256) == 64
+    c = CompressedKVCache(2, [5, 7, 3], device="cpu")
+    assert c.base.tolist() == [0, 5, 12] and c.total == 15 and c.data.shape == (2, 15, 576)
+    c.pos.copy_(torch.tensor([1, 2, 3], dtype=torch.int32))
+    snap = c.snapshot()
+    c.pos.add_(4)
+    c.restore(snap)
+    assert c.pos.tolist() == [1, 2, 3]
+
+
+def test_engine_rejects_unknown_family_and_dims():
+    from dsv2lite.config import DSV2Config
+    from dsv2lite.engine import DecodeEngine
+
+    with pytest.raises(ValueError, match="Unknown kernel family"):
+        DecodeEngine(None, [8], family="tiny")
+    with pytest.raises(ValueError, match="specialised"):
+        DSV2Config(hidden=1024).check_kernel_dims()
+
+
+def test_weights_hf_views_roundtrip_cpu():
+    from dsv2lite.config import DSV2Config
+    from dsv2lite.weights import init_weights, pack_hf_layer
+
+    cfg = DSV2Config(n_layers=1, vocab=128, dense_inter=128)
+    w = init_weights(cfg, device="cpu", seed=0)
+    hf = w.hf_layer(0)
+    assert hf["q_proj"].shape == (3072, 2048) and hf["kv_b_proj"].shape == (4096, 512)
+    L = pack_hf_layer(cfg, hf, device="cpu")
+    assert torch.equal(L.w_qkva, w.layers[0].w_qkva) and torch.equal(L.w_uk, w.layers[0].w_uk)
+    assert torch.equal(L.w_ukt, w.layers[0].w_uk.transpose(1, 2))
+    std = float(w.layers[0].w_qkva.float().std())
+    assert abs(std - 0.02) < 1e-3
