@@ -1,0 +1,244 @@
+"""Decode-throughput benchmark of the HIP DeepSeek-V2-Lite decode step on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1|2|3] [--no-cpu-baseline]
+
+Default workload: full 27-layer random-init DeepSeek-V2-Lite
+bf16 (N(0,0.02), seed 0), bsz=1, a 128-token prompt of uniform random ids (seed
+1), eager prefill, then K greedy decode steps with the small kernel family, the
+whole step replayed as one hipGraph.  Prints ONE JSON line.
+
+Extra fields:
+  roofline      -- dominant kernel of the step: algorithmic bytes per launch /
+                   average launch time (HIP events around a graph of repeated
+                   launches on the engine's stream) vs 8 TB/s.
+  step_roofline -- algorithmic bytes per step (weights of the experts actually hit,
+                   counted from the router output, + compressed KV read) / step time.
+  cpu_baseline  -- the CPU oracle (PyTorch eager restatement of the HF math) timed on
+                   this host on BASELINE config 0 (one MoE layer: prefill 256 + 32
+                   decode steps) and scaled to whole-model tokens/s.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "flash-deepseek-v2-lite_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import torch  # noqa: E402
+
+HBM_PEAK = 8.0e12
+METRIC = "decode tokens/s at bsz=1/64/256 (1 GPU) + % of HBM roofline per step"
+
+CONFIGS = {
+    1: dict(batch=1, family="small", prompt=lambda g: [128], seed=1,
+            workload="C1: full 27-layer DeepSeek-V2-Lite, bsz=1, 128-token random prompt, small family, hipGraph"),
+    2: dict(batch=64, family="batch", prompt=lambda g: torch.randint(256, 1025, (64,), generator=g).tolist(), seed=2,
+            workload="C2: bsz=64, prompt lengths U[256,1024], batch family, hipGraph"),
+    3: dict(batch=256, family="batch", prompt=lambda g: [2048] * 256, seed=2,
+            workload="C3: bsz=256, prompt 2048, batch family, hipGraph"),
+}
+
+
+def step_bytes(cfg, n_exp_per_layer: list[int], ctx_sum_per_layer: float, batch: int) -> float:
+    """Algorithmic HBM bytes of one decode step (BASELINE.md section 2 byte model)."""
+    attn_w = 2048 * 3648 + 512 * 4096 + 2048 * 2048  # 13,762,560 elements per layer
+    expert = 3 * 2048 * 1408  # 8,650,752
+    shared = 3 * 2048 * 2816  # 17,301,504
+    dense = 3 * 2048 * 10944  # 67,239,936
+    head = 102400 * 2048
+    elems = cfg.n_layers * attn_w + cfg.n_layers * 4608 + sum(n * expert + shared for n in n_exp_per_layer) \
+        + dense + head + 2048
+    return 2 * elems + 26 * 64 * 2048 * 2 + 4096 * batch + 1152 * ctx_sum_per_layer * cfg.n_layers
+
+
+def time_dominant_kernel(eng, family: str, reps: int = 4) -> dict:
+    """Average duration of the step's dominant kernel: a graph with one launch per MoE layer
+    (each on that layer's own weights, so the 26-layer working set streams from HBM rather
+    than the 256 MB Infinity Cache), replayed `reps` times between HIP events on the
+    current stream, with the step's own activations and routing."""
+    from triton_kernels._hip import call, ptr, stream_ptr
+
+    c, b = eng.cfg, eng.buf
+    moe_layers = [L for L in eng.w.layers if L.moe]
+    B = eng.B
+    if family == "small":
+        name = "route_gateup_kernel (small-family MoE gate_up+SwiGLU, 6 routed + 2 shared halves)"
+        bytes_per = B * 8 * 2 * c.moe_inter * c.hidden * 2 + B * 8 * c.moe_inter * 2
+
+        def launch(L):
+            call("dsv2_moe_route_gateup", ptr(b.xn), B, ptr(b.ids32), ptr(L.w_gu), ptr(L.sh_gu), c.moe_inter,
+                 ptr(b.hbuf), stream_ptr())
+    else:
+        name = "gemm_kernel<swiglu> via dsv2_moe_grouped_gateup (expert-grouped gate_up+SwiGLU on MFMA)"
+        n_exp = int(torch.unique(b.ids32[:B]).numel())
+        bytes_per = n_exp * 2 * c.moe_inter * c.hidden * 2 + B * 6 * c.moe_inter * 2
+
+        def launch(L):
+            call("dsv2_moe_grouped_gateup", ptr(b.xn), ptr(b.sorted), ptr(b.tiles), ptr(b.ntiles), b.max_tiles,
+                 b.tile_tokens, ptr(L.w_gu), c.moe_inter, ptr(b.hs), stream_ptr())
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        launch(moe_layers[0])
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for L in moe_layers:
+            launch(L)
+    n_launch = len(moe_layers)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    avg_s = e0.elapsed_time(e1) / 1e3 / (n_launch * reps)
+    ach = bytes_per / avg_s
+    return {"kernel": name, "bound": "hbm", "achieved": ach / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+            "frac": ach / HBM_PEAK, "traffic": None, "bytes_per_launch": bytes_per, "avg_us": avg_s * 1e6}
+
+
+def cpu_baseline(max_seconds: float = 30.0) -> dict:
+    """Oracle (PyTorch eager, HF math) on the host cores, BASELINE config 0."""
+    from oracle import dsv2_oracle as O
+
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    d = O.Dims(n_layers=2)
+    w = O.init_weights_cpu(d, n_layers=2, seed=0, with_head=False)
+    g = torch.Generator().manual_seed(0)
+    m = O.OracleModel(d, w, mode="bf16", max_pos=512)
+    moe_w = w["layers"][1]
+    cos, sin = m.cos, m.sin
+    rb = m.rb
+    cache = O.SeqCache()
+    h = torch.randn(256, d.hidden, generator=g).to(torch.bfloat16).float()
+    t0 = time.perf_counter()
+    O.layer_forward(moe_w, d, 1, h, cache, torch.arange(256), cos, sin, rb)
+    t_prefill = time.perf_counter() - t0
+    steps, t_dec = 0, 0.0
+    x = torch.randn(1, d.hidden, generator=g).to(torch.bfloat16).float()
+    for i in range(32):
+        t0 = time.perf_counter()
+        x = O.layer_forward(moe_w, d, 1, x, cache, torch.tensor([256 + i]), cos, sin, rb)
+        t_dec += time.perf_counter() - t0
+        steps += 1
+        if t_dec > max_seconds:
+            break
+    t_moe = t_dec / steps
+    # the dense layer 0 and the lm_head, once each (same oracle), to scale to the whole model
+    dense_w = w["layers"][0]
+    c0 = O.SeqCache()
+    O.layer_forward(dense_w, d, 0, h[:8], c0, torch.arange(8), cos, sin, rb)
+    t0 = time.perf_counter()
+    O.layer_forward(dense_w, d, 0, x, c0, torch.tensor([8]), cos, sin, rb)
+    t_dense = time.perf_counter() - t0
+    head = (torch.randn(d.vocab, d.hidden, generator=g) * 0.02).to(torch.bfloat16).float()
+    t0 = time.perf_counter()
+    _ = O.linear(O.rmsnorm(x, torch.ones(d.hidden), d.eps, rb), head, rb).argmax()
+    t_head = time.perf_counter() - t0
+    t_tok = 26 * t_moe + t_dense + t_head
+    return {"value": 1.0 / t_tok, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": (f"config 0: one MoE layer, prefill 256 ({t_prefill:.2f}s) + {steps} decode steps "
+                       f"({t_moe * 1e3:.1f} ms/step); model tok/s = 1/(26*t_moe + t_dense + t_head) with "
+                       f"t_dense={t_dense * 1e3:.1f} ms, t_head={t_head * 1e3:.1f} ms; oracle bf16-rounded fp32 math")}
+
+
+def _log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=99)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=1, choices=sorted(CONFIGS))
+    ap.add_argument("--family", choices=("small", "batch"), default=None)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (every box here has one "
+              "GPU); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import dsv2lite
+
+    spec = CONFIGS[args.config]
+    family = args.family or spec["family"]
+    cfg = dsv2lite.DSV2Config()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    t0 = time.perf_counter()
+    w = dsv2lite.init_weights(cfg, device=dev, seed=0)
+    torch.cuda.synchronize()
+    t_init = time.perf_counter() - t0
+    _log(f"weights ready ({w.nbytes() / 1e9:.1f} GB, {t_init:.1f}s)")
+    g = torch.Generator().manual_seed(spec["seed"])
+    lens = spec["prompt"](g)
+    prompts = [torch.randint(0, cfg.vocab, (n,), generator=g) for n in lens]
+    steps, warm = args.steps, args.warmup
+    caps = [n + steps + warm + 8 for n in lens]
+    eng = dsv2lite.DecodeEngine(w, caps, family=family)
+    t0 = time.perf_counter()
+    eng.prefill([p.to(dev) for p in prompts])
+    torch.cuda.synchronize()
+    t_prefill = time.perf_counter() - t0
+    _log(f"prefill of {sum(lens)} tokens done ({t_prefill:.2f}s)")
+    snap = eng.snapshot()
+
+    # one recorded eager step: distinct experts per layer (router output) for the byte model
+    rec = []
+    eng.step(record=rec)
+    torch.cuda.synchronize()
+    n_exp = [int(torch.unique(r[2]).numel()) for r in rec if r[0] == "router"]
+    eng.restore(snap)
+    for _ in range(warm):
+        eng.step()
+    torch.cuda.synchronize()
+    eng.restore(snap)
+    eng.capture()
+    eng.restore(snap)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        eng.replay()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    B = eng.B
+    value = B * steps / dt
+    ms = dt / steps * 1e3
+    # KV rows read per layer per step, averaged over the timed steps (ctx = pos + 1)
+    ctx_avg = sum(n + 1 + (steps - 1) / 2 for n in lens)
+    sb = step_bytes(cfg, n_exp, ctx_avg, B)
+    _log(f"timed {steps} graph replays: {ms:.3f} ms/step, {value:.1f} tok/s")
+    roof = time_dominant_kernel(eng, family)
+    out = {
+        "metric": METRIC, "value": round(value, 2), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warm,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic: random-init weights N(0,0.02) seed 0, uniform random prompt ids",
+        "config": {"workload": spec["workload"], "global_batch": B, "seq_len": max(lens), "kernel_family": family,
+                   "prompt_tokens": sum(lens), "parallelism": "none (1 GPU)"},
+        "roofline": roof,
+        "step_roofline": {"bytes_per_step": sb, "achieved_GBps": sb / (ms / 1e3) / 1e9,
+                          "frac_of_8TBps": sb / (ms / 1e3) / HBM_PEAK, "distinct_experts_per_layer": n_exp},
+        "setup_s": {"init_weights": round(t_init, 2), "prefill": round(t_prefill, 3)},
+    }
+    if not args.no_cpu_baseline:
+        _log("cpu baseline (oracle, config 0)")
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,215 @@
+// Fused absorbed-MLA decode for a few rows (the small family): one 1024-thread
+// workgroup per (row, head) does the whole head:
+//   1. q_lat_h = W_UK_h^T q_nope_h        (16 lanes per output, all loads in flight)
+//   2. new cache row (kv-norm + RoPE(k_pe)) into LDS; the h == 0 workgroup stores it
+//   3. RoPE(q_pe_h); per-wave online softmax over 8-token batches of the cached rows
+//      (one 16-byte load per lane serves both q.k and p.v), the new token from LDS
+//   4. log-sum-exp merge of the 16 waves -> o_lat_h (fp32)
+//   5. attn[row, h*128 + i] = W_UV_h o_lat_h
+// Replaces prepare + split decode + combine (three launches) when the batch is small.
+#include "common.h"
+
+namespace {
+constexpr int kRow = 576, kLat = 512, kWaves = 16, kBatch = 8;
+}
+
+__global__ __launch_bounds__(1024) void mla_fused_kernel(const bf16_t* __restrict__ qkva, int64_t qs,
+                                                         const int32_t* __restrict__ pos,
+                                                         const int64_t* __restrict__ base,
+                                                         const bf16_t* __restrict__ kvw, float eps,
+                                                         const bf16_t* __restrict__ cosT,
+                                                         const bf16_t* __restrict__ sinT, int max_pos,
+                                                         const bf16_t* __restrict__ w_ukt,
+                                                         const bf16_t* __restrict__ w_uv, bf16_t* __restrict__ cache,
+                                                         float scale_log2, bf16_t* __restrict__ out, int64_t os) {
+  __shared__ float qv[kRow];    // q_lat (bf16-rounded) | rotated q_pe
+  __shared__ float nrow[kRow];  // the new token's cache row
+  __shared__ float wm[kWaves], wl[kWaves];
+  __shared__ float wo[kWaves][kLat];
+  __shared__ float olat[kLat];
+  const int b = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const bf16_t* q = qkva + b * qs;
+  const int p = pos[b];
+  const int pc = p < 0 ? 0 : (p >= max_pos ? max_pos - 1 : p);
+  const bf16_t* cs = cosT + (int64_t)pc * 64;
+  const bf16_t* sn = sinT + (int64_t)pc * 64;
+
+  // 1. absorption: row j = u*64 + gi of W_UKT_h (K = 128 split over 16 lanes)
+  {
+    const int gi = tid >> 4, k = tid & 15;
+    float qn[8];
+    unpack8(ldg16(q + h * 192 + k * 8), qn);
+    uint4 wr[8];
+    const bf16_t* wk = w_ukt + ((int64_t)h * kLat + gi) * 128 + k * 8;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) wr[u] = ldg16(wk + (int64_t)u * 64 * 128);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      float s = dot8(wr[u], qn);
+      s += __shfl_xor(s, 8, 64);
+      s += __shfl_xor(s, 4, 64);
+      s += __shfl_xor(s, 2, 64);
+      s += __shfl_xor(s, 1, 64);
+      if (k == 0) qv[u * 64 + gi] = rbf(s);
+    }
+  }
+  // 2./3a. new row (wave 0) and RoPE(q_pe) (wave 1)
+  if (wv == 0) {
+    float f[8], g[8];
+    unpack8(ldg16(q + 3072 + lane * 8), f);
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(f[i], f[i], ss);
+    ss = wave_sum(ss);
+    const float rs = rsqrtf(ss / static_cast<float>(kLat) + eps);
+    unpack8(ldg16(kvw + lane * 8), g);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      f[i] = rbf(g[i] * rbf(f[i] * rs));
+      nrow[lane * 8 + i] = f[i];
+    }
+    bf16_t* crow = cache + (base[b] + p) * kRow;
+    if (h == 0) *reinterpret_cast<uint4*>(crow + lane * 8) = pack8(f);
+    if (lane < 32) {
+      const float e = bf2f(q[3584 + 2 * lane]), o = bf2f(q[3585 + 2 * lane]);
+      const float v0 = rbf(e * bf2f(cs[lane]) - o * bf2f(sn[lane]));
+      const float v1 = rbf(o * bf2f(cs[32 + lane]) + e * bf2f(sn[32 + lane]));
+      nrow[kLat + lane] = v0;
+      nrow[kLat + 32 + lane] = v1;
+      if (h == 0) {
+        crow[kLat + lane] = f2bf(v0);
+        crow[kLat + 32 + lane] = f2bf(v1);
+      }
+    }
+  } else if (wv == 1 && lane < 32) {
+    const bf16_t* qp = q + h * 192 + 128;
+    const float e = bf2f(qp[2 * lane]), o = bf2f(qp[2 * lane + 1]);
+    qv[kLat + lane] = rbf(e * bf2f(cs[lane]) - o * bf2f(sn[lane]));
+    qv[kLat + 32 + lane] = rbf(o * bf2f(cs[32 + lane]) + e * bf2f(sn[32 + lane]));
+  }
+  __syncthreads();
+
+  // 3b. attention: wave wv takes token batches [wv*kBatch + n*kWaves*kBatch, +kBatch)
+  float qa[8], qb[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    qa[i] = qv[lane * 8 + i];
+    qb[i] = lane < 8 ? qv[kLat + lane * 8 + i] : 0.f;
+  }
+  const bf16_t* crow0 = cache + base[b] * kRow;
+  float m = -INFINITY, l = 0.f, o[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = 0.f;
+  const uint4 zero = {0u, 0u, 0u, 0u};
+  for (int t0 = wv * kBatch; t0 < p; t0 += kWaves * kBatch) {
+    uint4 va[kBatch], vb[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int t = min(t0 + u, p - 1);
+      va[u] = ldg16(crow0 + (int64_t)t * kRow + lane * 8);
+      vb[u] = lane < 8 ? ldg16(crow0 + (int64_t)t * kRow + kLat + lane * 8) : zero;
+    }
+    float s[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) s[u] = dot8(va[u], qa) + dot8(vb[u], qb);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1)
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) s[u] += __shfl_xor(s[u], off, 64);
+    float mx = m;
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      s[u] = (t0 + u < p) ? s[u] * scale_log2 : -INFINITY;
+      mx = fmaxf(mx, s[u]);
+    }
+    const float alpha = exp2f(m - mx);
+    m = mx;
+    l *= alpha;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] *= alpha;
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const float pu = exp2f(s[u] - m);
+      l += pu;
+      float v[8];
+      unpack8(va[u], v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = __builtin_fmaf(pu, v[i], o[i]);
+    }
+  }
+  if (wv == 0) {  // the new token (position p) from LDS
+    float sp = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sp = __builtin_fmaf(qa[i], nrow[lane * 8 + i], sp);
+    if (lane < 8) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sp = __builtin_fmaf(qb[i], nrow[kLat + lane * 8 + i], sp);
+    }
+    sp = wave_sum(sp) * scale_log2;
+    const float mx = fmaxf(m, sp);
+    const float alpha = exp2f(m - mx), pu = exp2f(sp - mx);
+    m = mx;
+    l = l * alpha + pu;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = o[i] * alpha + pu * nrow[lane * 8 + i];
+  }
+  if (lane == 0) {
+    wm[wv] = m;
+    wl[wv] = l;
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) wo[wv][lane * 8 + i] = o[i];
+  __syncthreads();
+
+  // 4. merge the waves
+  if (tid < kLat) {
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, wm[w]);
+    float L = 0.f, acc = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float sc = exp2f(wm[w] - M);  // 0 for waves that saw no token
+      L = __builtin_fmaf(wl[w], sc, L);
+      acc = __builtin_fmaf(wo[w][tid], sc, acc);
+    }
+    olat[tid] = acc / L;
+  }
+  __syncthreads();
+
+  // 5. W_UV: wave wv computes rows wv*8 .. wv*8+7 of head h
+  float xo[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) xo[i] = olat[lane * 8 + i];
+  const bf16_t* wp = w_uv + ((int64_t)h * 128 + wv * 8) * kLat + lane * 8;
+  uint4 wr[8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r) wr[r] = ldg16(wp + (int64_t)r * kLat);
+  float rr[8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r) rr[r] = dot8(wr[r], xo);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1)
+#pragma unroll
+    for (int r = 0; r < 8; ++r) rr[r] += __shfl_xor(rr[r], off, 64);
+  if (lane == 0) *reinterpret_cast<uint4*>(out + b * os + h * 128 + wv * 8) = pack8(rr);
+}
+
+extern "C" int dsv2_mla_fused(const void* qkva, int64_t qkva_stride, int rows, const int32_t* pos,
+                              const int64_t* base, const void* kv_norm_w, float eps, const void* rope_cos,
+                              const void* rope_sin, int max_pos, const void* w_ukt, const void* w_uv, void* cache,
+                              float softmax_scale, void* out, int64_t out_stride, void* stream) {
+  DSV2_REQUIRE(qkva && pos && base && kv_norm_w && rope_cos && rope_sin && w_ukt && w_uv && cache && out, DSV2_E_NULL,
+               "mla_fused: null pointer");
+  DSV2_REQUIRE(rows >= 0 && rows <= 65535 && max_pos > 0 && qkva_stride >= 3648, DSV2_E_SHAPE,
+               "mla_fused: bad shape");
+  DSV2_REQUIRE(dsv2_aligned16(qkva) && qkva_stride % 8 == 0 && dsv2_aligned16(kv_norm_w) && dsv2_aligned16(cache) &&
+                   dsv2_aligned16(w_ukt) && dsv2_aligned16(w_uv) && dsv2_aligned16(out) && out_stride % 8 == 0,
+               DSV2_E_ALIGN, "mla_fused: alignment");
+  if (rows == 0) return DSV2_OK;
+  hipLaunchKernelGGL(mla_fused_kernel, dim3(rows, 16), dim3(1024), 0, (hipStream_t)stream, (const bf16_t*)qkva,
+                     qkva_stride, pos, base, (const bf16_t*)kv_norm_w, eps, (const bf16_t*)rope_cos,
+                     (const bf16_t*)rope_sin, max_pos, (const bf16_t*)w_ukt, (const bf16_t*)w_uv, (bf16_t*)cache,
+                     softmax_scale * 1.4426950408889634f, (bf16_t*)out, out_stride);
+  return dsv2_launch_status("mla_fused");
+}

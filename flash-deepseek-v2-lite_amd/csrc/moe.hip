@@ -14,46 +14,49 @@ constexpr int kTopK = 6;
 // (bf16 x bf16 products are exact in fp32); softmax; top-6 by repeated max with
 // ties to the lower index.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void router_kernel(const bf16_t* __restrict__ h, int64_t hs,
-                                                     const bf16_t* __restrict__ nw, float eps,
-                                                     const bf16_t* __restrict__ wr, float scaling,
-                                                     bf16_t* __restrict__ xn_out, const float* __restrict__ logits_in,
-                                                     int32_t* __restrict__ ids32, int64_t* __restrict__ ids64,
-                                                     float* __restrict__ wts) {
+__global__ __launch_bounds__(1024) void router_kernel(const bf16_t* __restrict__ h, int64_t hs,
+                                                      const bf16_t* __restrict__ nw, float eps,
+                                                      const bf16_t* __restrict__ wr, float scaling,
+                                                      bf16_t* __restrict__ xn_out, const float* __restrict__ logits_in,
+                                                      int32_t* __restrict__ ids32, int64_t* __restrict__ ids64,
+                                                      float* __restrict__ wts) {
+  // 16 waves x 4 experts; every router-weight load is issued before the norm
   __shared__ float xs[kH];
   __shared__ float lg[kE];
-  __shared__ float red[4];
+  __shared__ float red[16];
   const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   if (!logits_in) {
-    float f[8], g[8];
-    unpack8(ldg16(h + b * hs + tid * 8), f);
-    float ss = 0.f;
+    uint4 wa[4][4];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(f[i], f[i], ss);
-    ss = block_sum<4>(ss, red);
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) wa[r][j] = ldg16(wr + (int64_t)(wv * 4 + r) * kH + (lane + 64 * j) * 8);
+    // norm: 2 elements per thread
+    const uint32_t x2 = reinterpret_cast<const uint32_t*>(h + b * hs)[tid];
+    float f0 = __uint_as_float(x2 << 16), f1 = __uint_as_float(x2 & 0xffff0000u);
+    const float ss = block_sum<16>(f0 * f0 + f1 * f1, red);
     const float rs = rsqrtf(ss / static_cast<float>(kH) + eps);
-    unpack8(ldg16(nw + tid * 8), g);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      f[i] = rbf(g[i] * rbf(f[i] * rs));
-      xs[tid * 8 + i] = f[i];
-    }
-    if (xn_out) *reinterpret_cast<uint4*>(xn_out + (int64_t)b * kH + tid * 8) = pack8(f);
+    const uint32_t g2 = reinterpret_cast<const uint32_t*>(nw)[tid];
+    f0 = rbf(__uint_as_float(g2 << 16) * rbf(f0 * rs));
+    f1 = rbf(__uint_as_float(g2 & 0xffff0000u) * rbf(f1 * rs));
+    xs[2 * tid] = f0;
+    xs[2 * tid + 1] = f1;
+    if (xn_out) reinterpret_cast<uint32_t*>(xn_out + (int64_t)b * kH)[tid] = pack2(f0, f1);
     __syncthreads();
-    float xl[32];
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 4; ++j) {
+      float xl[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) xl[j * 8 + i] = xs[(lane + 64 * j) * 8 + i];
-    for (int e16 = 0; e16 < 16; ++e16) {
-      const int e = wv * 16 + e16;
-      const bf16_t* we = wr + (int64_t)e * kH;
-      float acc = 0.f;
+      for (int i = 0; i < 8; ++i) xl[i] = xs[(lane + 64 * j) * 8 + i];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc += dot8(ldg16(we + (lane + 64 * j) * 8), xl + j * 8);
-      acc = wave_sum(acc);
-      if (lane == 0) lg[e] = acc;
+      for (int r = 0; r < 4; ++r) acc[r] += dot8(wa[r][j], xl);
     }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] += __shfl_xor(acc[r], off, 64);
+    if (lane < 4) lg[wv * 4 + lane] = lane == 0 ? acc[0] : (lane == 1 ? acc[1] : (lane == 2 ? acc[2] : acc[3]));
     __syncthreads();
   } else {
     if (tid < kE) lg[tid] = logits_in[(int64_t)b * kE + tid];
@@ -88,7 +91,7 @@ extern "C" int dsv2_router_topk6(const void* h, int64_t h_stride, const void* no
                    (!xn_out || dsv2_aligned16(xn_out)),
                DSV2_E_ALIGN, "router: alignment");
   if (rows == 0) return DSV2_OK;
-  hipLaunchKernelGGL(router_kernel, dim3(rows), dim3(256), 0, (hipStream_t)stream, (const bf16_t*)h, h_stride,
+  hipLaunchKernelGGL(router_kernel, dim3(rows), dim3(1024), 0, (hipStream_t)stream, (const bf16_t*)h, h_stride,
                      (const bf16_t*)norm_w, eps, (const bf16_t*)w_router, scaling, (bf16_t*)xn_out, nullptr, ids32,
                      ids64, weights);
   return dsv2_launch_status("router");
@@ -99,9 +102,83 @@ extern "C" int dsv2_router_topk6_from_logits(const float* logits, int rows, floa
   DSV2_REQUIRE(logits && weights && (ids32 || ids64), DSV2_E_NULL, "router_from_logits: null pointer");
   DSV2_REQUIRE(rows >= 0, DSV2_E_SHAPE, "router_from_logits: bad rows");
   if (rows == 0) return DSV2_OK;
-  hipLaunchKernelGGL(router_kernel, dim3(rows), dim3(256), 0, (hipStream_t)stream, nullptr, 0, nullptr, 0.f, nullptr,
+  hipLaunchKernelGGL(router_kernel, dim3(rows), dim3(1024), 0, (hipStream_t)stream, nullptr, 0, nullptr, 0.f, nullptr,
                      scaling, nullptr, logits, ids32, ids64, weights);
   return dsv2_launch_status("router_from_logits");
+}
+
+// ---------------------------------------------------------------------------
+// router logits spread over 8 workgroups per token (8 experts each); the softmax +
+// top-6 is done by the consumers (route_gateup_kernel) from the 64 fp32 logits.
+// ---------------------------------------------------------------------------
+// softmax over 64 logits + top-6 (descending, ties -> lower index) in one wave: lane e
+// holds logit e and counts the lanes that beat it (a larger logit, or an equal one at a
+// lower index); the lanes with rank < 6 publish themselves.  Same selection as repeated
+// argmax, without six serial reductions.
+__device__ __forceinline__ void topk6_wave(const float* __restrict__ lg, float scaling, int* ids, float* w) {
+  const int lane = threadIdx.x & 63;
+  const float x = lg[lane];
+  int rank = 0;
+#pragma unroll 16
+  for (int j = 0; j < kE; ++j) {
+    const float xj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), j));
+    rank += (xj > x || (xj == x && j < lane)) ? 1 : 0;
+  }
+  const float mx = wave_max(x);
+  const float ex = expf(x - mx);
+  const float sm = wave_sum(ex);
+  if (rank < kTopK) {
+    ids[rank] = lane;
+    w[rank] = ex / sm * scaling;
+  }
+}
+
+// router logits over 16 workgroups per token (one expert per wave, its 4 KB row requested
+// before the norm); the softmax + top-6 runs in the consumers (route_gateup_kernel).
+__global__ __launch_bounds__(256) void router_logits_kernel(const bf16_t* __restrict__ h, int64_t hs,
+                                                            const bf16_t* __restrict__ nw, float eps,
+                                                            const bf16_t* __restrict__ wr,
+                                                            bf16_t* __restrict__ xn_out, float* __restrict__ logits) {
+  __shared__ float xs[kH];
+  __shared__ float red[4];
+  const int b = blockIdx.x, part = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int e = part * 4 + wv;
+  uint4 wa[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) wa[j] = ldg16(wr + (int64_t)e * kH + (lane + 64 * j) * 8);
+  float f[8], g[8];
+  unpack8(ldg16(h + b * hs + tid * 8), f);
+  unpack8(ldg16(nw + tid * 8), g);
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(f[i], f[i], ss);
+  ss = block_sum<4>(ss, red);
+  const float rs = rsqrtf(ss / static_cast<float>(kH) + eps);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    f[i] = rbf(g[i] * rbf(f[i] * rs));
+    xs[tid * 8 + i] = f[i];
+  }
+  if (part == 0 && xn_out) *reinterpret_cast<uint4*>(xn_out + (int64_t)b * kH + tid * 8) = pack8(f);
+  __syncthreads();
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc += dot8(wa[j], &xs[(lane + 64 * j) * 8]);
+  acc = wave_sum(acc);
+  if (lane == 0) logits[(int64_t)b * kE + e] = acc;
+}
+
+extern "C" int dsv2_router_logits(const void* h, int64_t h_stride, const void* norm_w, float eps,
+                                  const void* w_router, int rows, void* xn_out, float* logits, void* stream) {
+  DSV2_REQUIRE(h && norm_w && w_router && logits, DSV2_E_NULL, "router_logits: null pointer");
+  DSV2_REQUIRE(rows >= 0 && rows <= 0x7fffffff / kE, DSV2_E_SHAPE, "router_logits: bad rows");
+  DSV2_REQUIRE(dsv2_aligned16(h) && h_stride % 8 == 0 && dsv2_aligned16(norm_w) && dsv2_aligned16(w_router) &&
+                   (!xn_out || dsv2_aligned16(xn_out)),
+               DSV2_E_ALIGN, "router_logits: alignment");
+  if (rows == 0) return DSV2_OK;
+  hipLaunchKernelGGL(router_logits_kernel, dim3(rows, 16), dim3(256), 0, (hipStream_t)stream, (const bf16_t*)h,
+                     h_stride, (const bf16_t*)norm_w, eps, (const bf16_t*)w_router, (bf16_t*)xn_out, logits);
+  return dsv2_launch_status("router_logits");
 }
 
 // ---------------------------------------------------------------------------
@@ -110,18 +187,33 @@ extern "C" int dsv2_router_topk6_from_logits(const float* logits, int rows, floa
 // ---------------------------------------------------------------------------
 template <int RPW>
 __global__ __launch_bounds__(256) void route_gateup_kernel(const bf16_t* __restrict__ xn,
-                                                           const int32_t* __restrict__ ids, int nr,
+                                                           int32_t* __restrict__ ids, int nr,
+                                                           const float* __restrict__ logits, float scaling,
+                                                           float* __restrict__ wts,
                                                            const bf16_t* __restrict__ wgu,
                                                            const bf16_t* __restrict__ shgu, int inter,
                                                            bf16_t* __restrict__ hbuf) {
+  __shared__ int sid[kTopK];
+  __shared__ float sw[kTopK];
   const int route = blockIdx.y;
   const int b = route / nr, s = route % nr;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int i0 = (blockIdx.x * 4 + wv) * RPW;
+  int e = 0;
+  if (s < kTopK && logits) {  // router top-6 from the logits (every routed workgroup; cheap)
+    if (wv == 0) topk6_wave(logits + (int64_t)b * kE, scaling, sid, sw);
+    __syncthreads();
+    e = sid[s];
+    if (blockIdx.x == 0 && s == 0 && threadIdx.x < kTopK) {
+      ids[b * kTopK + threadIdx.x] = sid[threadIdx.x];
+      wts[b * kTopK + threadIdx.x] = sw[threadIdx.x];
+    }
+  } else if (s < kTopK) {
+    e = min(max(ids[b * kTopK + s], 0), kE - 1);
+  }
   if (i0 >= inter) return;
   const bf16_t *gp, *up;
   if (s < kTopK) {
-    const int e = min(max(ids[b * kTopK + s], 0), kE - 1);
     gp = wgu + (int64_t)e * 2 * inter * kH;
     up = gp + (int64_t)inter * kH;
   } else {
@@ -171,74 +263,114 @@ extern "C" int dsv2_moe_route_gateup(const void* xn, int rows, const int32_t* id
   if (rows == 0) return DSV2_OK;
   constexpr int RPW = 2;
   hipLaunchKernelGGL(route_gateup_kernel<RPW>, dim3((inter + 4 * RPW - 1) / (4 * RPW), rows * nr), dim3(256), 0,
-                     (hipStream_t)stream, (const bf16_t*)xn, ids, nr, (const bf16_t*)w_gate_up,
-                     (const bf16_t*)sh_gate_up, inter, (bf16_t*)hbuf);
+                     (hipStream_t)stream, (const bf16_t*)xn, const_cast<int32_t*>(ids), nr, nullptr, 0.f, nullptr,
+                     (const bf16_t*)w_gate_up, (const bf16_t*)sh_gate_up, inter, (bf16_t*)hbuf);
   return dsv2_launch_status("moe_route_gateup");
+}
+
+extern "C" int dsv2_moe_route_gateup_logits(const void* xn, int rows, const float* logits, float scaling,
+                                            int32_t* ids, float* weights, const void* w_gate_up,
+                                            const void* sh_gate_up, int inter, void* hbuf, void* stream) {
+  DSV2_REQUIRE(xn && logits && ids && weights && w_gate_up && hbuf, DSV2_E_NULL,
+               "moe_route_gateup_logits: null pointer");
+  const int nr = sh_gate_up ? kTopK + 2 : kTopK;
+  DSV2_REQUIRE(rows >= 0 && (int64_t)rows * nr <= 65535 && inter > 0 && inter % 8 == 0, DSV2_E_SHAPE,
+               "moe_route_gateup_logits: bad shape");
+  DSV2_REQUIRE(dsv2_aligned16(xn) && dsv2_aligned16(w_gate_up) && (!sh_gate_up || dsv2_aligned16(sh_gate_up)),
+               DSV2_E_ALIGN, "moe_route_gateup_logits: alignment");
+  if (rows == 0) return DSV2_OK;
+  constexpr int RPW = 2;
+  hipLaunchKernelGGL(route_gateup_kernel<RPW>, dim3((inter + 4 * RPW - 1) / (4 * RPW), rows * nr), dim3(256), 0,
+                     (hipStream_t)stream, (const bf16_t*)xn, ids, nr, logits, scaling, weights,
+                     (const bf16_t*)w_gate_up, (const bf16_t*)sh_gate_up, inter, (bf16_t*)hbuf);
+  return dsv2_launch_status("moe_route_gateup_logits");
 }
 
 // ---------------------------------------------------------------------------
 // small family: down projection of every route of a token + weighted top-6 sum
 // (+ shared halves, + residual), deterministic (no atomics). grid (2048/(4*RPW), rows)
 // ---------------------------------------------------------------------------
-template <int NR, int RPW>
+template <int NR>
 __global__ __launch_bounds__(256) void route_down_kernel(const bf16_t* __restrict__ hbuf,
                                                          const int32_t* __restrict__ ids,
                                                          const float* __restrict__ wts,
                                                          const bf16_t* __restrict__ wd,
                                                          const bf16_t* __restrict__ shd, int inter,
                                                          const bf16_t* __restrict__ res, bf16_t* __restrict__ out) {
+  // workgroup: output rows j0, j0+1 of token b; wave w: routes 2w, 2w+1 (all chunks of K = inter)
+  __shared__ float part[8][2];
   const int b = blockIdx.y;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int j0 = (blockIdx.x * 4 + wv) * RPW;
-  if (j0 >= kH) return;
-  const bf16_t* wrow[NR];
-  int64_t wstride[NR];
-#pragma unroll
-  for (int s = 0; s < NR; ++s) {
-    if (s < kTopK) {
-      wrow[s] = wd + (int64_t)min(max(ids[b * kTopK + s], 0), kE - 1) * kH * inter + (int64_t)j0 * inter;
-      wstride[s] = inter;
-    } else {
-      wrow[s] = shd + (int64_t)(s - kTopK) * inter + (int64_t)j0 * 2 * inter;
-      wstride[s] = 2 * inter;
-    }
-  }
-  const bf16_t* hb = hbuf + (int64_t)b * NR * inter;
-  float acc[NR][RPW];
-#pragma unroll
-  for (int s = 0; s < NR; ++s)
-#pragma unroll
-    for (int r = 0; r < RPW; ++r) acc[s][r] = 0.f;
+  const int j0 = blockIdx.x * 2;
   const int nch = inter >> 3;
-  for (int c = lane; c < nch; c += 64) {
-    uint4 w[NR][RPW];
+  constexpr int kMaxCh = 3;  // chunks per lane: ceil(176 / 64) for inter = 1408
+  // the residual is requested up front, not after the dot products
+  const float resv = (res && threadIdx.x < 2) ? bf2f(res[(int64_t)b * kH + j0 + threadIdx.x]) : 0.f;
+  if (2 * wv < NR) {
+    const bf16_t* wrow[2];
+    int64_t wstride[2];
 #pragma unroll
-    for (int s = 0; s < NR; ++s)
+    for (int q = 0; q < 2; ++q) {
+      const int s = 2 * wv + q;
+      if (s < kTopK) {
+        wrow[q] = wd + (int64_t)min(max(ids[b * kTopK + s], 0), kE - 1) * kH * inter + (int64_t)j0 * inter;
+        wstride[q] = inter;
+      } else {
+        wrow[q] = shd + (int64_t)(s - kTopK) * inter + (int64_t)j0 * 2 * inter;
+        wstride[q] = 2 * inter;
+      }
+    }
+    const uint4 zero = {0u, 0u, 0u, 0u};
+    uint4 w[2][2][kMaxCh], x[2][kMaxCh];
 #pragma unroll
-      for (int r = 0; r < RPW; ++r) w[s][r] = ldg16(wrow[s] + r * wstride[s] + c * 8);
+    for (int k = 0; k < kMaxCh; ++k) {
+      const int c = lane + 64 * k;
+      const bool ok = c < nch;
 #pragma unroll
-    for (int s = 0; s < NR; ++s) {
-      float hx[8];
-      unpack8(ldg16(hb + (int64_t)s * inter + c * 8), hx);
+      for (int q = 0; q < 2; ++q) {
+        x[q][k] = ok ? ldg16(hbuf + ((int64_t)b * NR + 2 * wv + q) * inter + c * 8) : zero;
 #pragma unroll
-      for (int r = 0; r < RPW; ++r) acc[s][r] += dot8(w[s][r], hx);
+        for (int r = 0; r < 2; ++r) w[q][r][k] = ok ? ldg16(wrow[q] + r * wstride[q] + c * 8) : zero;
+      }
+    }
+    float acc[2][2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        float a = 0.f;
+#pragma unroll
+        for (int k = 0; k < kMaxCh; ++k) {
+          float hx[8];
+          unpack8(x[q][k], hx);
+          a += dot8(w[q][r][k], hx);
+        }
+        acc[q][r] = a;
+      }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1)
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int r = 0; r < 2; ++r) acc[q][r] += __shfl_xor(acc[q][r], off, 64);
+    if (lane == 0) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int r = 0; r < 2; ++r) part[2 * wv + q][r] = acc[q][r];
     }
   }
+  __syncthreads();
+  if (threadIdx.x < 2) {
+    const int r = threadIdx.x;
+    float routed = 0.f;
+    const float rv = res ? resv : 0.f;
 #pragma unroll
-  for (int s = 0; s < NR; ++s)
-#pragma unroll
-    for (int r = 0; r < RPW; ++r) acc[s][r] = wave_sum(acc[s][r]);
-  if (lane == 0) {
-#pragma unroll
-    for (int r = 0; r < RPW; ++r) {
-      float routed = 0.f;
-#pragma unroll
-      for (int s = 0; s < kTopK; ++s) routed += wts[b * kTopK + s] * rbf(acc[s][r]);
-      float y = rbf(routed);
-      if (NR > kTopK) y = rbf(y + rbf(acc[kTopK][r] + acc[kTopK + 1][r]));
-      if (res) y = rbf(bf2f(res[(int64_t)b * kH + j0 + r]) + y);
-      out[(int64_t)b * kH + j0 + r] = f2bf(y);
-    }
+    for (int s = 0; s < kTopK; ++s) routed += wts[b * kTopK + s] * rbf(part[s][r]);
+    float y = rbf(routed);
+    if (NR > kTopK) y = rbf(y + rbf(part[kTopK][r] + part[kTopK + 1][r]));
+    if (res) y = rbf(rv + y);
+    out[(int64_t)b * kH + j0 + r] = f2bf(y);
   }
 }
 
@@ -246,19 +378,19 @@ extern "C" int dsv2_moe_route_down(const void* hbuf, int rows, const int32_t* id
                                    const void* w_down, const void* sh_down, int inter, const void* residual, void* out,
                                    void* stream) {
   DSV2_REQUIRE(hbuf && ids && weights && w_down && out, DSV2_E_NULL, "moe_route_down: null pointer");
-  DSV2_REQUIRE(rows >= 0 && rows <= 65535 && inter > 0 && inter % 8 == 0, DSV2_E_SHAPE, "moe_route_down: bad shape");
+  DSV2_REQUIRE(rows >= 0 && rows <= 65535 && inter > 0 && inter % 8 == 0 && inter <= 3 * 64 * 8, DSV2_E_SHAPE,
+               "moe_route_down: bad shape (inter %% 8 == 0, inter <= 1536)");
   DSV2_REQUIRE(dsv2_aligned16(hbuf) && dsv2_aligned16(w_down) && (!sh_down || dsv2_aligned16(sh_down)),
                DSV2_E_ALIGN, "moe_route_down: alignment");
   if (rows == 0) return DSV2_OK;
-  constexpr int RPW = 2;
-  const dim3 grid(kH / (4 * RPW), rows);
+  const dim3 grid(kH / 2, rows);
   if (sh_down)
-    hipLaunchKernelGGL((route_down_kernel<kTopK + 2, RPW>), grid, dim3(256), 0, (hipStream_t)stream,
-                       (const bf16_t*)hbuf, ids, weights, (const bf16_t*)w_down, (const bf16_t*)sh_down, inter,
-                       (const bf16_t*)residual, (bf16_t*)out);
+    hipLaunchKernelGGL((route_down_kernel<kTopK + 2>), grid, dim3(256), 0, (hipStream_t)stream, (const bf16_t*)hbuf,
+                       ids, weights, (const bf16_t*)w_down, (const bf16_t*)sh_down, inter, (const bf16_t*)residual,
+                       (bf16_t*)out);
   else
-    hipLaunchKernelGGL((route_down_kernel<kTopK, RPW>), grid, dim3(256), 0, (hipStream_t)stream, (const bf16_t*)hbuf,
-                       ids, weights, (const bf16_t*)w_down, nullptr, inter, (const bf16_t*)residual, (bf16_t*)out);
+    hipLaunchKernelGGL((route_down_kernel<kTopK>), grid, dim3(256), 0, (hipStream_t)stream, (const bf16_t*)hbuf, ids,
+                       weights, (const bf16_t*)w_down, nullptr, inter, (const bf16_t*)residual, (bf16_t*)out);
   return dsv2_launch_status("moe_route_down");
 }
 

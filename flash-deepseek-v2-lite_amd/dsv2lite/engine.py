@@ -34,6 +34,7 @@ from .weights import ModelWeights
 
 BF16 = torch.bfloat16
 FAMILIES = ("small", "batch")
+FUSED_MLA_MAX_CTX = 2048
 
 
 def plan_splits(rows: int, max_ctx: int, target_wgs: int = 1024) -> tuple[int, int]:
@@ -71,6 +72,7 @@ class RowBuffers:
         self.mid = e(rows, cfg.dense_inter)
         if family == "small":
             self.hbuf = e(rows, cfg.top_k + 2, cfg.moe_inter)
+            self.router_logits = e(rows, cfg.n_experts, dt=torch.float32)
         else:
             R = rows * cfg.top_k
             self.olat = e(rows, cfg.n_heads, cfg.kv_rank)
@@ -105,6 +107,9 @@ class DecodeEngine:
         self.ids = torch.zeros(self.B, dtype=torch.int64, device=device)
         self.logits = torch.empty(self.B, cfg.vocab, dtype=torch.float32, device=device)
         self.buf = RowBuffers(cfg, self.B, family, self.max_pos, device)
+        # small family: one fused workgroup per (row, head) while contexts are short; the
+        # split-KV kernel (parallel over the context) takes over for long contexts
+        self.fused_mla = family == "small" and self.max_pos <= FUSED_MLA_MAX_CTX
         self.max_prefill_rows = max_prefill_rows
         self.graph = None
         self._host_pos = [0] * self.B  # host mirror of cache.pos, for capacity checks only
@@ -113,6 +118,15 @@ class DecodeEngine:
     def _attention(self, L, li: int, b: RowBuffers, R: int, pos, base, family: str, st: int) -> None:
         c = self.cfg
         cache = self.cache.layer(li)
+        if family == "small" and self.fused_mla and b is self.buf:
+            call("dsv2_gemv_bf16", ptr(b.h), c.hidden, R, c.hidden, ptr(L.w_qkva), c.qkva_dim, ptr(L.ln_in), c.eps,
+                 None, 0, ptr(b.qkva), c.qkva_dim, 0, st)
+            call("dsv2_mla_fused", ptr(b.qkva), c.qkva_dim, R, ptr(pos), ptr(base), ptr(L.kv_norm), c.eps,
+                 ptr(self.cos), ptr(self.sin), self.max_pos, ptr(L.w_ukt), ptr(L.w_uv), ptr(cache), self.scale,
+                 ptr(b.attn), c.hidden, st)
+            call("dsv2_gemv_bf16", ptr(b.attn), c.hidden, R, c.hidden, ptr(L.w_o), c.hidden, None, 0.0, ptr(b.h),
+                 c.hidden, ptr(b.h), c.hidden, 0, st)
+            return
         if family == "small":
             call("dsv2_gemv_bf16", ptr(b.h), c.hidden, R, c.hidden, ptr(L.w_qkva), c.qkva_dim, ptr(L.ln_in), c.eps,
                  None, 0, ptr(b.qkva), c.qkva_dim, 0, st)
@@ -148,10 +162,10 @@ class DecodeEngine:
         H = c.hidden
         if family == "small":
             if L.moe:
-                call("dsv2_router_topk6", ptr(b.h), H, ptr(L.ln_post), c.eps, ptr(L.w_router), c.routed_scaling, R,
-                     ptr(b.xn), ptr(b.ids32), None, ptr(b.wts), st)
-                call("dsv2_moe_route_gateup", ptr(b.xn), R, ptr(b.ids32), ptr(L.w_gu), ptr(L.sh_gu), c.moe_inter,
-                     ptr(b.hbuf), st)
+                call("dsv2_router_logits", ptr(b.h), H, ptr(L.ln_post), c.eps, ptr(L.w_router), R, ptr(b.xn),
+                     ptr(b.router_logits), st)
+                call("dsv2_moe_route_gateup_logits", ptr(b.xn), R, ptr(b.router_logits), c.routed_scaling,
+                     ptr(b.ids32), ptr(b.wts), ptr(L.w_gu), ptr(L.sh_gu), c.moe_inter, ptr(b.hbuf), st)
                 call("dsv2_moe_route_down", ptr(b.hbuf), R, ptr(b.ids32), ptr(b.wts), ptr(L.w_down), ptr(L.sh_down),
                      c.moe_inter, ptr(b.h), ptr(b.h), st)
             else:

@@ -41,6 +41,9 @@ _SIGS = {
     "dsv2_mla_prepare": ([_p, _i64, _i32, _p, _p, _p, _f32, _p, _p, _i32, _p, _p, _p, _p], _i32),
     "dsv2_mla_decode": ([_p, _p, _p, _p, _i32, _i32, _i32, _f32, _p, _p, _p], _i32),
     "dsv2_mla_combine": ([_p, _p, _p, _i32, _i32, _i32, _p, _p, _i64, _p], _i32),
+    "dsv2_mla_fused": ([_p, _i64, _i32, _p, _p, _p, _f32, _p, _p, _i32, _p, _p, _p, _f32, _p, _i64, _p], _i32),
+    "dsv2_router_logits": ([_p, _i64, _p, _f32, _p, _i32, _p, _p, _p], _i32),
+    "dsv2_moe_route_gateup_logits": ([_p, _i32, _p, _f32, _p, _p, _p, _p, _i32, _p, _p], _i32),
     "dsv2_router_topk6": ([_p, _i64, _p, _f32, _p, _f32, _i32, _p, _p, _p, _p, _p], _i32),
     "dsv2_router_topk6_from_logits": ([_p, _i32, _f32, _p, _p, _p, _p], _i32),
     "dsv2_moe_route_gateup": ([_p, _i32, _p, _p, _p, _i32, _p, _p], _i32),

@@ -139,7 +139,33 @@ int dsv2_mla_combine(const float* part_o, const float* part_ml, const int32_t* p
                      int split_tokens, int max_splits, const void* w_uv, void* out, int64_t out_stride,
                      void* stream);
 
+/* Fused absorbed-MLA decode for a few rows: one workgroup per (row, head) does the W_UK
+ * absorption, kv-norm + RoPE of the new token (stored to cache[base+pos] by the h == 0
+ * workgroup), RoPE(q_pe), softmax over the row's pos+1 cached tokens and W_UV:
+ *   out[r, h*128 + i] = bf16(W_UV_h softmax(scale * q_h . C^T) C[:, :512]).
+ * w_ukt is W_UK transposed [16, 512, 128].  Together with dsv2_gemv_bf16 for the q/kv and
+ * o projections this replaces attention_decode_only_triton / attention_decode_small_batch_triton
+ * (triton_kernels/attention_decode_small.py:553-674, :932-1070) for the small family. */
+int dsv2_mla_fused(const void* qkva, int64_t qkva_stride, int rows, const int32_t* pos, const int64_t* base,
+                   const void* kv_norm_w, float eps, const void* rope_cos, const void* rope_sin, int max_pos,
+                   const void* w_ukt, const void* w_uv, void* cache, float softmax_scale, void* out,
+                   int64_t out_stride, void* stream);
+
 /* ---- MoE ------------------------------------------------------------------ */
+
+/* Router logits only, spread over 16 workgroups per token: xn = RMSNorm(h) (written by the
+ * first workgroup of each row to xn_out), logits[r, e] = fp32(xn) . fp32(W_r[e]) (fp32 [rows, 64]).
+ * The softmax/top-6 then runs inside dsv2_moe_route_gateup_logits.  Replaces the router
+ * GEMV of _graph_gate_forward (src/run.py:268-272). */
+int dsv2_router_logits(const void* h, int64_t h_stride, const void* norm_w, float eps, const void* w_router,
+                       int rows, void* xn_out, float* logits, void* stream);
+
+/* dsv2_moe_route_gateup with the router's softmax + top-6 (triton_kernels/moe_router.py:9-60)
+ * done inside every routed workgroup from the fp32 logits; ids [rows, 6] (int32) and weights
+ * [rows, 6] (score * scaling) are written once per row for the down projection. */
+int dsv2_moe_route_gateup_logits(const void* xn, int rows, const float* logits, float scaling, int32_t* ids,
+                                 float* weights, const void* w_gate_up, const void* sh_gate_up, int inter,
+                                 void* hbuf, void* stream);
 
 /* Router: xn = RMSNorm(h; norm_w) (written to xn_out), logits = fp32(xn) . fp32(W_r)^T
  * [64], softmax, top-6 by repeated max (ties -> lower index), weights = score * scaling.

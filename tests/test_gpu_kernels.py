@@ -305,7 +305,8 @@ def test_mla_decode_combine_vs_fp32(B, lo, hi, seed):
     ns = math.ceil(maxL / split)
     po = torch.empty(B, ns, 16, 512, device=DEV)
     pm = torch.empty(B, ns, 16, 2, device=DEV)
-    call("dsv2_mla_decode", q.data_ptr(), cache.data_ptr(), base.to(DEV).data_ptr(), pos.data_ptr(), B, split, ns,
+    base_d = base.to(DEV)  # keep device copies alive until the kernels have run
+    call("dsv2_mla_decode", q.data_ptr(), cache.data_ptr(), base_d.data_ptr(), pos.data_ptr(), B, split, ns,
          scale, po.data_ptr(), pm.data_ptr(), st())
     olat = torch.empty(B, 16, 512, dtype=BF, device=DEV)
     call("dsv2_mla_combine", po.data_ptr(), pm.data_ptr(), pos.data_ptr(), B, split, ns, None, olat.data_ptr(),
@@ -399,3 +400,79 @@ def test_embed_gather_and_api_errors():
     with pytest.raises(_hip.HipKernelError, match="K%32"):
         call("dsv2_gemm_bf16", table.data_ptr(), 2048, 0, 3, 2000, table.data_ptr(), 0, 64, 1, None, 0,
              out.data_ptr(), 2048, 0, 0, st())
+
+
+@pytest.mark.parametrize("lens", [[1], [231], [40, 7, 300]])
+def test_mla_fused_small_family_vs_fp32(lens):
+    from dsv2lite.config import DSV2Config
+    from dsv2lite.rope import cos_sin_tables
+
+    cfg = DSV2Config()
+    B = len(lens)
+    g = torch.Generator().manual_seed(sum(lens))
+    cap = [L + 5 for L in lens]
+    base = torch.tensor([0] + list(torch.cumsum(torch.tensor(cap), 0)[:-1].tolist()), dtype=torch.int64)
+    cache = (torch.randn(sum(cap), 576, generator=g) * 0.5).to(BF).to(DEV)
+    pos = torch.tensor([L - 1 for L in lens], dtype=torch.int32)  # new token at position L-1
+    qkva = rnd(B, 3648, seed=90)
+    kvw = (rnd(512, seed=91, std=0.1) + 1).to(BF)
+    w_uk = rnd(16, 128, 512, std=0.05, seed=92)
+    w_uv = rnd(16, 128, 512, std=0.05, seed=93)
+    cos, sin = cos_sin_tables(cfg, 512, device=DEV)
+    out = torch.empty(B, 2048, dtype=BF, device=DEV)
+    before = cache.clone()
+    scale = cfg.softmax_scale
+    pos_d, base_d, w_ukt = pos.to(DEV), base.to(DEV), w_uk.transpose(1, 2).contiguous()  # alive across the launch
+    call("dsv2_mla_fused", qkva.data_ptr(), 3648, B, pos_d.data_ptr(), base_d.data_ptr(), kvw.data_ptr(),
+         1e-6, cos.data_ptr(), sin.data_ptr(), 512, w_ukt.data_ptr(), w_uv.data_ptr(),
+         cache.data_ptr(), scale, out.data_ptr(), 2048, st())
+    # reference: same prepare math (oracle pieces), fp32 attention over the updated rows
+    x = qkva.float().cpu()
+    ocos, osin = O.yarn_cos_sin(O.Dims(), 512, mode="bf16")
+    p = pos.long()
+    c_n = O.rmsnorm(x[:, 3072:3584], kvw.float().cpu(), 1e-6, rb)
+    k_pe = rb(O.rope_deinterleave(x[:, 3584:], ocos[p], osin[p], lambda t: t))
+    new_rows = torch.cat([c_n, k_pe], -1)
+    slots = base + p
+    got_rows = cache.float().cpu()[slots]
+    assert rel_err(got_rows, new_rows) < 8e-3
+    mask = torch.ones(cache.shape[0], dtype=torch.bool)
+    mask[slots] = False
+    assert torch.equal(cache.cpu()[mask], before.cpu()[mask])  # nothing else written
+    q_pe = rb(O.rope_deinterleave(x[:, :3072].view(B, 16, 192)[:, :, 128:], ocos[p][:, None], osin[p][:, None],
+                                  lambda t: t))
+    q_lat = rb(torch.einsum("bhi,hij->bhj", x[:, :3072].view(B, 16, 192)[:, :, :128], w_uk.float().cpu()))
+    q_full = torch.cat([q_lat, q_pe], -1)
+    rows = [cache.float().cpu()[int(base[b]):int(base[b]) + lens[b]] for b in range(B)]
+    olat = _mla_reference(q_full, rows, lens, scale)
+    ref = torch.einsum("hij,bhj->bhi", w_uv.float().cpu(), olat).reshape(B, 2048)
+    assert rel_err(out.float().cpu(), ref) < 1e-2
+
+
+@pytest.mark.parametrize("rows", [1, 3])
+def test_router_logits_split_and_gateup_topk(rows):
+    h, nw, wr = _router_case(rows, 95)
+    xn = torch.empty_like(h)
+    lg = torch.empty(rows, 64, dtype=torch.float32, device=DEV)
+    call("dsv2_router_logits", h.data_ptr(), 2048, nw.data_ptr(), 1e-6, wr.data_ptr(), rows, xn.data_ptr(),
+         lg.data_ptr(), st())
+    xr = O.rmsnorm(h.float().cpu(), nw.float().cpu(), 1e-6, rb)
+    assert rel_err(xn.float().cpu(), xr) < 8e-3
+    ref_lg = xn.float().cpu() @ wr.float().cpu().t()
+    assert torch.allclose(lg.cpu(), ref_lg, rtol=1e-5, atol=1e-5)
+    gu, dn, sgu, sdn = _moe_layer(96)
+    ids = torch.full((rows, 6), -1, dtype=torch.int32, device=DEV)
+    w = torch.empty(rows, 6, dtype=torch.float32, device=DEV)
+    hb = torch.empty(rows, 8, 1408, dtype=BF, device=DEV)
+    call("dsv2_moe_route_gateup_logits", xn.data_ptr(), rows, lg.data_ptr(), 1.0, ids.data_ptr(), w.data_ptr(),
+         gu.data_ptr(), sgu.data_ptr(), 1408, hb.data_ptr(), st())
+    oid, ow, _ = O.router_topk(xn.float().cpu(), wr.float().cpu(), 6, 1.0)
+    from_lg = torch.softmax(lg.cpu(), -1)
+    ref_ids = torch.stack([torch.tensor(sorted(range(64), key=lambda e: (-float(from_lg[r, e]), e))[:6])
+                           for r in range(rows)])
+    assert torch.equal(ids.cpu().long(), ref_ids)
+    assert torch.allclose(w.cpu(), from_lg.gather(1, ref_ids), rtol=1e-5)
+    hb2 = torch.empty_like(hb)
+    call("dsv2_moe_route_gateup", xn.data_ptr(), rows, ids.data_ptr(), gu.data_ptr(), sgu.data_ptr(), 1408,
+         hb2.data_ptr(), st())
+    assert torch.equal(hb, hb2)
