@@ -27,88 +27,98 @@ __device__ __forceinline__ void rope_pair(const bf16_t* x, const bf16_t* cs, con
   out[32 + t] = f2bf(o * bf2f(cs[32 + t]) + e * bf2f(sn[32 + t]));
 }
 
+// Workgroup (x, y) handles rows y*RB .. y*RB+RB-1.  With w_ukt != null every workgroup
+// computes 64 of the 16*512 absorbed outputs (rows of W_UK_h^T, K = 128 split over 16
+// lanes, weights requested first); workgroup x == 0 also writes the new cache rows
+// (kv-norm + RoPE(k_pe)) and RoPE(q_pe) of its rows.
 template <bool ABSORB>
-__global__ __launch_bounds__(64) void mla_prepare_kernel(const bf16_t* __restrict__ qkva, int64_t qs, int rows,
-                                                         const int32_t* __restrict__ pos,
-                                                         const int64_t* __restrict__ base,
-                                                         const bf16_t* __restrict__ kvw, float eps,
-                                                         const bf16_t* __restrict__ cosT,
-                                                         const bf16_t* __restrict__ sinT, int max_pos,
-                                                         const bf16_t* __restrict__ w_uk, bf16_t* __restrict__ cache,
-                                                         bf16_t* __restrict__ qout) {
-  constexpr int RB = 16;
-  __shared__ float qn[RB][128];
-  const int b0 = blockIdx.x * RB, h = blockIdx.y, jb = blockIdx.z, lane = threadIdx.x;
+__global__ __launch_bounds__(256) void mla_prepare_kernel(const bf16_t* __restrict__ qkva, int64_t qs, int rows,
+                                                          const int32_t* __restrict__ pos,
+                                                          const int64_t* __restrict__ base,
+                                                          const bf16_t* __restrict__ kvw, float eps,
+                                                          const bf16_t* __restrict__ cosT,
+                                                          const bf16_t* __restrict__ sinT, int max_pos,
+                                                          const bf16_t* __restrict__ w_ukt, bf16_t* __restrict__ cache,
+                                                          bf16_t* __restrict__ qout) {
+  constexpr int RB = ABSORB ? 8 : 1;  // RoPE/cache only: one row per workgroup
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int b0 = blockIdx.y * RB;
   const int nr = min(RB, rows - b0);
-  if (jb == 0) {
+  if (ABSORB) {
+    const int gi = tid >> 4, k = tid & 15;
+    const int row0 = blockIdx.x * 64 + gi * 4;  // 4 consecutive rows of one head
+    const int h = row0 / kLat, j0 = row0 % kLat;
+    uint4 wr[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) wr[q] = ldg16(w_ukt + (int64_t)(row0 + q) * 128 + k * 8);
     for (int r = 0; r < nr; ++r) {
-      const int b = b0 + r;
-      int p = pos[b];
-      p = p < 0 ? 0 : (p >= max_pos ? max_pos - 1 : p);
-      const bf16_t* q = qkva + b * qs;
-      const bf16_t* cs = cosT + (int64_t)p * 64;
-      const bf16_t* sn = sinT + (int64_t)p * 64;
-      if (lane < 32) rope_pair(q + h * 192 + 128, cs, sn, qout + ((int64_t)b * kHeads + h) * kRow + kLat, lane);
-      if (h == 0) {
-        float f[8], g[8];
-        unpack8(ldg16(q + 3072 + lane * 8), f);
-        float ss = 0.f;
+      float qn[8];
+      unpack8(ldg16(qkva + (b0 + r) * qs + h * 192 + k * 8), qn);
+      float sdot[4];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(f[i], f[i], ss);
-        ss = wave_sum(ss);
-        const float rs = rsqrtf(ss / static_cast<float>(kLat) + eps);
-        unpack8(ldg16(kvw + lane * 8), g);
+      for (int q = 0; q < 4; ++q) sdot[q] = dot8(wr[q], qn);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) f[i] = g[i] * rbf(f[i] * rs);
-        bf16_t* crow = cache + (base[b] + pos[b]) * kRow;
-        *reinterpret_cast<uint4*>(crow + lane * 8) = pack8(f);
-        if (lane < 32) rope_pair(q + 3584, cs, sn, crow + kLat, lane);
+      for (int off = 8; off > 0; off >>= 1)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) sdot[q] += __shfl_xor(sdot[q], off, 64);
+      if (k == 0) {
+        uint2 o;
+        o.x = pack2(sdot[0], sdot[1]);
+        o.y = pack2(sdot[2], sdot[3]);
+        *reinterpret_cast<uint2*>(qout + ((int64_t)(b0 + r) * kHeads + h) * kRow + j0) = o;
       }
     }
   }
-  if (!ABSORB) return;
-  for (int idx = lane; idx < nr * 128; idx += 64) {
-    const int r = idx >> 7, i = idx & 127;
-    qn[r][i] = bf2f(qkva[(b0 + r) * qs + h * 192 + i]);
-  }
-  __syncthreads();
-  float acc[RB][2];
+  if (blockIdx.x != 0) return;
+  for (int r = 0; r < nr; ++r) {
+    const int b = b0 + r;
+    int p = pos[b];
+    p = p < 0 ? 0 : (p >= max_pos ? max_pos - 1 : p);
+    const bf16_t* q = qkva + b * qs;
+    const bf16_t* cs = cosT + (int64_t)p * 64;
+    const bf16_t* sn = sinT + (int64_t)p * 64;
+    // RoPE(q_pe) of the 16 heads: 512 (head, pair) items over 256 threads
+    for (int it = tid; it < kHeads * 32; it += 256) {
+      const int h = it >> 5, t = it & 31;
+      rope_pair(q + h * 192 + 128, cs, sn, qout + ((int64_t)b * kHeads + h) * kRow + kLat, t);
+    }
+    if (wv == 0) {
+      float f[8], g[8];
+      unpack8(ldg16(q + 3072 + lane * 8), f);
+      float ss = 0.f;
 #pragma unroll
-  for (int r = 0; r < RB; ++r) acc[r][0] = acc[r][1] = 0.f;
-  const bf16_t* wp = w_uk + (int64_t)h * 128 * kLat + jb * 128 + 2 * lane;
-#pragma unroll 8
-  for (int i = 0; i < 128; ++i) {
-    const uint32_t w2 = *reinterpret_cast<const uint32_t*>(wp + i * kLat);
-    const float w0 = __uint_as_float(w2 << 16), w1 = __uint_as_float(w2 & 0xffff0000u);
+      for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(f[i], f[i], ss);
+      ss = wave_sum(ss);
+      const float rs = rsqrtf(ss / static_cast<float>(kLat) + eps);
+      unpack8(ldg16(kvw + lane * 8), g);
 #pragma unroll
-    for (int r = 0; r < RB; ++r) {
-      acc[r][0] = __builtin_fmaf(qn[r][i], w0, acc[r][0]);
-      acc[r][1] = __builtin_fmaf(qn[r][i], w1, acc[r][1]);
+      for (int i = 0; i < 8; ++i) f[i] = g[i] * rbf(f[i] * rs);
+      bf16_t* crow = cache + (base[b] + pos[b]) * kRow;
+      *reinterpret_cast<uint4*>(crow + lane * 8) = pack8(f);
+      if (lane < 32) rope_pair(q + 3584, cs, sn, crow + kLat, lane);
     }
   }
-  for (int r = 0; r < nr; ++r)
-    *reinterpret_cast<uint32_t*>(qout + ((int64_t)(b0 + r) * kHeads + h) * kRow + jb * 128 + 2 * lane) =
-        pack2(acc[r][0], acc[r][1]);
 }
 
 extern "C" int dsv2_mla_prepare(const void* qkva, int64_t qkva_stride, int rows, const int32_t* pos,
                                 const int64_t* base, const void* kv_norm_w, float eps, const void* rope_cos,
-                                const void* rope_sin, int max_pos, const void* w_uk, void* cache, void* q_out,
+                                const void* rope_sin, int max_pos, const void* w_ukt, void* cache, void* q_out,
                                 void* stream) {
   DSV2_REQUIRE(qkva && pos && base && kv_norm_w && rope_cos && rope_sin && cache && q_out, DSV2_E_NULL,
                "mla_prepare: null pointer");
-  DSV2_REQUIRE(rows >= 0 && max_pos > 0 && qkva_stride >= kQkvA, DSV2_E_SHAPE, "mla_prepare: bad shape");
+  DSV2_REQUIRE(rows >= 0 && rows <= 65535 && max_pos > 0 && qkva_stride >= kQkvA, DSV2_E_SHAPE,
+               "mla_prepare: bad shape");
   DSV2_REQUIRE(dsv2_aligned16(qkva) && qkva_stride % 8 == 0 && dsv2_aligned16(kv_norm_w) && dsv2_aligned16(cache) &&
-                   dsv2_aligned16(q_out) && (!w_uk || dsv2_aligned16(w_uk)),
+                   dsv2_aligned16(q_out) && (!w_ukt || dsv2_aligned16(w_ukt)),
                DSV2_E_ALIGN, "mla_prepare: alignment");
   if (rows == 0) return DSV2_OK;
-  const dim3 grid((rows + 15) / 16, kHeads, w_uk ? 4 : 1);
-  if (w_uk)
-    hipLaunchKernelGGL(mla_prepare_kernel<true>, grid, dim3(64), 0, (hipStream_t)stream, (const bf16_t*)qkva,
+  const dim3 grid(w_ukt ? kHeads * kLat / 64 : 1, w_ukt ? (rows + 7) / 8 : rows);
+  if (w_ukt)
+    hipLaunchKernelGGL(mla_prepare_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, (const bf16_t*)qkva,
                        qkva_stride, rows, pos, base, (const bf16_t*)kv_norm_w, eps, (const bf16_t*)rope_cos,
-                       (const bf16_t*)rope_sin, max_pos, (const bf16_t*)w_uk, (bf16_t*)cache, (bf16_t*)q_out);
+                       (const bf16_t*)rope_sin, max_pos, (const bf16_t*)w_ukt, (bf16_t*)cache, (bf16_t*)q_out);
   else
-    hipLaunchKernelGGL(mla_prepare_kernel<false>, grid, dim3(64), 0, (hipStream_t)stream, (const bf16_t*)qkva,
+    hipLaunchKernelGGL(mla_prepare_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, (const bf16_t*)qkva,
                        qkva_stride, rows, pos, base, (const bf16_t*)kv_norm_w, eps, (const bf16_t*)rope_cos,
                        (const bf16_t*)rope_sin, max_pos, nullptr, (bf16_t*)cache, (bf16_t*)q_out);
   return dsv2_launch_status("mla_prepare");
@@ -273,9 +283,16 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(const float* __restric
                                                           bf16_t* __restrict__ out, int64_t os) {
   __shared__ float olat[kLat];
   __shared__ float wsp[64];
-  const int b = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int b = blockIdx.x, h = blockIdx.y, part = blockIdx.z, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int len = pos[b] + 1;
   const int ns = min((len + split_tokens - 1) / split_tokens, max_splits);
+  // W_UV rows of this workgroup (part*32 + wv*8 .. +8) are requested before the merge
+  uint4 wr[8];
+  if (UV) {
+    const bf16_t* wp = w_uv + ((int64_t)h * 128 + part * 32 + wv * 8) * kLat + lane * 8;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) wr[r] = ldg16(wp + (int64_t)r * kLat);
+  }
   if (wv == 0) {
     const float* pm = part_ml + ((int64_t)b * max_splits * kHeads + h) * 2;
     const float m = lane < ns ? pm[(int64_t)lane * kHeads * 2] : -INFINITY;
@@ -294,7 +311,7 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(const float* __restric
     o1 = __builtin_fmaf(wsp[s], v.y, o1);
   }
   if (!UV) {
-    *reinterpret_cast<uint32_t*>(out + b * os + h * kLat + 2 * tid) = pack2(o0, o1);
+    if (part == 0) *reinterpret_cast<uint32_t*>(out + b * os + h * kLat + 2 * tid) = pack2(o0, o1);
     return;
   }
   olat[2 * tid] = o0;
@@ -303,17 +320,14 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(const float* __restric
   float xo[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) xo[e] = olat[lane * 8 + e];
-  const bf16_t* wp = w_uv + ((int64_t)h * 128 + wv * 32) * kLat + lane * 8;
-  float r[32];
+  float r[8];
 #pragma unroll
-  for (int i = 0; i < 32; ++i) r[i] = dot8(ldg16(wp + i * kLat), xo);
+  for (int i = 0; i < 8; ++i) r[i] = dot8(wr[i], xo);
 #pragma unroll
-  for (int i = 0; i < 32; ++i) r[i] = wave_sum(r[i]);
-  if (lane == 0) {
-    bf16_t* o = out + b * os + h * 128 + wv * 32;
+  for (int off = 32; off > 0; off >>= 1)
 #pragma unroll
-    for (int i = 0; i < 32; i += 2) *reinterpret_cast<uint32_t*>(o + i) = pack2(r[i], r[i + 1]);
-  }
+    for (int i = 0; i < 8; ++i) r[i] += __shfl_xor(r[i], off, 64);
+  if (lane == 0) *reinterpret_cast<uint4*>(out + b * os + h * 128 + part * 32 + wv * 8) = pack8(r);
 }
 
 extern "C" int dsv2_mla_combine(const float* part_o, const float* part_ml, const int32_t* pos, int rows,
@@ -326,7 +340,7 @@ extern "C" int dsv2_mla_combine(const float* part_o, const float* part_ml, const
                "mla_combine: alignment");
   if (rows == 0) return DSV2_OK;
   if (w_uv)
-    hipLaunchKernelGGL(mla_combine_kernel<true>, dim3(rows, kHeads), dim3(256), 0, (hipStream_t)stream, part_o,
+    hipLaunchKernelGGL(mla_combine_kernel<true>, dim3(rows, kHeads, 4), dim3(256), 0, (hipStream_t)stream, part_o,
                        part_ml, pos, split_tokens, max_splits, (const bf16_t*)w_uv, (bf16_t*)out, out_stride);
   else
     hipLaunchKernelGGL(mla_combine_kernel<false>, dim3(rows, kHeads), dim3(256), 0, (hipStream_t)stream, part_o,

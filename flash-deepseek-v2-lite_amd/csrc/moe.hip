@@ -135,13 +135,12 @@ __device__ __forceinline__ void topk6_wave(const float* __restrict__ lg, float s
 
 // router logits over 16 workgroups per token (one expert per wave, its 4 KB row requested
 // before the norm); the softmax + top-6 runs in the consumers (route_gateup_kernel).
-__global__ __launch_bounds__(256) void router_logits_kernel(const bf16_t* __restrict__ h, int64_t hs,
-                                                            const bf16_t* __restrict__ nw, float eps,
-                                                            const bf16_t* __restrict__ wr,
-                                                            bf16_t* __restrict__ xn_out, float* __restrict__ logits) {
-  __shared__ float xs[kH];
-  __shared__ float red[4];
-  const int b = blockIdx.x, part = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+// xs: kH floats of LDS, red: 4 floats of LDS (owned by the calling kernel)
+__device__ __forceinline__ void router_logits_block(int b, int part, const bf16_t* __restrict__ h, int64_t hs,
+                                                    const bf16_t* __restrict__ nw, float eps,
+                                                    const bf16_t* __restrict__ wr, bf16_t* __restrict__ xn_out,
+                                                    float* __restrict__ logits, float* xs, float* red) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int e = part * 4 + wv;
   uint4 wa[4];
 #pragma unroll
@@ -168,45 +167,49 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const bf16_t* __rest
   if (lane == 0) logits[(int64_t)b * kE + e] = acc;
 }
 
-extern "C" int dsv2_router_logits(const void* h, int64_t h_stride, const void* norm_w, float eps,
-                                  const void* w_router, int rows, void* xn_out, float* logits, void* stream) {
-  DSV2_REQUIRE(h && norm_w && w_router && logits, DSV2_E_NULL, "router_logits: null pointer");
-  DSV2_REQUIRE(rows >= 0 && rows <= 0x7fffffff / kE, DSV2_E_SHAPE, "router_logits: bad rows");
-  DSV2_REQUIRE(dsv2_aligned16(h) && h_stride % 8 == 0 && dsv2_aligned16(norm_w) && dsv2_aligned16(w_router) &&
-                   (!xn_out || dsv2_aligned16(xn_out)),
-               DSV2_E_ALIGN, "router_logits: alignment");
-  if (rows == 0) return DSV2_OK;
-  hipLaunchKernelGGL(router_logits_kernel, dim3(rows, 16), dim3(256), 0, (hipStream_t)stream, (const bf16_t*)h,
-                     h_stride, (const bf16_t*)norm_w, eps, (const bf16_t*)w_router, (bf16_t*)xn_out, logits);
-  return dsv2_launch_status("router_logits");
-}
 
 // ---------------------------------------------------------------------------
 // small family: route-local gate_up + SwiGLU.  grid (inter/(4*RPW), rows*NR)
 // route r*NR+s: s < 6 -> routed expert ids[r,s]; s = 6, 7 -> shared-expert half.
 // ---------------------------------------------------------------------------
 template <int RPW>
-__global__ __launch_bounds__(256) void route_gateup_kernel(const bf16_t* __restrict__ xn,
-                                                           int32_t* __restrict__ ids, int nr,
-                                                           const float* __restrict__ logits, float scaling,
-                                                           float* __restrict__ wts,
-                                                           const bf16_t* __restrict__ wgu,
-                                                           const bf16_t* __restrict__ shgu, int inter,
-                                                           bf16_t* __restrict__ hbuf) {
-  __shared__ int sid[kTopK];
-  __shared__ float sw[kTopK];
-  const int route = blockIdx.y;
-  const int b = route / nr, s = route % nr;
+__device__ __forceinline__ void route_gateup_block(int bx, int route, const bf16_t* __restrict__ xn,
+                                                   int32_t* __restrict__ ids, int nr, int s_off, int hbuf_routes,
+                                                   const float* __restrict__ logits, float scaling,
+                                                   float* __restrict__ wts, const bf16_t* __restrict__ h, int64_t hs,
+                                                   const bf16_t* __restrict__ nw, float eps,
+                                                   const bf16_t* __restrict__ wgu, const bf16_t* __restrict__ shgu,
+                                                   int inter, bf16_t* __restrict__ hbuf) {
+  // route r = blockIdx.y: row b = r / nr, route slot s = r % nr + s_off (s < 6 routed,
+  // s = 6, 7 the shared-expert halves); output row (b * hbuf_routes + s) of hbuf.
+  // With h != null the input is RMSNorm(h; nw) computed here (each wave from its own
+  // chunks), so shared-expert launches need nothing from the router.
+  const int b = route / nr, s = route % nr + s_off;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int i0 = (blockIdx.x * 4 + wv) * RPW;
+  const int i0 = (bx * 4 + wv) * RPW;
   int e = 0;
-  if (s < kTopK && logits) {  // router top-6 from the logits (every routed workgroup; cheap)
-    if (wv == 0) topk6_wave(logits + (int64_t)b * kE, scaling, sid, sw);
-    __syncthreads();
-    e = sid[s];
-    if (blockIdx.x == 0 && s == 0 && threadIdx.x < kTopK) {
-      ids[b * kTopK + threadIdx.x] = sid[threadIdx.x];
-      wts[b * kTopK + threadIdx.x] = sw[threadIdx.x];
+  if (s < kTopK && logits) {
+    // every wave ranks the 64 logits itself (no LDS, no barrier): lane j holds logit j,
+    // rank = number of lanes with a larger logit or an equal one at a lower index;
+    // route slot s takes the lane of rank s (softmax is monotonic, so this is the top-6
+    // of the router scores, descending, ties to the lower index)
+    const float x = logits[(int64_t)b * kE + lane];
+    int rank = 0;
+#pragma unroll 16
+    for (int j = 0; j < kE; ++j) {
+      const float xj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), j));
+      rank += (xj > x || (xj == x && j < lane)) ? 1 : 0;
+    }
+    const unsigned long long m = __ballot(rank == s);
+    e = __ffsll(m) - 1;
+    if (bx == 0 && s == 0 && wv == 0) {
+      const float mx = wave_max(x);
+      const float ex = expf(x - mx);
+      const float sm = wave_sum(ex);
+      if (rank < kTopK) {
+        ids[b * kTopK + rank] = lane;
+        wts[b * kTopK + rank] = ex / sm * scaling;
+      }
     }
   } else if (s < kTopK) {
     e = min(max(ids[b * kTopK + s], 0), kE - 1);
@@ -223,9 +226,6 @@ __global__ __launch_bounds__(256) void route_gateup_kernel(const bf16_t* __restr
   }
   gp += (int64_t)i0 * kH;
   up += (int64_t)i0 * kH;
-  float xf[32];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) unpack8(ldg16(xn + (int64_t)b * kH + (lane + 64 * j) * 8), xf + j * 8);
   uint4 wg[RPW][4], wu[RPW][4];
 #pragma unroll
   for (int r = 0; r < RPW; ++r)
@@ -234,6 +234,25 @@ __global__ __launch_bounds__(256) void route_gateup_kernel(const bf16_t* __restr
       wg[r][j] = ldg16(gp + (int64_t)r * kH + (lane + 64 * j) * 8);
       wu[r][j] = ldg16(up + (int64_t)r * kH + (lane + 64 * j) * 8);
     }
+  float xf[32];
+  if (h) {
+    float g8[32];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      unpack8(ldg16(h + b * hs + (lane + 64 * j) * 8), xf + j * 8);
+      unpack8(ldg16(nw + (lane + 64 * j) * 8), g8 + j * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < 32; ++i) ss = __builtin_fmaf(xf[i], xf[i], ss);
+    ss = wave_sum(ss);
+    const float rn = rsqrtf(ss / static_cast<float>(kH) + eps);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) xf[i] = rbf(g8[i] * rbf(xf[i] * rn));
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) unpack8(ldg16(xn + (int64_t)b * kH + (lane + 64 * j) * 8), xf + j * 8);
+  }
   float ag[RPW], au[RPW];
 #pragma unroll
   for (int r = 0; r < RPW; ++r) {
@@ -248,8 +267,118 @@ __global__ __launch_bounds__(256) void route_gateup_kernel(const bf16_t* __restr
   }
   if (lane == 0) {
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) hbuf[(int64_t)route * inter + i0 + r] = f2bf(swiglu_bf(ag[r], au[r]));
+    for (int r = 0; r < RPW; ++r)
+      hbuf[((int64_t)b * hbuf_routes + s) * inter + i0 + r] = f2bf(swiglu_bf(ag[r], au[r]));
   }
+}
+
+// shared-expert down projection, one wave per output row j of token b:
+// shared_y[b, j] = bf16(hbuf[b, 6:8, :] . sh_down[j, :])   (K = 2 * inter)
+__device__ __forceinline__ void shared_down_block(int blk, int b, const bf16_t* __restrict__ hbuf,
+                                                  const bf16_t* __restrict__ shd, int inter,
+                                                  bf16_t* __restrict__ shared_y) {
+  constexpr int kMaxCh = 6;  // ceil(2 * 1408 / 8 / 64)
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int j = blk * 4 + wv;
+  const int K = 2 * inter, nch = K >> 3;
+  const bf16_t* w = shd + (int64_t)j * K;
+  const bf16_t* x = hbuf + ((int64_t)b * (kTopK + 2) + kTopK) * inter;
+  const uint4 zero = {0u, 0u, 0u, 0u};
+  uint4 wv4[kMaxCh], xv4[kMaxCh];
+#pragma unroll
+  for (int k = 0; k < kMaxCh; ++k) {
+    const int c = lane + 64 * k;
+    wv4[k] = c < nch ? ldg16(w + c * 8) : zero;
+    xv4[k] = c < nch ? ldg16(x + c * 8) : zero;
+  }
+  float a = 0.f;
+#pragma unroll
+  for (int k = 0; k < kMaxCh; ++k) {
+    float xf[8];
+    unpack8(xv4[k], xf);
+    a += dot8(wv4[k], xf);
+  }
+  a = wave_sum(a);
+  if (lane == 0) shared_y[(int64_t)b * kH + j] = f2bf(a);
+}
+
+// The one MoE "gate" kernel.  Workgroup ranges, in dispatch order:
+//   [0, n_router)              router logits, 16 workgroups per token
+//   [n_router, + n_gate)       gate_up + SwiGLU, gu_blocks workgroups per (token, route)
+//   [.., + n_sdown)            shared-expert down, 512 workgroups per token
+// Every MoE entry point (router logits, route-local gate_up) launches this kernel with the
+// other ranges empty.
+struct MoeGateArgs {
+  int n_router, n_gate, n_sdown;
+  // router
+  const bf16_t* h;
+  int64_t hs;
+  const bf16_t* nw;
+  float eps;
+  const bf16_t* wr;
+  bf16_t* xn_out;
+  float* logits_out;
+  // gate_up
+  int gu_blocks, nr, s_off, hbuf_routes;
+  const bf16_t* xn;
+  int32_t* ids;
+  const float* logits_in;
+  float scaling;
+  float* wts;
+  const bf16_t* gate_h;  // non-null: the gate_up input is RMSNorm(gate_h; nw) (shared halves)
+  const bf16_t* wgu;
+  const bf16_t* shgu;
+  int inter;
+  bf16_t* hbuf;
+  // shared down
+  const bf16_t* shd;
+  bf16_t* shared_y;
+};
+
+__global__ __launch_bounds__(256) void moe_gate_kernel(const MoeGateArgs a) {
+  __shared__ float xs[kH];
+  __shared__ float red[4];
+  int v = blockIdx.x;
+  if (v < a.n_router) {
+    router_logits_block(v >> 4, v & 15, a.h, a.hs, a.nw, a.eps, a.wr, a.xn_out, a.logits_out, xs, red);
+    return;
+  }
+  v -= a.n_router;
+  if (v < a.n_gate) {
+    route_gateup_block<2>(v % a.gu_blocks, v / a.gu_blocks, a.xn, a.ids, a.nr, a.s_off, a.hbuf_routes, a.logits_in,
+                          a.scaling, a.wts, a.gate_h, a.hs, a.nw, a.eps, a.wgu, a.shgu, a.inter, a.hbuf);
+    return;
+  }
+  v -= a.n_gate;
+  shared_down_block(v % (kH / 4), v / (kH / 4), a.hbuf, a.shd, a.inter, a.shared_y);
+}
+
+static int launch_moe_gate(const MoeGateArgs& a, hipStream_t st, const char* what) {
+  const int64_t grid = (int64_t)a.n_router + a.n_gate + a.n_sdown;
+  DSV2_REQUIRE(grid <= 0x7fffffff, DSV2_E_SHAPE, "%s: too many rows", what);
+  if (grid == 0) return DSV2_OK;
+  hipLaunchKernelGGL(moe_gate_kernel, dim3((unsigned)grid), dim3(256), 0, st, a);
+  return dsv2_launch_status(what);
+}
+
+extern "C" int dsv2_router_logits(const void* h, int64_t h_stride, const void* norm_w, float eps,
+                                  const void* w_router, int rows, void* xn_out, float* logits, void* stream) {
+  DSV2_REQUIRE(h && norm_w && w_router && logits, DSV2_E_NULL, "router_logits: null pointer");
+  DSV2_REQUIRE(rows >= 0 && rows <= 0x7fffffff / kE, DSV2_E_SHAPE, "router_logits: bad rows");
+  DSV2_REQUIRE(dsv2_aligned16(h) && h_stride % 8 == 0 && dsv2_aligned16(norm_w) && dsv2_aligned16(w_router) &&
+                   (!xn_out || dsv2_aligned16(xn_out)),
+               DSV2_E_ALIGN, "router_logits: alignment");
+  if (rows == 0) return DSV2_OK;
+  MoeGateArgs a{};
+  a.n_router = rows * 16;
+  a.h = (const bf16_t*)h;
+  a.hs = h_stride;
+  a.nw = (const bf16_t*)norm_w;
+  a.eps = eps;
+  a.wr = (const bf16_t*)w_router;
+  a.xn_out = (bf16_t*)xn_out;
+  a.logits_out = logits;
+  return launch_moe_gate(a, (hipStream_t)stream, "router_logits");
 }
 
 extern "C" int dsv2_moe_route_gateup(const void* xn, int rows, const int32_t* ids, const void* w_gate_up,
@@ -262,11 +391,22 @@ extern "C" int dsv2_moe_route_gateup(const void* xn, int rows, const int32_t* id
                DSV2_E_ALIGN, "moe_route_gateup: alignment");
   if (rows == 0) return DSV2_OK;
   constexpr int RPW = 2;
-  hipLaunchKernelGGL(route_gateup_kernel<RPW>, dim3((inter + 4 * RPW - 1) / (4 * RPW), rows * nr), dim3(256), 0,
-                     (hipStream_t)stream, (const bf16_t*)xn, const_cast<int32_t*>(ids), nr, nullptr, 0.f, nullptr,
-                     (const bf16_t*)w_gate_up, (const bf16_t*)sh_gate_up, inter, (bf16_t*)hbuf);
-  return dsv2_launch_status("moe_route_gateup");
+  MoeGateArgs a{};
+  a.gu_blocks = (inter + 4 * RPW - 1) / (4 * RPW);
+  a.n_gate = rows * nr * a.gu_blocks;
+  a.nr = nr;
+  a.hbuf_routes = nr;
+  a.xn = (const bf16_t*)xn;
+  a.ids = const_cast<int32_t*>(ids);
+  a.wgu = (const bf16_t*)w_gate_up;
+  a.shgu = (const bf16_t*)sh_gate_up;
+  a.inter = inter;
+  a.hbuf = (bf16_t*)hbuf;
+  return launch_moe_gate(a, (hipStream_t)stream, "moe_route_gateup");
 }
+
+
+
 
 extern "C" int dsv2_moe_route_gateup_logits(const void* xn, int rows, const float* logits, float scaling,
                                             int32_t* ids, float* weights, const void* w_gate_up,
@@ -280,10 +420,21 @@ extern "C" int dsv2_moe_route_gateup_logits(const void* xn, int rows, const floa
                DSV2_E_ALIGN, "moe_route_gateup_logits: alignment");
   if (rows == 0) return DSV2_OK;
   constexpr int RPW = 2;
-  hipLaunchKernelGGL(route_gateup_kernel<RPW>, dim3((inter + 4 * RPW - 1) / (4 * RPW), rows * nr), dim3(256), 0,
-                     (hipStream_t)stream, (const bf16_t*)xn, ids, nr, logits, scaling, weights,
-                     (const bf16_t*)w_gate_up, (const bf16_t*)sh_gate_up, inter, (bf16_t*)hbuf);
-  return dsv2_launch_status("moe_route_gateup_logits");
+  MoeGateArgs a{};
+  a.gu_blocks = (inter + 4 * RPW - 1) / (4 * RPW);
+  a.n_gate = rows * nr * a.gu_blocks;
+  a.nr = nr;
+  a.hbuf_routes = kTopK + 2;
+  a.xn = (const bf16_t*)xn;
+  a.ids = ids;
+  a.logits_in = logits;
+  a.scaling = scaling;
+  a.wts = weights;
+  a.wgu = (const bf16_t*)w_gate_up;
+  a.shgu = (const bf16_t*)sh_gate_up;
+  a.inter = inter;
+  a.hbuf = (bf16_t*)hbuf;
+  return launch_moe_gate(a, (hipStream_t)stream, "moe_route_gateup_logits");
 }
 
 // ---------------------------------------------------------------------------
@@ -295,7 +446,8 @@ __global__ __launch_bounds__(256) void route_down_kernel(const bf16_t* __restric
                                                          const int32_t* __restrict__ ids,
                                                          const float* __restrict__ wts,
                                                          const bf16_t* __restrict__ wd,
-                                                         const bf16_t* __restrict__ shd, int inter,
+                                                         const bf16_t* __restrict__ shd, int inter, int hbuf_routes,
+                                                         const bf16_t* __restrict__ shared_y,
                                                          const bf16_t* __restrict__ res, bf16_t* __restrict__ out) {
   // workgroup: output rows j0, j0+1 of token b; wave w: routes 2w, 2w+1 (all chunks of K = inter)
   __shared__ float part[8][2];
@@ -306,6 +458,7 @@ __global__ __launch_bounds__(256) void route_down_kernel(const bf16_t* __restric
   constexpr int kMaxCh = 3;  // chunks per lane: ceil(176 / 64) for inter = 1408
   // the residual is requested up front, not after the dot products
   const float resv = (res && threadIdx.x < 2) ? bf2f(res[(int64_t)b * kH + j0 + threadIdx.x]) : 0.f;
+  const float shv = (shared_y && threadIdx.x < 2) ? bf2f(shared_y[(int64_t)b * kH + j0 + threadIdx.x]) : 0.f;
   if (2 * wv < NR) {
     const bf16_t* wrow[2];
     int64_t wstride[2];
@@ -328,7 +481,7 @@ __global__ __launch_bounds__(256) void route_down_kernel(const bf16_t* __restric
       const bool ok = c < nch;
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
-        x[q][k] = ok ? ldg16(hbuf + ((int64_t)b * NR + 2 * wv + q) * inter + c * 8) : zero;
+        x[q][k] = ok ? ldg16(hbuf + ((int64_t)b * hbuf_routes + 2 * wv + q) * inter + c * 8) : zero;
 #pragma unroll
         for (int r = 0; r < 2; ++r) w[q][r][k] = ok ? ldg16(wrow[q] + r * wstride[q] + c * 8) : zero;
       }
@@ -369,28 +522,33 @@ __global__ __launch_bounds__(256) void route_down_kernel(const bf16_t* __restric
     for (int s = 0; s < kTopK; ++s) routed += wts[b * kTopK + s] * rbf(part[s][r]);
     float y = rbf(routed);
     if (NR > kTopK) y = rbf(y + rbf(part[kTopK][r] + part[kTopK + 1][r]));
+    else if (shared_y) y = rbf(y + shv);
     if (res) y = rbf(rv + y);
     out[(int64_t)b * kH + j0 + r] = f2bf(y);
   }
 }
 
 extern "C" int dsv2_moe_route_down(const void* hbuf, int rows, const int32_t* ids, const float* weights,
-                                   const void* w_down, const void* sh_down, int inter, const void* residual, void* out,
-                                   void* stream) {
+                                   const void* w_down, const void* sh_down, int inter, int hbuf_routes,
+                                   const void* shared_y, const void* residual, void* out, void* stream) {
   DSV2_REQUIRE(hbuf && ids && weights && w_down && out, DSV2_E_NULL, "moe_route_down: null pointer");
   DSV2_REQUIRE(rows >= 0 && rows <= 65535 && inter > 0 && inter % 8 == 0 && inter <= 3 * 64 * 8, DSV2_E_SHAPE,
                "moe_route_down: bad shape (inter %% 8 == 0, inter <= 1536)");
   DSV2_REQUIRE(dsv2_aligned16(hbuf) && dsv2_aligned16(w_down) && (!sh_down || dsv2_aligned16(sh_down)),
                DSV2_E_ALIGN, "moe_route_down: alignment");
+  DSV2_REQUIRE(!(sh_down && shared_y), DSV2_E_FLAGS, "moe_route_down: sh_down and shared_y are exclusive");
+  DSV2_REQUIRE(hbuf_routes >= (sh_down ? kTopK + 2 : kTopK) && hbuf_routes <= kTopK + 2, DSV2_E_SHAPE,
+               "moe_route_down: hbuf_routes must cover the routes read");
   if (rows == 0) return DSV2_OK;
   const dim3 grid(kH / 2, rows);
   if (sh_down)
     hipLaunchKernelGGL((route_down_kernel<kTopK + 2>), grid, dim3(256), 0, (hipStream_t)stream, (const bf16_t*)hbuf,
-                       ids, weights, (const bf16_t*)w_down, (const bf16_t*)sh_down, inter, (const bf16_t*)residual,
-                       (bf16_t*)out);
+                       ids, weights, (const bf16_t*)w_down, (const bf16_t*)sh_down, inter, hbuf_routes, nullptr,
+                       (const bf16_t*)residual, (bf16_t*)out);
   else
     hipLaunchKernelGGL((route_down_kernel<kTopK>), grid, dim3(256), 0, (hipStream_t)stream, (const bf16_t*)hbuf, ids,
-                       weights, (const bf16_t*)w_down, nullptr, inter, (const bf16_t*)residual, (bf16_t*)out);
+                       weights, (const bf16_t*)w_down, nullptr, inter, hbuf_routes, (const bf16_t*)shared_y,
+                       (const bf16_t*)residual, (bf16_t*)out);
   return dsv2_launch_status("moe_route_down");
 }
 

@@ -90,9 +90,11 @@ class RowBuffers:
 
 class DecodeEngine:
     def __init__(self, weights: ModelWeights, capacities: list[int], family: str = "small",
-                 max_prefill_rows: int = 1024, device="cuda"):
+                 max_prefill_rows: int = 1024, device="cuda", mla_path: str = "fused"):
         if family not in FAMILIES:
             raise ValueError(f"Unknown kernel family: {family}")
+        if mla_path not in ("split", "fused"):
+            raise ValueError(f"Unknown MLA path: {mla_path}")
         cfg = weights.cfg
         cfg.check_kernel_dims()
         self.cfg = cfg
@@ -109,7 +111,7 @@ class DecodeEngine:
         self.buf = RowBuffers(cfg, self.B, family, self.max_pos, device)
         # small family: one fused workgroup per (row, head) while contexts are short; the
         # split-KV kernel (parallel over the context) takes over for long contexts
-        self.fused_mla = family == "small" and self.max_pos <= FUSED_MLA_MAX_CTX
+        self.fused_mla = family == "small" and self.max_pos <= FUSED_MLA_MAX_CTX and mla_path == "fused"
         self.max_prefill_rows = max_prefill_rows
         self.graph = None
         self._host_pos = [0] * self.B  # host mirror of cache.pos, for capacity checks only
@@ -131,7 +133,7 @@ class DecodeEngine:
             call("dsv2_gemv_bf16", ptr(b.h), c.hidden, R, c.hidden, ptr(L.w_qkva), c.qkva_dim, ptr(L.ln_in), c.eps,
                  None, 0, ptr(b.qkva), c.qkva_dim, 0, st)
             call("dsv2_mla_prepare", ptr(b.qkva), c.qkva_dim, R, ptr(pos), ptr(base), ptr(L.kv_norm), c.eps,
-                 ptr(self.cos), ptr(self.sin), self.max_pos, ptr(L.w_uk), ptr(cache), ptr(b.q), st)
+                 ptr(self.cos), ptr(self.sin), self.max_pos, ptr(L.w_ukt), ptr(cache), ptr(b.q), st)
         else:
             call("dsv2_gemm_bf16", ptr(b.xn), c.hidden, 0, R, c.hidden, ptr(L.w_qkva), 0, c.qkva_dim, 1, None, 0,
                  ptr(b.qkva), c.qkva_dim, 0, 0, st)
@@ -167,7 +169,7 @@ class DecodeEngine:
                 call("dsv2_moe_route_gateup_logits", ptr(b.xn), R, ptr(b.router_logits), c.routed_scaling,
                      ptr(b.ids32), ptr(b.wts), ptr(L.w_gu), ptr(L.sh_gu), c.moe_inter, ptr(b.hbuf), st)
                 call("dsv2_moe_route_down", ptr(b.hbuf), R, ptr(b.ids32), ptr(b.wts), ptr(L.w_down), ptr(L.sh_down),
-                     c.moe_inter, ptr(b.h), ptr(b.h), st)
+                     c.moe_inter, c.top_k + 2, None, ptr(b.h), ptr(b.h), st)
             else:
                 call("dsv2_gemv_bf16", ptr(b.h), H, R, H, ptr(L.w_gu), c.dense_inter, ptr(L.ln_post), c.eps, None, 0,
                      ptr(b.mid), c.dense_inter, LINEAR_SWIGLU, st)

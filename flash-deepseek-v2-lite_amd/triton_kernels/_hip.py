@@ -47,7 +47,7 @@ _SIGS = {
     "dsv2_router_topk6": ([_p, _i64, _p, _f32, _p, _f32, _i32, _p, _p, _p, _p, _p], _i32),
     "dsv2_router_topk6_from_logits": ([_p, _i32, _f32, _p, _p, _p, _p], _i32),
     "dsv2_moe_route_gateup": ([_p, _i32, _p, _p, _p, _i32, _p, _p], _i32),
-    "dsv2_moe_route_down": ([_p, _i32, _p, _p, _p, _p, _i32, _p, _p, _p], _i32),
+    "dsv2_moe_route_down": ([_p, _i32, _p, _p, _p, _p, _i32, _i32, _p, _p, _p, _p], _i32),
     "dsv2_moe_bucket": ([_p, _i32, _i32, _p, _p, _p, _p, _p], _i32),
     "dsv2_moe_grouped_gateup": ([_p, _p, _p, _p, _i32, _i32, _p, _i32, _p, _p], _i32),
     "dsv2_moe_grouped_down": ([_p, _p, _p, _i32, _i32, _p, _i32, _p, _p], _i32),

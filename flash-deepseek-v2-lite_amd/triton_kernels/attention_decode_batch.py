@@ -95,7 +95,7 @@ def _attention_decode(family: str, hidden_states, cos, sin, position_ids, cache_
              qkva.data_ptr(), QKVA, 0, st)
         call("dsv2_mla_prepare", qkva.data_ptr(), QKVA, B, pos.data_ptr(), base.data_ptr(),
              packed.kv_norm_weight.data_ptr(), packed.kv_norm_eps, cos2.data_ptr(), sin2.data_ptr(), max_pos,
-             packed.w_uk.data_ptr(), key_cache.data_ptr(), q.data_ptr(), st)
+             packed.w_ukt.data_ptr(), key_cache.data_ptr(), q.data_ptr(), st)
     else:
         call("dsv2_gemm_bf16", x.data_ptr(), HID, 0, B, HID, packed.w_qkva.data_ptr(), 0, QKVA, 1, None, 0,
              qkva.data_ptr(), QKVA, 0, 0, st)

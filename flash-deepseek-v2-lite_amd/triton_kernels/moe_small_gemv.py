@@ -28,7 +28,7 @@ def batched_grouped_routed_moe_route_gemv(x: torch.Tensor, topk_ids: torch.Tenso
     _hip.call("dsv2_moe_route_gateup", x.data_ptr(), B, ids.data_ptr(), packed.gate_up_weights.data_ptr(), None, I,
               hbuf.data_ptr(), st)
     _hip.call("dsv2_moe_route_down", hbuf.data_ptr(), B, ids.data_ptr(), w.data_ptr(), packed.down_weights.data_ptr(),
-              None, I, None, out.data_ptr(), st)
+              None, I, 6, None, None, out.data_ptr(), st)
     return out
 
 

@@ -111,13 +111,14 @@ int dsv2_gemm_bf16(const void* x, int64_t x_stride, int64_t x_gstride, int rows,
  *   c = RMSNorm(qkva[r, 3072:3584]; kv_norm_w) -> cache[slot, 0:512]
  *   k_pe = RoPE(qkva[r, 3584:3648], pos)      -> cache[slot, 512:576]
  *   q_out[r, h, 512:576] = RoPE(q_pe_h);  q_out[r, h, 0:512] = W_UK_h^T q_nope_h
- *     (only when w_uk != NULL; the batch family runs the absorption as a grouped GEMM).
+ *     (only when w_ukt != NULL: W_UK transposed, [16, 512, 128]; the batch family runs the
+ *     absorption as a grouped GEMM instead).
  * RoPE rotates de-interleaved pairs with bf16 cos/sin tables [max_pos, 64].
  * Replaces kv-norm + _batched_build_qkv_rope_kernel + _cache_write_q1_dual_kernel
  * (attention_decode_batch.py:719-813; attention_decode_small.py:141-339). */
 int dsv2_mla_prepare(const void* qkva, int64_t qkva_stride, int rows, const int32_t* pos,
                      const int64_t* base, const void* kv_norm_w, float eps, const void* rope_cos,
-                     const void* rope_sin, int max_pos, const void* w_uk, void* cache, void* q_out,
+                     const void* rope_sin, int max_pos, const void* w_ukt, void* cache, void* q_out,
                      void* stream);
 
 /* Split-KV absorbed-MLA decode over the compressed cache [*, 576] bf16.
@@ -162,7 +163,8 @@ int dsv2_router_logits(const void* h, int64_t h_stride, const void* norm_w, floa
 
 /* dsv2_moe_route_gateup with the router's softmax + top-6 (triton_kernels/moe_router.py:9-60)
  * done inside every routed workgroup from the fp32 logits; ids [rows, 6] (int32) and weights
- * [rows, 6] (score * scaling) are written once per row for the down projection. */
+ * [rows, 6] (score * scaling) are written once per row for the down projection.  hbuf is
+ * [rows, 8, inter]: routes 0..5 (and the shared halves 6, 7 when sh_gate_up != NULL). */
 int dsv2_moe_route_gateup_logits(const void* xn, int rows, const float* logits, float scaling, int32_t* ids,
                                  float* weights, const void* w_gate_up, const void* sh_gate_up, int inter,
                                  void* hbuf, void* stream);
@@ -191,13 +193,14 @@ int dsv2_moe_route_gateup(const void* xn, int rows, const int32_t* ids, const vo
 
 /* Small family, route-local down + top-6 combine (+ shared, + residual):
  *   d_s = bf16(hbuf[r,s,:] . Wd_s[j,:]);  routed = bf16(sum_{s<6} w[r,s] d_s)  (fp32, slot order)
- *   shared = bf16(d_6 + d_7) (when sh_down != NULL);  y = bf16(routed + shared)
+ *   shared = bf16(d_6 + d_7) when sh_down != NULL, or shared_y[r, j] (a precomputed shared-expert
+ *   output) when shared_y != NULL;  y = bf16(routed + shared)
  *   out[r, j] = residual ? bf16(residual[r, j] + y) : y.
- * w_down [64, 2048, inter]; sh_down [2048, 2*inter].  Replaces _down_partial_kernel +
- * _down_reduce_topk6_kernel (moe_small_gemv.py:109-191, :257-347). */
+ * hbuf is [rows, hbuf_routes, inter] (6 or 8).  w_down [64, 2048, inter]; sh_down [2048, 2*inter].
+ * Replaces _down_partial_kernel + _down_reduce_topk6_kernel (moe_small_gemv.py:109-191, :257-347). */
 int dsv2_moe_route_down(const void* hbuf, int rows, const int32_t* ids, const float* weights,
-                        const void* w_down, const void* sh_down, int inter, const void* residual, void* out,
-                        void* stream);
+                        const void* w_down, const void* sh_down, int inter, int hbuf_routes, const void* shared_y,
+                        const void* residual, void* out, void* stream);
 
 /* Batch family bucketing (one workgroup, deterministic counting sort by expert):
  *   sorted_routes[p] = route index r*6+s in expert order, stable in r;

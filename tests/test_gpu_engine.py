@@ -116,14 +116,15 @@ def _oracle_step(om, cache, toks, start):
     return res, trace
 
 
-@pytest.mark.parametrize("family,lens", [("small", [16]), ("batch", [16]), ("small", [5, 11]),
-                                         ("batch", [5, 16, 9, 1])])
-def test_engine_decode_vs_oracle(model, family, lens):
+@pytest.mark.parametrize("family,lens,mla", [("small", [16], "split"), ("small", [16], "fused"), ("batch", [16], "split"),
+                                             ("small", [5, 11], "split"), ("small", [5, 11], "fused"),
+                                             ("batch", [5, 16, 9, 1], "split")])
+def test_engine_decode_vs_oracle(model, family, lens, mla):
     import dsv2lite
 
     cfg, w, om = model
     B = len(lens)
-    eng = dsv2lite.DecodeEngine(w, [n + 16 for n in lens], family=family)
+    eng = dsv2lite.DecodeEngine(w, [n + 16 for n in lens], family=family, mla_path=mla)
     prompts = _prompts(lens, seed=7 + B)
     first = eng.prefill([p.cuda() for p in prompts]).cpu().clone()
     torch.cuda.synchronize()

@@ -242,7 +242,7 @@ def test_moe_small_family_route_local(rows):
     call("dsv2_moe_route_gateup", xn.data_ptr(), rows, dids.data_ptr(), gu.data_ptr(), sgu.data_ptr(), 1408,
          hbuf.data_ptr(), st())
     call("dsv2_moe_route_down", hbuf.data_ptr(), rows, dids.data_ptr(), dw.data_ptr(), dn.data_ptr(), sdn.data_ptr(),
-         1408, h.data_ptr(), out.data_ptr(), st())
+         1408, 8, None, h.data_ptr(), out.data_ptr(), st())
     c = lambda t: t.float().cpu()  # noqa: E731
     routed, shared = _oracle_moe_parts(c(xn), ids, w, c(gu), c(dn), c(sgu), c(sdn))
     ref = rb(c(h) + rb(routed + shared))
@@ -251,9 +251,19 @@ def test_moe_small_family_route_local(rows):
     hb6 = torch.empty(rows, 6, 1408, dtype=BF, device=DEV)
     call("dsv2_moe_route_gateup", xn.data_ptr(), rows, dids.data_ptr(), gu.data_ptr(), None, 1408, hb6.data_ptr(),
          st())
-    call("dsv2_moe_route_down", hb6.data_ptr(), rows, dids.data_ptr(), dw.data_ptr(), dn.data_ptr(), None, 1408, None,
-         out.data_ptr(), st())
+    call("dsv2_moe_route_down", hb6.data_ptr(), rows, dids.data_ptr(), dw.data_ptr(), dn.data_ptr(), None, 1408, 6,
+         None, None, out.data_ptr(), st())
     assert rel_err(c(out), routed) < 1e-2
+    # precomputed shared output (shared_y) added by the 6-route down == 8-route down
+    shy = torch.empty(rows, 2048, dtype=BF, device=DEV)
+    call("dsv2_gemv_bf16", hbuf[:, 6:].data_ptr(), 8 * 1408, rows, 2816, sdn.data_ptr(), 2048, None, 0.0, None, 0,
+         shy.data_ptr(), 2048, 0, st())
+    out2 = torch.empty_like(h)
+    call("dsv2_moe_route_down", hbuf.data_ptr(), rows, dids.data_ptr(), dw.data_ptr(), dn.data_ptr(), None, 1408, 8,
+         shy.data_ptr(), h.data_ptr(), out2.data_ptr(), st())
+    call("dsv2_moe_route_down", hbuf.data_ptr(), rows, dids.data_ptr(), dw.data_ptr(), dn.data_ptr(), sdn.data_ptr(),
+         1408, 8, None, h.data_ptr(), out.data_ptr(), st())
+    assert rel_err(c(out2), c(out)) < 1e-2
 
 
 @pytest.mark.parametrize("rows", [3, 64, 256])
@@ -341,22 +351,24 @@ def test_mla_constant_cache_returns_value():
     assert torch.allclose(olat.float().cpu(), row[:512].float().expand(B, 16, 512), rtol=1e-2, atol=1e-3)
 
 
-def test_mla_prepare_vs_oracle():
+@pytest.mark.parametrize("B", [5, 11])
+def test_mla_prepare_vs_oracle(B):
     from dsv2lite.config import DSV2Config
     from dsv2lite.rope import cos_sin_tables
 
     cfg = DSV2Config()
-    B = 5
     qkva = rnd(B, 3648, seed=70)
     kvw = (rnd(512, seed=71, std=0.1) + 1).to(BF)
     w_uk = rnd(16, 128, 512, std=0.05, seed=72)
     cos, sin = cos_sin_tables(cfg, 4096, device=DEV)
-    pos = torch.tensor([0, 5, 127, 2048, 4000], dtype=torch.int32, device=DEV)
-    base = torch.tensor([0, 10, 200, 3000, 7000], dtype=torch.int64, device=DEV)
+    pos = torch.tensor([0, 5, 127, 2048, 4000, 1, 2, 3, 4, 6, 7][:B], dtype=torch.int32, device=DEV)
+    base = torch.tensor([0, 10, 200, 3000, 7000, 8000, 8100, 8200, 8300, 8400, 8500][:B], dtype=torch.int64,
+                        device=DEV)
     cache = torch.zeros(12000, 576, dtype=BF, device=DEV)
     q = torch.zeros(B, 16, 576, dtype=BF, device=DEV)
+    w_ukt = w_uk.transpose(1, 2).contiguous()
     call("dsv2_mla_prepare", qkva.data_ptr(), 3648, B, pos.data_ptr(), base.data_ptr(), kvw.data_ptr(), 1e-6,
-         cos.data_ptr(), sin.data_ptr(), 4096, w_uk.data_ptr(), cache.data_ptr(), q.data_ptr(), st())
+         cos.data_ptr(), sin.data_ptr(), 4096, w_ukt.data_ptr(), cache.data_ptr(), q.data_ptr(), st())
     ocos, osin = O.yarn_cos_sin(O.Dims(), 4096, mode="bf16")
     assert torch.equal(cos.float().cpu(), ocos) and torch.equal(sin.float().cpu(), osin)
     x = qkva.float().cpu()
