@@ -166,6 +166,9 @@ def main() -> None:
     ap.add_argument("--config", type=int, default=1, choices=sorted(CONFIGS))
     ap.add_argument("--family", choices=("small", "batch"), default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run 3 plain 512 MiB device copies (the reference kernel for scaling the "
+                         "FETCH_SIZE / WRITE_SIZE counters of a --pmc run)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (every box here has one "
@@ -234,6 +237,14 @@ def main() -> None:
                           "frac_of_8TBps": sb / (ms / 1e3) / HBM_PEAK, "distinct_experts_per_layer": n_exp},
         "setup_s": {"init_weights": round(t_init, 2), "prefill": round(t_prefill, 3)},
     }
+    if args.copy_calibration:
+        src = torch.empty(256 * 2**20, dtype=torch.float16, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        out["copy_calibration_bytes"] = {"read": src.nbytes, "write": dst.nbytes}
+        del src, dst
     if not args.no_cpu_baseline:
         _log("cpu baseline (oracle, config 0)")
         out["cpu_baseline"] = cpu_baseline()

