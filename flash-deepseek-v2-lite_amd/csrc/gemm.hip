@@ -1,12 +1,15 @@
-// Grouped bf16 GEMM on CDNA4 matrix cores (v_mfma_f32_16x16x32_bf16).
+// Grouped bf16 GEMM on CDNA4 matrix cores (v_mfma_f32_16x16x32_bf16) for the
+// weight-streaming shapes of batched decode (tokens M <= 128 per tile, K up to 10944).
 //
-// Output tile of a wave: 16 weight rows (MFMA M) x 16*TB tokens (MFMA N), fp32
-// accumulators, K stepped by 32.  A operand = weight rows straight from HBM
-// (16 B per lane per step: row li = lane&15, k-group kg = lane>>4), B operand =
-// token rows (same k mapping; L2-resident).  A workgroup = 4 waves = 64 weight
-// rows, so every weight byte of a (group, row-block) is fetched once per token
-// tile.  Groups are experts (MoE), heads (MLA absorption) or a single dense
-// matrix.  D layout: lane holds rows 4*kg..4*kg+3 of column li.
+// A workgroup owns 16 output features (SwiGLU: 16 gate rows and the 16 matching up
+// rows) for 16*TB tokens and streams those weight rows from HBM exactly once; its NW
+// waves split K into contiguous ranges of 32-wide steps, and their fp32 partial tiles
+// are summed through LDS in a fixed wave order (deterministic).  Per step a lane loads
+// 16 B of weight row (lane & 15) at k-group (lane >> 4) (A operand) and 16 B of each
+// token row (B operand, L2-resident); D layout: lane holds rows 4*kg..4*kg+3 of
+// token column (lane & 15).  Grid: x = N / 16 feature tiles, y = token tiles x groups
+// (or the MoE tile table).  Groups are experts (MoE), heads (MLA absorption) or one
+// dense matrix.
 #include "common.h"
 
 struct GemmArgs {
@@ -27,8 +30,10 @@ struct GemmArgs {
   bool out_f32;
 };
 
-template <int TB, bool SWIGLU>
-__global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
+template <int TB, bool SWIGLU, int NW, int U>
+__global__ __launch_bounds__(NW * 64) void gemm_kernel(const GemmArgs a) {
+  constexpr int R = SWIGLU ? 2 : 1;  // weight row blocks per tile (gate, up)
+  __shared__ floatx4_t red[NW][R][TB][64];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int li = lane & 15, kg = lane >> 4;
   int g, start, count;
@@ -43,68 +48,73 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
     start = (blockIdx.y % a.tiles_per_group) * 16 * TB;
     count = min(16 * TB, a.rows - start);
   }
-  const int n0 = blockIdx.x * 64 + wv * 16;
+  const int n0 = blockIdx.x * 16;
   const int K = a.K;
-  const bf16_t* wrow = a.W + g * a.wg + (int64_t)(n0 + li) * K + kg * 8;
-  const bf16_t* wrow_u = wrow + (int64_t)a.N * K;
+  const bf16_t* wrow[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) wrow[r] = a.W + g * a.wg + (int64_t)(n0 + r * a.N + li) * K + kg * 8;
 
+  // token rows past the tile read the tile's first row (always valid) and are not stored,
+  // so every load below is unconditional (exact vmcnt waits, no masked loads)
   const bf16_t* xrow[TB];
-  bool valid[TB];
 #pragma unroll
   for (int tb = 0; tb < TB; ++tb) {
-    const int j = tb * 16 + li;
-    valid[tb] = j < count;
-    int xr = 0;
-    if (valid[tb]) xr = a.slot_row ? a.slot_row[start + j] / a.slot_div : start + j;
+    const int j = tb * 16 + li < count ? tb * 16 + li : 0;
+    const int xr = a.slot_row ? a.slot_row[start + j] / a.slot_div : start + j;
     xrow[tb] = a.X + g * a.xg + (int64_t)xr * a.xs + kg * 8;
   }
 
-  floatx4_t acc[TB], accu[TB];
+  floatx4_t acc[R][TB];
 #pragma unroll
-  for (int tb = 0; tb < TB; ++tb) acc[tb] = accu[tb] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) acc[r][tb] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 
-  const uint4 zero = {0u, 0u, 0u, 0u};
-  constexpr int U = 4;
-  int k0 = 0;
-  for (; k0 + 32 * U <= K; k0 += 32 * U) {
-    uint4 av[U], au[U], bv[U][TB];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      av[u] = ldg16(wrow + k0 + u * 32);
-      if (SWIGLU) au[u] = ldg16(wrow_u + k0 + u * 32);
-    }
+  // K = nb batches of U 32-wide steps (the host picks U | K/32); wave wv takes the
+  // contiguous batches [nb*wv/NW, nb*(wv+1)/NW), all loads of a batch before its MFMAs
+  const int nb = (K >> 5) / U;
+  const int b0 = (nb * wv) / NW, b1 = (nb * (wv + 1)) / NW;
+  for (int bi = b0; bi < b1; ++bi) {
+    const int s = bi * U;
+    uint4 av[U][R], bv[U][TB];
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int tb = 0; tb < TB; ++tb) bv[u][tb] = valid[tb] ? ldg16(xrow[tb] + k0 + u * 32) : zero;
+      for (int r = 0; r < R; ++r) av[u][r] = ldg16(wrow[r] + (s + u) * 32);
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int tb = 0; tb < TB; ++tb) {
-        acc[tb] = mfma16x16x32(as_bf16x8(av[u]), as_bf16x8(bv[u][tb]), acc[tb]);
-        if (SWIGLU) accu[tb] = mfma16x16x32(as_bf16x8(au[u]), as_bf16x8(bv[u][tb]), accu[tb]);
-      }
-  }
-  for (; k0 < K; k0 += 32) {
-    const uint4 av = ldg16(wrow + k0);
-    uint4 au = zero;
-    if (SWIGLU) au = ldg16(wrow_u + k0);
+      for (int tb = 0; tb < TB; ++tb) bv[u][tb] = ldg16(xrow[tb] + (s + u) * 32);
 #pragma unroll
-    for (int tb = 0; tb < TB; ++tb) {
-      const uint4 bv = valid[tb] ? ldg16(xrow[tb] + k0) : zero;
-      acc[tb] = mfma16x16x32(as_bf16x8(av), as_bf16x8(bv), acc[tb]);
-      if (SWIGLU) accu[tb] = mfma16x16x32(as_bf16x8(au), as_bf16x8(bv), accu[tb]);
-    }
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb) acc[r][tb] = mfma16x16x32(as_bf16x8(av[u][r]), as_bf16x8(bv[u][tb]), acc[r][tb]);
   }
 
+  if (NW > 1) {
 #pragma unroll
-  for (int tb = 0; tb < TB; ++tb) {
-    if (!valid[tb]) continue;
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int tb = 0; tb < TB; ++tb) red[wv][r][tb][lane] = acc[r][tb];
+    __syncthreads();
+  }
+  // epilogue: wave wv finishes token blocks wv, wv + NW, ... (sum over waves in order 0..NW-1)
+  for (int tb = wv; tb < TB; tb += NW) {
     const int slot = start + tb * 16 + li;
+    if (tb * 16 + li >= count) continue;
+    floatx4_t sum[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      sum[r] = NW > 1 ? red[0][r][tb][lane] : acc[r][tb];
+#pragma unroll
+      for (int w = 1; w < NW; ++w) sum[r] += red[w][r][tb][lane];
+    }
     const int n = n0 + 4 * kg;
     float v[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = SWIGLU ? swiglu_bf(acc[tb][e], accu[tb][e]) : rbf(acc[tb][e]);
+    for (int e = 0; e < 4; ++e) v[e] = SWIGLU ? swiglu_bf(sum[0][e], sum[R - 1][e]) : rbf(sum[0][e]);
     if (a.res) {
       const uint2 r2 = *reinterpret_cast<const uint2*>(a.res + slot * a.rs + n);
       v[0] = rbf(__uint_as_float(r2.x << 16) + v[0]);
@@ -124,32 +134,39 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
   }
 }
 
+// Launch shape by token blocks: NW waves split K in batches of U steps (U = 4 when it
+// divides K/32, else 2).  The fp32 reduction buffer is NW*R*TB KB of LDS (<= 64 KB).
+// Token tiles are at most 128 (TB = 8): larger row counts run as several tiles (their
+// weights then come from L2 / Infinity Cache after the first).
 static int launch_gemm(const GemmArgs& a, int tb, bool swiglu, int grid_y, hipStream_t st) {
-  const dim3 grid(a.N / 64, grid_y);
-#define DSV2_GEMM(TBV)                                                        \
-  if (swiglu)                                                                 \
-    hipLaunchKernelGGL((gemm_kernel<TBV, true>), grid, dim3(256), 0, st, a);  \
-  else                                                                        \
-    hipLaunchKernelGGL((gemm_kernel<TBV, false>), grid, dim3(256), 0, st, a);
+  const dim3 grid(a.N / 16, grid_y);
+  const bool u4 = ((a.K >> 5) % 4) == 0;
+#define DSV2_GEMM(TBV, SWV, NWV)                                                                  \
+  if (u4)                                                                                         \
+    hipLaunchKernelGGL((gemm_kernel<TBV, SWV, NWV, 4>), grid, dim3(NWV * 64), 0, st, a);          \
+  else                                                                                            \
+    hipLaunchKernelGGL((gemm_kernel<TBV, SWV, NWV, 2>), grid, dim3(NWV * 64), 0, st, a);
   if (tb == 1) {
-    DSV2_GEMM(1)
+    if (swiglu) { DSV2_GEMM(1, true, 8) } else { DSV2_GEMM(1, false, 8) }
   } else if (tb == 2) {
-    DSV2_GEMM(2)
+    if (swiglu) { DSV2_GEMM(2, true, 8) } else { DSV2_GEMM(2, false, 8) }
+  } else if (tb == 4) {
+    if (swiglu) { DSV2_GEMM(4, true, 8) } else { DSV2_GEMM(4, false, 8) }
   } else {
-    DSV2_GEMM(4)
+    if (swiglu) { DSV2_GEMM(8, true, 4) } else { DSV2_GEMM(8, false, 8) }
   }
 #undef DSV2_GEMM
   return dsv2_launch_status("gemm");
 }
 
-static int pick_tb(int rows) { return rows <= 16 ? 1 : (rows <= 32 ? 2 : 4); }
+static int pick_tb(int rows) { return rows <= 16 ? 1 : (rows <= 32 ? 2 : (rows <= 64 ? 4 : 8)); }
 
 extern "C" int dsv2_gemm_bf16(const void* x, int64_t x_stride, int64_t x_gstride, int rows, int K, const void* W,
                               int64_t w_gstride, int N, int n_groups, const void* residual, int64_t res_stride,
                               void* y, int64_t y_stride, int64_t y_gstride, int flags, void* stream) {
   DSV2_REQUIRE(x && W && y, DSV2_E_NULL, "gemm: null pointer");
-  DSV2_REQUIRE(rows >= 0 && K > 0 && K % 32 == 0 && N > 0 && N % 64 == 0 && n_groups >= 1, DSV2_E_SHAPE,
-               "gemm: bad shape rows=%d K=%d N=%d groups=%d (K%%32, N%%64 required)", rows, K, N, n_groups);
+  DSV2_REQUIRE(rows >= 0 && K > 0 && K % 64 == 0 && N > 0 && N % 16 == 0 && n_groups >= 1, DSV2_E_SHAPE,
+               "gemm: bad shape rows=%d K=%d N=%d groups=%d (K%%64, N%%16 required)", rows, K, N, n_groups);
   DSV2_REQUIRE((flags & ~(DSV2_LINEAR_SWIGLU | DSV2_LINEAR_OUT_F32)) == 0, DSV2_E_FLAGS, "gemm: unknown flags");
   DSV2_REQUIRE(!(residual && ((flags & DSV2_LINEAR_SWIGLU) || n_groups != 1)), DSV2_E_FLAGS,
                "gemm: residual needs a plain single-group GEMM");
@@ -191,9 +208,9 @@ extern "C" int dsv2_moe_grouped_gateup(const void* xn, const int32_t* sorted_rou
                                        int inter, void* hsorted, void* stream) {
   DSV2_REQUIRE(xn && sorted_routes && tiles && num_tiles && w_gate_up && hsorted, DSV2_E_NULL,
                "moe_grouped_gateup: null pointer");
-  DSV2_REQUIRE(max_tiles >= 0 && max_tiles <= 65535 && inter > 0 && inter % 64 == 0 &&
+  DSV2_REQUIRE(max_tiles >= 0 && max_tiles <= 65535 && inter > 0 && inter % 16 == 0 &&
                    (tile_tokens == 16 || tile_tokens == 32 || tile_tokens == 64),
-               DSV2_E_SHAPE, "moe_grouped_gateup: bad shape (inter %% 64, tile_tokens in {16,32,64})");
+               DSV2_E_SHAPE, "moe_grouped_gateup: bad shape (inter %% 16, tile_tokens in {16,32,64})");
   DSV2_REQUIRE(dsv2_aligned16(xn) && dsv2_aligned16(w_gate_up) && dsv2_aligned16(tiles), DSV2_E_ALIGN,
                "moe_grouped_gateup: alignment");
   if (max_tiles == 0) return DSV2_OK;
@@ -219,7 +236,7 @@ extern "C" int dsv2_moe_grouped_down(const void* hsorted, const int32_t* tiles, 
                                      int max_tiles, int tile_tokens, const void* w_down, int inter, void* ysorted,
                                      void* stream) {
   DSV2_REQUIRE(hsorted && tiles && num_tiles && w_down && ysorted, DSV2_E_NULL, "moe_grouped_down: null pointer");
-  DSV2_REQUIRE(max_tiles >= 0 && max_tiles <= 65535 && inter > 0 && inter % 32 == 0 &&
+  DSV2_REQUIRE(max_tiles >= 0 && max_tiles <= 65535 && inter > 0 && inter % 64 == 0 &&
                    (tile_tokens == 16 || tile_tokens == 32 || tile_tokens == 64),
                DSV2_E_SHAPE, "moe_grouped_down: bad shape");
   DSV2_REQUIRE(dsv2_aligned16(hsorted) && dsv2_aligned16(w_down) && dsv2_aligned16(tiles) && inter % 8 == 0,

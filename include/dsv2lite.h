@@ -99,7 +99,7 @@ int dsv2_gemv_bf16(const void* x, int64_t x_stride, int rows, int K, const void*
  *   for group g < n_groups, row r < rows:
  *     Y[g*y_gstride + r*y_stride + n] = x[g*x_gstride + r*x_stride, :] . W[g*w_gstride + n*K, :]
  * Same flags/residual semantics as dsv2_gemv_bf16 (residual only with n_groups == 1).
- * K % 32 == 0, N % 64 == 0.  Replaces _batched_linear_kernel
+ * K % 64 == 0, N % 16 == 0.  Replaces _batched_linear_kernel
  * (triton_kernels/attention_decode_batch.py:421-468) and cuBLAS F.linear at batch sizes. */
 int dsv2_gemm_bf16(const void* x, int64_t x_stride, int64_t x_gstride, int rows, int K, const void* W,
                    int64_t w_gstride, int N, int n_groups, const void* residual, int64_t res_stride, void* y,

@@ -90,7 +90,7 @@ def test_gemv(rows, mode):
     assert rel_err(y.float(), ref) < 1e-2
 
 
-@pytest.mark.parametrize("rows", [1, 16, 37, 64, 256])
+@pytest.mark.parametrize("rows", [1, 16, 37, 64, 200, 256])
 @pytest.mark.parametrize("mode", ["plain", "swiglu", "residual", "f32"])
 def test_gemm_dense(rows, mode):
     K, N = 2048, 384
@@ -108,6 +108,23 @@ def test_gemm_dense(rows, mode):
         ref = rb(res.float() + rb(acc))
     else:
         ref = rb(acc)
+    assert rel_err(y.float(), ref) < 1e-2
+
+
+@pytest.mark.parametrize("rows", [5, 100])
+@pytest.mark.parametrize("K,N,swiglu", [(128, 512, False), (1408, 2048, False), (2816, 2048, False), (10944, 2048, False),
+                                        (2048, 1408, True), (512, 128, False), (2048, 102400, False),
+                                        (2048, 65536, True), (1408, 65536, False)])
+def test_gemm_k_split_shapes(rows, K, N, swiglu):
+    """Every K of the model (uneven per-wave k ranges, multi-batch ranges, one-wave K), and
+    output widths large enough for the streaming launch shape (lm_head-sized)."""
+    x = rnd(rows, K, seed=K + rows)
+    W = rnd(2 * N if swiglu else N, K, std=0.02, seed=K + 1)
+    y = torch.empty(rows, N, dtype=BF, device=DEV)
+    call("dsv2_gemm_bf16", x.data_ptr(), K, 0, rows, K, W.data_ptr(), 0, N, 1, None, 0, y.data_ptr(), N, 0,
+         LINEAR_SWIGLU if swiglu else 0, st())
+    acc = x.float() @ W.float().t()
+    ref = rb(rb(torch.nn.functional.silu(rb(acc[:, :N]))) * rb(acc[:, N:])) if swiglu else rb(acc)
     assert rel_err(y.float(), ref) < 1e-2
 
 
@@ -409,7 +426,7 @@ def test_embed_gather_and_api_errors():
     assert torch.equal(out, table[ids])
     with pytest.raises(_hip.HipKernelError, match="multiple of 8"):
         call("dsv2_residual_add_bf16", table.data_ptr(), table.data_ptr(), out.data_ptr(), 13, st())
-    with pytest.raises(_hip.HipKernelError, match="K%32"):
+    with pytest.raises(_hip.HipKernelError, match="K%64"):
         call("dsv2_gemm_bf16", table.data_ptr(), 2048, 0, 3, 2000, table.data_ptr(), 0, 64, 1, None, 0,
              out.data_ptr(), 2048, 0, 0, st())
 
