@@ -165,6 +165,8 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=1, choices=sorted(CONFIGS))
     ap.add_argument("--family", choices=("small", "batch"), default=None)
+    ap.add_argument("--mla-path", choices=("fused", "split"), default="fused",
+                    help="small family: one fused MLA kernel per layer, or prepare + split-KV decode + combine")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 3 plain 512 MiB device copies (the reference kernel for scaling the "
@@ -192,7 +194,7 @@ def main() -> None:
     prompts = [torch.randint(0, cfg.vocab, (n,), generator=g) for n in lens]
     steps, warm = args.steps, args.warmup
     caps = [n + steps + warm + 8 for n in lens]
-    eng = dsv2lite.DecodeEngine(w, caps, family=family)
+    eng = dsv2lite.DecodeEngine(w, caps, family=family, mla_path=args.mla_path)
     t0 = time.perf_counter()
     eng.prefill([p.to(dev) for p in prompts])
     torch.cuda.synchronize()
@@ -231,6 +233,7 @@ def main() -> None:
         "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16", "data": "synthetic: random-init weights N(0,0.02) seed 0, uniform random prompt ids",
         "config": {"workload": spec["workload"], "global_batch": B, "seq_len": max(lens), "kernel_family": family,
+                   "mla_path": args.mla_path if family == "small" else "split",
                    "prompt_tokens": sum(lens), "parallelism": "none (1 GPU)"},
         "roofline": roof,
         "step_roofline": {"bytes_per_step": sb, "achieved_GBps": sb / (ms / 1e3) / 1e9,

@@ -14,7 +14,8 @@ __global__ __launch_bounds__(256) void gemv_k2048_kernel(const bf16_t* __restric
                                                          const bf16_t* __restrict__ W, int N,
                                                          const bf16_t* __restrict__ nw, float eps,
                                                          const bf16_t* __restrict__ res, int64_t rs,
-                                                         void* __restrict__ y, int64_t ys, bool out_f32) {
+                                                         void* __restrict__ y, int64_t ys, bool out_f32,
+                                                         float* __restrict__ amax) {
   constexpr int U = 4;
   __shared__ float xl[NB][2048];
   __shared__ float red[NB][4];
@@ -82,6 +83,15 @@ __global__ __launch_bounds__(256) void gemv_k2048_kernel(const bf16_t* __restric
     __syncthreads();
   }
 
+  // amax != null (fp32 logits): per wave and row, the first index of the largest output
+  // (rows are visited in increasing order, so a strict > keeps the lowest index)
+  float best[NB];
+  int bidx[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    best[b] = -INFINITY;
+    bidx[b] = 0x7fffffff;
+  }
   while (g < ngroups) {
     const int n0 = g * RPW;
     float rv[RPW][NB];
@@ -136,9 +146,109 @@ __global__ __launch_bounds__(256) void gemv_k2048_kernel(const bf16_t* __restric
             reinterpret_cast<float*>(y)[b * ys + n] = v;
           else
             reinterpret_cast<bf16_t*>(y)[b * ys + n] = f2bf(v);
+          if (v > best[b]) {
+            best[b] = v;
+            bidx[b] = n;
+          }
         }
       }
     }
+  }
+  if (amax && lane == 0) {
+    const int nw = gridDim.x * 4, gw = blockIdx.x * 4 + wv;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      if (b >= B) break;
+      amax[2 * (b * nw + gw)] = best[b];
+      reinterpret_cast<int*>(amax)[2 * (b * nw + gw) + 1] = bidx[b];
+    }
+  }
+}
+
+// One row (bsz = 1), K = 2048: one-shot launch, one wave per RPW output rows (plus the RPW
+// matching up rows for SwiGLU), so the grid is N / (4 RPW) workgroups.  Each wave loads x
+// itself from L2/L1 while its weight rows are in flight -- no LDS staging, no barrier.
+// (Used without a norm prologue: with one, the per-wave RMSNorm measured slower on MI355X
+// than the workgroup-shared norm of gemv_k2048_kernel.)
+template <int RPW, bool SW, bool NORM>
+__global__ __launch_bounds__(256) void gemv_b1_kernel(const bf16_t* __restrict__ x, const bf16_t* __restrict__ W, int N,
+                                                      const bf16_t* __restrict__ nw, float eps,
+                                                      const bf16_t* __restrict__ res, void* __restrict__ y,
+                                                      bool out_f32) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int n0 = (blockIdx.x * 4 + wv) * RPW;
+  if (n0 >= N) return;
+  uint4 wg[RPW][4], wu[RPW][4];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      wg[r][j] = ldg16(W + (int64_t)(n0 + r) * 2048 + (lane + 64 * j) * 8);
+      if (SW) wu[r][j] = ldg16(W + (int64_t)(N + n0 + r) * 2048 + (lane + 64 * j) * 8);
+    }
+  float rv[RPW];
+  if (res && lane == 0) {
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) rv[r] = bf2f(res[n0 + r]);
+  }
+  float xf[32];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) unpack8(ldg16(x + (lane + 64 * j) * 8), xf + 8 * j);
+  if (NORM) {
+    float g8[32];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) unpack8(ldg16(nw + (lane + 64 * j) * 8), g8 + 8 * j);
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) ss = __builtin_fmaf(xf[i], xf[i], ss);
+    ss = wave_sum(ss);
+    const float rs = rsqrtf(ss / 2048.f + eps);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) xf[i] = rbf(g8[i] * rbf(xf[i] * rs));
+  }
+  float ag[RPW], au[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    ag[r] = au[r] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      ag[r] += dot8(wg[r][j], xf + 8 * j);
+      if (SW) au[r] += dot8(wu[r][j], xf + 8 * j);
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1)
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      ag[r] += __shfl_xor(ag[r], off, 64);
+      if (SW) au[r] += __shfl_xor(au[r], off, 64);
+    }
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      float v = SW ? swiglu_bf(ag[r], au[r]) : rbf(ag[r]);
+      if (res) v = rbf(rv[r] + v);
+      if (out_f32)
+        reinterpret_cast<float*>(y)[n0 + r] = v;
+      else
+        reinterpret_cast<bf16_t*>(y)[n0 + r] = f2bf(v);
+    }
+  }
+}
+
+static void launch_b1(const bf16_t* x, const bf16_t* W, int N, const bf16_t* nw, float eps, const bf16_t* res, void* y,
+                      bool sw, bool f32, hipStream_t st) {
+  const dim3 grid((N + 3) / 4);
+  if (sw) {
+    if (nw)
+      hipLaunchKernelGGL((gemv_b1_kernel<1, true, true>), grid, dim3(256), 0, st, x, W, N, nw, eps, res, y, f32);
+    else
+      hipLaunchKernelGGL((gemv_b1_kernel<1, true, false>), grid, dim3(256), 0, st, x, W, N, nw, eps, res, y, f32);
+  } else {
+    if (nw)
+      hipLaunchKernelGGL((gemv_b1_kernel<1, false, true>), grid, dim3(256), 0, st, x, W, N, nw, eps, res, y, f32);
+    else
+      hipLaunchKernelGGL((gemv_b1_kernel<1, false, false>), grid, dim3(256), 0, st, x, W, N, nw, eps, res, y, f32);
   }
 }
 
@@ -215,14 +325,18 @@ __global__ __launch_bounds__(256) void gemv_klong_kernel(const bf16_t* __restric
   }
 }
 
+static int k2048_grid(int N, int RPW) {
+  const int groups = N / RPW;
+  const int grid = (groups + 3) / 4;
+  return grid > 1024 ? 1024 : grid;  // grid-stride beyond 4 workgroups per CU
+}
+
 template <int NB, int RPW, bool SW>
 static void launch_k2048(const bf16_t* x, int64_t xs, int B, int K, const bf16_t* W, int N, const bf16_t* nw,
-                         float eps, const bf16_t* res, int64_t rs, void* y, int64_t ys, bool f32, hipStream_t st) {
-  const int groups = N / RPW;
-  int grid = (groups + 3) / 4;
-  if (grid > 1024) grid = 1024;  // grid-stride beyond 4 workgroups per CU
-  hipLaunchKernelGGL((gemv_k2048_kernel<NB, RPW, SW>), dim3(grid), dim3(256), 0, st, x, xs, B, K, W, N, nw, eps, res,
-                     rs, y, ys, f32);
+                         float eps, const bf16_t* res, int64_t rs, void* y, int64_t ys, bool f32, hipStream_t st,
+                         float* amax = nullptr) {
+  hipLaunchKernelGGL((gemv_k2048_kernel<NB, RPW, SW>), dim3(k2048_grid(N, RPW)), dim3(256), 0, st, x, xs, B, K, W, N,
+                     nw, eps, res, rs, y, ys, f32, amax);
 }
 
 template <int NB>
@@ -263,6 +377,10 @@ extern "C" int dsv2_gemv_bf16(const void* x, int64_t x_stride, int rows, int K, 
   DSV2_REQUIRE(K <= 2048 || (!norm_w && !sw), DSV2_E_FLAGS, "gemv: K > 2048 supports neither norm nor SwiGLU");
   hipStream_t st = (hipStream_t)stream;
   const bf16_t* xb = (const bf16_t*)x;
+  if (rows == 1 && K == 2048 && !norm_w) {
+    launch_b1(xb, (const bf16_t*)W, N, (const bf16_t*)norm_w, eps, (const bf16_t*)residual, y, sw, f32, st);
+    return dsv2_launch_status("gemv");
+  }
   for (int r0 = 0; r0 < rows; r0 += 8) {
     const int B = rows - r0 < 8 ? rows - r0 : 8;
     const bf16_t* xr = xb + r0 * x_stride;
@@ -282,4 +400,86 @@ extern "C" int dsv2_gemv_bf16(const void* x, int64_t x_stride, int rows, int K, 
     if (rc) return rc;
   }
   return DSV2_OK;
+}
+
+// ---------------------------------------------------------------------------
+// lm_head + greedy argmax: the GEMV records each wave's (max, first index) while it
+// writes the fp32 logits, then one workgroup per row reduces the per-wave partials
+// (a few KB instead of the whole vocabulary row).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void argmax_partials_kernel(const float* __restrict__ amax, int nw,
+                                                              int64_t* __restrict__ next_ids, int32_t* __restrict__ pos) {
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  const int b = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  float best = -INFINITY;
+  int bi = 0x7fffffff;
+  // nw <= 4096: every thread requests its (up to) 16 partials before comparing any
+  float2 pv[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int i = threadIdx.x + 256 * k;
+    pv[k] = i < nw ? reinterpret_cast<const float2*>(amax)[b * nw + i] : make_float2(-INFINITY, 0.f);
+  }
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const float v = pv[k].x;
+    const int ix = __float_as_int(pv[k].y);
+    if (threadIdx.x + 256 * k < nw && (v > best || (v == best && ix < bi))) {
+      best = v;
+      bi = ix;
+    }
+  }
+  wave_argmax(best, bi);
+  if (lane == 0) {
+    sv[w] = best;
+    si[w] = bi;
+  }
+  __syncthreads();
+  if (w == 0) {
+    best = lane < 4 ? sv[lane] : -INFINITY;
+    bi = lane < 4 ? si[lane] : 0x7fffffff;
+    wave_argmax(best, bi);
+    if (lane == 0) {
+      next_ids[b] = bi == 0x7fffffff ? 0 : bi;
+      if (pos) pos[b] += 1;
+    }
+  }
+}
+
+extern "C" int64_t dsv2_lm_head_argmax_workspace_size(int rows) {
+  return rows < 0 ? -1 : (int64_t)rows * 1024 * 4 * 8;
+}
+
+extern "C" int dsv2_lm_head_argmax_bf16(const void* x, int64_t x_stride, int rows, const void* W, int vocab,
+                                        const void* norm_w, float eps, float* logits, void* partials,
+                                        int64_t partials_bytes, int64_t* next_ids, int32_t* pos, void* stream) {
+  DSV2_REQUIRE(x && W && norm_w && logits && partials && next_ids, DSV2_E_NULL, "lm_head_argmax: null pointer");
+  DSV2_REQUIRE(rows >= 1 && rows <= 8 && vocab > 0 && vocab % 2 == 0, DSV2_E_SHAPE,
+               "lm_head_argmax: 1 <= rows <= 8 and an even vocabulary required (rows %d, vocab %d)", rows, vocab);
+  DSV2_REQUIRE(partials_bytes >= dsv2_lm_head_argmax_workspace_size(rows), DSV2_E_SHAPE,
+               "lm_head_argmax: partials buffer too small");
+  DSV2_REQUIRE(dsv2_aligned16(x) && dsv2_aligned16(W) && dsv2_aligned16(norm_w) && x_stride % 8 == 0, DSV2_E_ALIGN,
+               "lm_head_argmax: alignment");
+  hipStream_t st = (hipStream_t)stream;
+  const bf16_t* xb = (const bf16_t*)x;
+  float* amax = (float*)partials;
+  constexpr int RPW = 2;
+  if (rows == 1)
+    launch_k2048<1, RPW, false>(xb, x_stride, rows, 2048, (const bf16_t*)W, vocab, (const bf16_t*)norm_w, eps,
+                                nullptr, 0, logits, vocab, true, st, amax);
+  else if (rows == 2)
+    launch_k2048<2, RPW, false>(xb, x_stride, rows, 2048, (const bf16_t*)W, vocab, (const bf16_t*)norm_w, eps,
+                                nullptr, 0, logits, vocab, true, st, amax);
+  else if (rows <= 4)
+    launch_k2048<4, RPW, false>(xb, x_stride, rows, 2048, (const bf16_t*)W, vocab, (const bf16_t*)norm_w, eps,
+                                nullptr, 0, logits, vocab, true, st, amax);
+  else
+    launch_k2048<8, RPW, false>(xb, x_stride, rows, 2048, (const bf16_t*)W, vocab, (const bf16_t*)norm_w, eps,
+                                nullptr, 0, logits, vocab, true, st, amax);
+  int rc = dsv2_launch_status("lm_head_argmax");
+  if (rc) return rc;
+  hipLaunchKernelGGL(argmax_partials_kernel, dim3(rows), dim3(256), 0, st, amax, k2048_grid(vocab, RPW) * 4, next_ids,
+                     pos);
+  return dsv2_launch_status("lm_head_argmax");
 }

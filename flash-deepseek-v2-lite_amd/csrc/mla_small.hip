@@ -2,7 +2,7 @@
 // workgroup per (row, head) does the whole head:
 //   1. q_lat_h = W_UK_h^T q_nope_h        (16 lanes per output, all loads in flight)
 //   2. new cache row (kv-norm + RoPE(k_pe)) into LDS; the h == 0 workgroup stores it
-//   3. RoPE(q_pe_h); per-wave online softmax over 8-token batches of the cached rows
+//   3. RoPE(q_pe_h); per-wave online softmax over 4-token batches of the cached rows
 //      (one 16-byte load per lane serves both q.k and p.v), the new token from LDS
 //   4. log-sum-exp merge of the 16 waves -> o_lat_h (fp32)
 //   5. attn[row, h*128 + i] = W_UV_h o_lat_h
@@ -10,7 +10,7 @@
 #include "common.h"
 
 namespace {
-constexpr int kRow = 576, kLat = 512, kWaves = 16, kBatch = 8;
+constexpr int kRow = 576, kLat = 512, kWaves = 16, kBatch = 4;
 }
 
 __global__ __launch_bounds__(1024) void mla_fused_kernel(const bf16_t* __restrict__ qkva, int64_t qs,
@@ -33,6 +33,15 @@ __global__ __launch_bounds__(1024) void mla_fused_kernel(const bf16_t* __restric
   const int pc = p < 0 ? 0 : (p >= max_pos ? max_pos - 1 : p);
   const bf16_t* cs = cosT + (int64_t)pc * 64;
   const bf16_t* sn = sinT + (int64_t)pc * 64;
+
+  // W_UV rows of step 5 (wave wv: rows wv*8 .. wv*8+7 of head h) are requested first: they
+  // depend on nothing, so their HBM latency overlaps steps 1-4
+  uint4 wuv[8];
+  {
+    const bf16_t* wp = w_uv + ((int64_t)h * 128 + wv * 8) * kLat + lane * 8;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) wuv[r] = ldg16(wp + (int64_t)r * kLat);
+  }
 
   // 1. absorption: row j = u*64 + gi of W_UKT_h (K = 128 split over 16 lanes)
   {
@@ -181,13 +190,9 @@ __global__ __launch_bounds__(1024) void mla_fused_kernel(const bf16_t* __restric
   float xo[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) xo[i] = olat[lane * 8 + i];
-  const bf16_t* wp = w_uv + ((int64_t)h * 128 + wv * 8) * kLat + lane * 8;
-  uint4 wr[8];
-#pragma unroll
-  for (int r = 0; r < 8; ++r) wr[r] = ldg16(wp + (int64_t)r * kLat);
   float rr[8];
 #pragma unroll
-  for (int r = 0; r < 8; ++r) rr[r] = dot8(wr[r], xo);
+  for (int r = 0; r < 8; ++r) rr[r] = dot8(wuv[r], xo);
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1)
 #pragma unroll

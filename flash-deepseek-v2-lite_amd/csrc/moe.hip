@@ -7,6 +7,8 @@ namespace {
 constexpr int kH = 2048;
 constexpr int kE = 64;
 constexpr int kTopK = 6;
+// gate_up rows per wave (gate + up each); 2 measured faster than 1 on MI355X
+constexpr int kGateRPW = 2;
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -342,7 +344,7 @@ __device__ __forceinline__ void moe_gate_body(const MoeGateArgs& a, int v, float
   }
   v -= a.n_router;
   if (v < a.n_gate) {
-    route_gateup_block<2>(v % a.gu_blocks, v / a.gu_blocks, a.xn, a.ids, a.nr, a.s_off, a.hbuf_routes, a.logits_in,
+    route_gateup_block<kGateRPW>(v % a.gu_blocks, v / a.gu_blocks, a.xn, a.ids, a.nr, a.s_off, a.hbuf_routes, a.logits_in,
                           a.scaling, a.wts, a.gate_h, a.hs, a.nw, a.eps, a.wgu, a.shgu, a.inter, a.hbuf);
     return;
   }
@@ -404,7 +406,7 @@ extern "C" int dsv2_moe_route_gateup(const void* xn, int rows, const int32_t* id
   DSV2_REQUIRE(dsv2_aligned16(xn) && dsv2_aligned16(w_gate_up) && (!sh_gate_up || dsv2_aligned16(sh_gate_up)),
                DSV2_E_ALIGN, "moe_route_gateup: alignment");
   if (rows == 0) return DSV2_OK;
-  constexpr int RPW = 2;
+  constexpr int RPW = kGateRPW;
   MoeGateArgs a{};
   a.gu_blocks = (inter + 4 * RPW - 1) / (4 * RPW);
   a.n_gate = rows * nr * a.gu_blocks;
@@ -433,7 +435,7 @@ extern "C" int dsv2_moe_route_gateup_logits(const void* xn, int rows, const floa
   DSV2_REQUIRE(dsv2_aligned16(xn) && dsv2_aligned16(w_gate_up) && (!sh_gate_up || dsv2_aligned16(sh_gate_up)),
                DSV2_E_ALIGN, "moe_route_gateup_logits: alignment");
   if (rows == 0) return DSV2_OK;
-  constexpr int RPW = 2;
+  constexpr int RPW = kGateRPW;
   MoeGateArgs a{};
   a.gu_blocks = (inter + 4 * RPW - 1) / (4 * RPW);
   a.n_gate = rows * nr * a.gu_blocks;

@@ -109,6 +109,8 @@ class DecodeEngine:
         self.ids = torch.zeros(self.B, dtype=torch.int64, device=device)
         self.logits = torch.empty(self.B, cfg.vocab, dtype=torch.float32, device=device)
         self.buf = RowBuffers(cfg, self.B, family, self.max_pos, device)
+        self._amax = torch.empty(max(0, _hip.lib.dsv2_lm_head_argmax_workspace_size(min(self.B, 8))),
+                                 dtype=torch.uint8, device=device)
         # small family: one fused workgroup per (row, head) while contexts are short; the
         # split-KV kernel (parallel over the context) takes over for long contexts
         self.fused_mla = family == "small" and self.max_pos <= FUSED_MLA_MAX_CTX and mla_path == "fused"
@@ -221,6 +223,10 @@ class DecodeEngine:
     def _head(self, b: RowBuffers, family: str, st: int, pos) -> None:
         c = self.cfg
         B = self.B
+        if family == "small" and B <= 8:
+            call("dsv2_lm_head_argmax_bf16", ptr(b.h), c.hidden, B, ptr(self.w.lm_head), c.vocab, ptr(self.w.norm),
+                 c.eps, ptr(self.logits), ptr(self._amax), self._amax.numel(), ptr(self.ids), ptr(pos), st)
+            return
         if family == "small":
             call("dsv2_gemv_bf16", ptr(b.h), c.hidden, B, c.hidden, ptr(self.w.lm_head), c.vocab, ptr(self.w.norm),
                  c.eps, None, 0, ptr(self.logits), c.vocab, LINEAR_OUT_F32, st)

@@ -95,6 +95,18 @@ int dsv2_gemv_bf16(const void* x, int64_t x_stride, int rows, int K, const void*
                    const void* norm_w, float eps, const void* residual, int64_t res_stride, void* y,
                    int64_t y_stride, int flags, void* stream);
 
+/* Final RMSNorm + lm_head + greedy argmax for 1..8 rows (hidden 2048):
+ *   logits[r, v] = fp32(bf16(RMSNorm(x[r]; norm_w) . W[v, :]))   (W [vocab, 2048], vocab even)
+ *   next_ids[r] = first index of the row maximum;  pos[r] += 1 when pos != NULL.
+ * The GEMV leaves each wave's (max, first index) in `partials` (caller-owned, at least
+ * dsv2_lm_head_argmax_workspace_size(rows) bytes) and a one-workgroup-per-row kernel
+ * reduces them.  Replaces lm_head + .float() + _greedy_decode + cache_position.add_(1)
+ * (src/run.py:252-253, 585-588). */
+int64_t dsv2_lm_head_argmax_workspace_size(int rows);
+int dsv2_lm_head_argmax_bf16(const void* x, int64_t x_stride, int rows, const void* W, int vocab, const void* norm_w,
+                             float eps, float* logits, void* partials, int64_t partials_bytes, int64_t* next_ids,
+                             int32_t* pos, void* stream);
+
 /* Grouped bf16 MFMA GEMM (v_mfma_f32_16x16x32_bf16), fp32 accumulation:
  *   for group g < n_groups, row r < rows:
  *     Y[g*y_gstride + r*y_stride + n] = x[g*x_gstride + r*x_stride, :] . W[g*w_gstride + n*K, :]

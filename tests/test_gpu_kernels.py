@@ -505,3 +505,32 @@ def test_router_logits_split_and_gateup_topk(rows):
     call("dsv2_moe_route_gateup", xn.data_ptr(), rows, ids.data_ptr(), gu.data_ptr(), sgu.data_ptr(), 1408,
          hb2.data_ptr(), st())
     assert torch.equal(hb, hb2)
+
+
+@pytest.mark.parametrize("rows", [1, 2, 5])
+def test_lm_head_argmax_matches_gemv_then_argmax(rows):
+    x = rnd(rows, 2048, seed=99)
+    W = rnd(102400, 2048, std=0.02, seed=100)
+    nw = rnd(2048, seed=101, std=0.1) + 1.0
+    W[77] = W[4000]  # a planted tie between two vocabulary rows: the lower index must win
+    lg = torch.empty(rows, 102400, dtype=torch.float32, device=DEV)
+    ids = torch.empty(rows, dtype=torch.int64, device=DEV)
+    pos = torch.arange(rows, dtype=torch.int32, device=DEV)
+    part = torch.empty(_hip.lib.dsv2_lm_head_argmax_workspace_size(rows), dtype=torch.uint8, device=DEV)
+    call("dsv2_lm_head_argmax_bf16", x.data_ptr(), 2048, rows, W.data_ptr(), 102400, nw.data_ptr(), 1e-6,
+         lg.data_ptr(), part.data_ptr(), part.numel(), ids.data_ptr(), pos.data_ptr(), st())
+    lg2 = torch.empty_like(lg)
+    call("dsv2_gemv_bf16", x.data_ptr(), 2048, rows, 2048, W.data_ptr(), 102400, nw.data_ptr(), 1e-6, None, 0,
+         lg2.data_ptr(), 102400, LINEAR_OUT_F32, st())
+    assert torch.equal(lg, lg2)
+    assert torch.equal(ids.cpu(), torch.argmax(lg.cpu(), -1))  # torch: first index of the maximum
+    assert pos.tolist() == list(range(1, rows + 1))
+    # force the tie to be the maximum of row 0 and check the lower index is returned
+    x0 = torch.zeros(rows, 2048, dtype=BF, device=DEV)
+    x0[:, :] = W[77].float().sign().to(BF)
+    call("dsv2_lm_head_argmax_bf16", x0.data_ptr(), 2048, rows, W.data_ptr(), 102400, nw.data_ptr(), 1e-6,
+         lg.data_ptr(), part.data_ptr(), part.numel(), ids.data_ptr(), None, st())
+    assert torch.equal(ids.cpu(), torch.argmax(lg.cpu(), -1))
+    with pytest.raises(_hip.HipKernelError, match="rows"):
+        call("dsv2_lm_head_argmax_bf16", x.data_ptr(), 2048, 9, W.data_ptr(), 102400, nw.data_ptr(), 1e-6,
+             lg.data_ptr(), part.data_ptr(), part.numel(), ids.data_ptr(), None, st())
