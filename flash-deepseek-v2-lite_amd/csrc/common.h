@@ -66,6 +66,13 @@ __device__ __forceinline__ uint4 pack8(const float* f) {
 
 __device__ __forceinline__ uint4 ldg16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 
+// v if ok else 0, component-wise (a `?:` between two uint4 values is lowered through
+// scratch memory; a mask keeps it in registers)
+__device__ __forceinline__ uint4 keep_if(bool ok, const uint4& v) {
+  const uint32_t m = ok ? 0xffffffffu : 0u;
+  return make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
+}
+
 __device__ __forceinline__ float dot8(const uint4& w, const float* x) {
   float f[8];
   unpack8(w, f);

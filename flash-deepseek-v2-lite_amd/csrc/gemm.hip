@@ -134,11 +134,199 @@ __global__ __launch_bounds__(NW * 64) void gemm_kernel(const GemmArgs a) {
   }
 }
 
+// Token-rows-in-LDS shape (used when the launch has enough tiles): a workgroup owns 64
+// weight rows (SwiGLU: 32 features = 32 gate + 32 up rows) of the tile, 8 waves = NRB
+// feature blocks x NKQ contiguous k ranges.  Per chunk of CS 32-wide steps the tile's
+// token rows are loaded once, with coalesced 16-byte loads, into LDS (double-buffered)
+// and every wave takes its MFMA B fragments from there, so token traffic from L2 is one
+// pass per 64 weight rows instead of one per 16.  Weight fragments stream straight from
+// HBM, the next chunk's requested before the current one is multiplied.  Steps past K
+// and token rows past the tile load clamped addresses and are zeroed, so every load is
+// unconditional.  The NKQ partial tiles are summed through LDS in a fixed order.
+template <int TB, bool SWIGLU, int CS>
+__global__ __launch_bounds__(512) void gemm_xlds_kernel(const GemmArgs a) {
+  constexpr int R = SWIGLU ? 2 : 1;    // row blocks per wave (gate, up)
+  constexpr int NRB = SWIGLU ? 2 : 4;  // feature blocks of 16 per workgroup
+  constexpr int NKQ = 8 / NRB;         // k ranges
+  constexpr int TOK = 16 * TB;
+  constexpr int XROW = CS * 32 + 8;  // LDS row in elements (+16 B pad: conflict-free B reads)
+  constexpr int XBUF = NKQ * TOK * XROW;
+  constexpr int RED = (NKQ - 1) * NRB * R * TB * 64 * 4;  // floats
+  constexpr int LDS_BYTES = (2 * XBUF * 2 > RED * 4) ? 2 * XBUF * 2 : RED * 4;
+  constexpr int UNITS = NKQ * TOK * CS * 4;  // 16-byte X units per chunk
+  constexpr int UPT = UNITS / 512;
+  static_assert(UNITS % 512 == 0, "X units must split evenly over the workgroup");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[LDS_BYTES];
+  bf16_t* xbuf = reinterpret_cast<bf16_t*>(lds);
+  floatx4_t* red = reinterpret_cast<floatx4_t*>(lds);
+
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int rb = wv % NRB, kq = wv / NRB;
+  const int li = lane & 15, kg = lane >> 4;
+  int g, start, count;
+  if (a.tiles) {
+    if ((int)blockIdx.y >= a.ntiles[0]) return;
+    const int4 t = reinterpret_cast<const int4*>(a.tiles)[blockIdx.y];
+    g = t.x;
+    start = t.y;
+    count = t.z;
+  } else {
+    g = blockIdx.y / a.tiles_per_group;
+    start = (blockIdx.y % a.tiles_per_group) * TOK;
+    count = min(TOK, a.rows - start);
+  }
+  const int K = a.K, S = K >> 5;
+  const int SP = ((S + NKQ - 1) / NKQ + CS - 1) / CS * CS;  // steps per k range (CS multiple)
+  const int nch = SP / CS;
+  const int f0 = blockIdx.x * 16 * NRB + rb * 16;
+  const bf16_t* wrow[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) wrow[r] = a.W + g * a.wg + (int64_t)(f0 + r * a.N + li) * K + kg * 8;
+
+  // this thread's X units: fixed (range, token, 16-byte part) for every chunk
+  const bf16_t* xsrc[UPT];
+  int xkq[UPT], xpart[UPT], xdst[UPT];
+  bool xok[UPT];
+#pragma unroll
+  for (int j = 0; j < UPT; ++j) {
+    const int u = tid + 512 * j;
+    const int uk = u / (TOK * CS * 4), rem = u % (TOK * CS * 4);
+    const int tok = rem / (CS * 4), part = rem % (CS * 4);
+    const int tk = tok < count ? tok : 0;
+    const int row = a.slot_row ? a.slot_row[start + tk] / a.slot_div : start + tk;
+    xsrc[j] = a.X + g * a.xg + (int64_t)row * a.xs + (part & 3) * 8;
+    xkq[j] = uk;
+    xpart[j] = part;
+    xok[j] = tok < count;
+    xdst[j] = (uk * TOK + tok) * XROW + (part >> 2) * 32 + (part & 3) * 8;
+  }
+  // chunk c of X (this thread's units) into registers / of this wave's weight fragments
+#define XL_LOAD_X(c)                                                             \
+  _Pragma("unroll") for (int j = 0; j < UPT; ++j) {                              \
+    const int step_ = xkq[j] * SP + (c) * CS + (xpart[j] >> 2);                  \
+    const uint4 v_ = ldg16(xsrc[j] + (int64_t)min(step_, S - 1) * 32);           \
+    xr[j] = keep_if(xok[j] && step_ < S, v_);                                    \
+  }
+#define XL_STORE_X(buf) \
+  _Pragma("unroll") for (int j = 0; j < UPT; ++j) *reinterpret_cast<uint4*>(xbuf + (buf) * XBUF + xdst[j]) = xr[j];
+#define XL_LOAD_A(c, av)                                                         \
+  _Pragma("unroll") for (int si = 0; si < CS; ++si) {                            \
+    const int step_ = kq * SP + (c) * CS + si;                                   \
+    _Pragma("unroll") for (int r = 0; r < R; ++r) {                              \
+      const uint4 v_ = ldg16(wrow[r] + (int64_t)min(step_, S - 1) * 32);         \
+      av[si][r] = keep_if(step_ < S, v_);                                        \
+    }                                                                            \
+  }
+
+  floatx4_t acc[R][TB];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) acc[r][tb] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+
+  uint4 a0[CS][R], a1[CS][R], xr[UPT];
+  XL_LOAD_A(0, a0)
+  XL_LOAD_X(0)
+  XL_STORE_X(0)
+  __syncthreads();
+  for (int c = 0; c < nch; ++c) {
+    const bool more = c + 1 < nch;
+    if (more) {
+      XL_LOAD_A(c + 1, a1)
+      XL_LOAD_X(c + 1)
+    }
+    const bf16_t* xb = xbuf + (c & 1) * XBUF + (kq * TOK + li) * XROW + kg * 8;
+#pragma unroll
+    for (int si = 0; si < CS; ++si)
+#pragma unroll
+      for (int tb = 0; tb < TB; ++tb) {
+        const bf16x8_t bfr = *reinterpret_cast<const bf16x8_t*>(xb + tb * 16 * XROW + si * 32);
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r][tb] = mfma16x16x32(as_bf16x8(a0[si][r]), bfr, acc[r][tb]);
+      }
+    if (more) {
+      XL_STORE_X((c + 1) & 1)
+    }
+    __syncthreads();
+#pragma unroll
+    for (int si = 0; si < CS; ++si)
+#pragma unroll
+      for (int r = 0; r < R; ++r) a0[si][r] = a1[si][r];
+  }
+
+#undef XL_LOAD_X
+#undef XL_STORE_X
+#undef XL_LOAD_A
+  // sum the k ranges in order 0, 1, ..., NKQ-1 (the X buffers are free after the last barrier)
+  if (kq > 0) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int tb = 0; tb < TB; ++tb) red[((((kq - 1) * NRB + rb) * R + r) * TB + tb) * 64 + lane] = acc[r][tb];
+  }
+  __syncthreads();
+  if (kq != 0) return;
+#pragma unroll
+  for (int q = 1; q < NKQ; ++q)
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int tb = 0; tb < TB; ++tb) acc[r][tb] += red[((((q - 1) * NRB + rb) * R + r) * TB + tb) * 64 + lane];
+#pragma unroll
+  for (int tb = 0; tb < TB; ++tb) {
+    if (tb * 16 + li >= count) continue;
+    const int slot = start + tb * 16 + li;
+    const int n = f0 + 4 * kg;
+    float v[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = SWIGLU ? swiglu_bf(acc[0][tb][e], acc[R - 1][tb][e]) : rbf(acc[0][tb][e]);
+    if (a.res) {
+      const uint2 r2 = *reinterpret_cast<const uint2*>(a.res + slot * a.rs + n);
+      v[0] = rbf(__uint_as_float(r2.x << 16) + v[0]);
+      v[1] = rbf(__uint_as_float(r2.x & 0xffff0000u) + v[1]);
+      v[2] = rbf(__uint_as_float(r2.y << 16) + v[2]);
+      v[3] = rbf(__uint_as_float(r2.y & 0xffff0000u) + v[3]);
+    }
+    const int64_t off = g * a.yg + (int64_t)slot * a.ys + n;
+    if (a.out_f32) {
+      *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.Y) + off) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+      uint2 o;
+      o.x = pack2(v[0], v[1]);
+      o.y = pack2(v[2], v[3]);
+      *reinterpret_cast<uint2*>(reinterpret_cast<bf16_t*>(a.Y) + off) = o;
+    }
+  }
+}
+
+// features per workgroup of gemm_xlds_kernel
+static int xlds_features(bool swiglu) { return swiglu ? 32 : 64; }
+
+static int launch_gemm_xlds(const GemmArgs& a, int tb, bool swiglu, int grid_y, hipStream_t st) {
+  const dim3 grid(a.N / xlds_features(swiglu), grid_y);
+#define DSV2_XL(TBV, SWV, CSV) hipLaunchKernelGGL((gemm_xlds_kernel<TBV, SWV, CSV>), grid, dim3(512), 0, st, a)
+  if (swiglu) {
+    if (tb == 1) DSV2_XL(1, true, 4);
+    else if (tb == 2) DSV2_XL(2, true, 4);
+    else DSV2_XL(4, true, 2);
+  } else {
+    if (tb == 1) DSV2_XL(1, false, 8);
+    else if (tb == 2) DSV2_XL(2, false, 8);
+    else if (tb == 4) DSV2_XL(4, false, 4);
+    else DSV2_XL(8, false, 2);
+  }
+#undef DSV2_XL
+  return dsv2_launch_status("gemm");
+}
+
 // Launch shape by token blocks: NW waves split K in batches of U steps (U = 4 when it
 // divides K/32, else 2).  The fp32 reduction buffer is NW*R*TB KB of LDS (<= 64 KB).
 // Token tiles are at most 128 (TB = 8): larger row counts run as several tiles (their
 // weights then come from L2 / Infinity Cache after the first).
 static int launch_gemm(const GemmArgs& a, int tb, bool swiglu, int grid_y, hipStream_t st) {
+  if ((a.tiles || (a.N % xlds_features(swiglu) == 0 && (int64_t)(a.N / xlds_features(swiglu)) * grid_y >= 512)) &&
+      !(swiglu && tb == 8))
+    return launch_gemm_xlds(a, tb, swiglu, grid_y, st);
   const dim3 grid(a.N / 16, grid_y);
   const bool u4 = ((a.K >> 5) % 4) == 0;
 #define DSV2_GEMM(TBV, SWV, NWV)                                                                  \

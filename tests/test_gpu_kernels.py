@@ -111,6 +111,29 @@ def test_gemm_dense(rows, mode):
     assert rel_err(y.float(), ref) < 1e-2
 
 
+@pytest.mark.parametrize("rows", [3, 64, 200])
+@pytest.mark.parametrize("mode", ["residual", "f32", "swiglu"])
+def test_gemm_token_lds_shape_epilogues(rows, mode):
+    """Launches wide enough for the token-rows-in-LDS shape (>= 512 workgroups), every
+    epilogue, ragged token tiles."""
+    K, N = 2048, 32768
+    x = rnd(rows, K, seed=41)
+    W = rnd(2 * N if mode == "swiglu" else N, K, std=0.02, seed=42)
+    res = rnd(rows, N, seed=43) if mode == "residual" else None
+    flags = LINEAR_SWIGLU if mode == "swiglu" else (LINEAR_OUT_F32 if mode == "f32" else 0)
+    y = torch.empty(rows, N, dtype=torch.float32 if mode == "f32" else BF, device=DEV)
+    call("dsv2_gemm_bf16", x.data_ptr(), K, 0, rows, K, W.data_ptr(), 0, N, 1, _hip.ptr(res), N, y.data_ptr(), N, 0,
+         flags, st())
+    acc = x.float() @ W.float().t()
+    if mode == "swiglu":
+        ref = rb(rb(torch.nn.functional.silu(rb(acc[:, :N]))) * rb(acc[:, N:]))
+    elif mode == "residual":
+        ref = rb(res.float() + rb(acc))
+    else:
+        ref = rb(acc)
+    assert rel_err(y.float(), ref) < 1e-2
+
+
 @pytest.mark.parametrize("rows", [5, 100])
 @pytest.mark.parametrize("K,N,swiglu", [(128, 512, False), (1408, 2048, False), (2816, 2048, False), (10944, 2048, False),
                                         (2048, 1408, True), (512, 128, False), (2048, 102400, False),
