@@ -143,8 +143,14 @@ __global__ __launch_bounds__(NW * 64) void gemm_kernel(const GemmArgs a) {
 // HBM, the next chunk's requested before the current one is multiplied.  Steps past K
 // and token rows past the tile load clamped addresses and are zeroed, so every load is
 // unconditional.  The NKQ partial tiles are summed through LDS in a fixed order.
-template <int TB, bool SWIGLU, int CS>
+//
+// AST (CS == 4): weights are read in a row-contiguous pattern -- each load covers 4 rows x
+// 256 B, four loads a wave's 16 rows x 128 k -- which streams ~35% faster from HBM on
+// MI355X than the MFMA fragment order (16 rows x 64 B per load); the wave then passes
+// them through its own 4 KB LDS tile to form the A fragments.
+template <int TB, bool SWIGLU, int CS, bool AST, int DEPTH>
 __global__ __launch_bounds__(512) void gemm_xlds_kernel(const GemmArgs a) {
+  static_assert(!AST || CS == 4, "row-contiguous weight staging works on 128-k chunks");
   constexpr int R = SWIGLU ? 2 : 1;    // row blocks per wave (gate, up)
   constexpr int NRB = SWIGLU ? 2 : 4;  // feature blocks of 16 per workgroup
   constexpr int NKQ = 8 / NRB;         // k ranges
@@ -152,13 +158,17 @@ __global__ __launch_bounds__(512) void gemm_xlds_kernel(const GemmArgs a) {
   constexpr int XROW = CS * 32 + 8;  // LDS row in elements (+16 B pad: conflict-free B reads)
   constexpr int XBUF = NKQ * TOK * XROW;
   constexpr int RED = (NKQ - 1) * NRB * R * TB * 64 * 4;  // floats
-  constexpr int LDS_BYTES = (2 * XBUF * 2 > RED * 4) ? 2 * XBUF * 2 : RED * 4;
+  constexpr int AROW = 136;                             // A tile row (128 k + 8 pad), elements
+  constexpr int ATILE = AST ? 8 * 16 * AROW : 0;         // elements (all waves)
+  constexpr int MAIN = 2 * XBUF * 2 + ATILE * 2;
+  constexpr int LDS_BYTES = (MAIN > RED * 4) ? MAIN : RED * 4;
   constexpr int UNITS = NKQ * TOK * CS * 4;  // 16-byte X units per chunk
   constexpr int UPT = UNITS / 512;
   static_assert(UNITS % 512 == 0, "X units must split evenly over the workgroup");
   __shared__ __attribute__((aligned(16))) uint8_t lds[LDS_BYTES];
   bf16_t* xbuf = reinterpret_cast<bf16_t*>(lds);
   floatx4_t* red = reinterpret_cast<floatx4_t*>(lds);
+  bf16_t* atile = reinterpret_cast<bf16_t*>(lds) + 2 * XBUF + (threadIdx.x >> 6) * 16 * AROW;
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int rb = wv % NRB, kq = wv / NRB;
@@ -176,17 +186,19 @@ __global__ __launch_bounds__(512) void gemm_xlds_kernel(const GemmArgs a) {
     count = min(TOK, a.rows - start);
   }
   const int K = a.K, S = K >> 5;
-  const int SP = ((S + NKQ - 1) / NKQ + CS - 1) / CS * CS;  // steps per k range (CS multiple)
+  // steps per k range: a multiple of CS * DEPTH (steps past K are zero in the X tile)
+  const int SP = ((S + NKQ - 1) / NKQ + CS * DEPTH - 1) / (CS * DEPTH) * (CS * DEPTH);
   const int nch = SP / CS;
   const int f0 = blockIdx.x * 16 * NRB + rb * 16;
   const bf16_t* wrow[R];
 #pragma unroll
-  for (int r = 0; r < R; ++r) wrow[r] = a.W + g * a.wg + (int64_t)(f0 + r * a.N + li) * K + kg * 8;
+  for (int r = 0; r < R; ++r)
+    wrow[r] = AST ? a.W + g * a.wg + (int64_t)(f0 + r * a.N + (lane >> 4)) * K + (lane & 3) * 8
+                  : a.W + g * a.wg + (int64_t)(f0 + r * a.N + li) * K + kg * 8;
 
   // this thread's X units: fixed (range, token, 16-byte part) for every chunk
   const bf16_t* xsrc[UPT];
   int xkq[UPT], xpart[UPT], xdst[UPT];
-  bool xok[UPT];
 #pragma unroll
   for (int j = 0; j < UPT; ++j) {
     const int u = tid + 512 * j;
@@ -197,25 +209,29 @@ __global__ __launch_bounds__(512) void gemm_xlds_kernel(const GemmArgs a) {
     xsrc[j] = a.X + g * a.xg + (int64_t)row * a.xs + (part & 3) * 8;
     xkq[j] = uk;
     xpart[j] = part;
-    xok[j] = tok < count;
     xdst[j] = (uk * TOK + tok) * XROW + (part >> 2) * 32 + (part & 3) * 8;
   }
-  // chunk c of X (this thread's units) into registers / of this wave's weight fragments
+  // chunk c of X (this thread's units) into registers / into LDS buffer buf.  Loaded values
+  // are only masked when they are stored, so no load is waited for before its data is
+  // needed.  Steps past K read step S-1 and are zeroed in the X tile only: the weight
+  // fragments there are real (finite) weights multiplied by zero.  Token rows past the
+  // tile hold row 0's values; their output columns are never stored.
 #define XL_LOAD_X(c)                                                             \
   _Pragma("unroll") for (int j = 0; j < UPT; ++j) {                              \
     const int step_ = xkq[j] * SP + (c) * CS + (xpart[j] >> 2);                  \
-    const uint4 v_ = ldg16(xsrc[j] + (int64_t)min(step_, S - 1) * 32);           \
-    xr[j] = keep_if(xok[j] && step_ < S, v_);                                    \
+    xr[j] = ldg16(xsrc[j] + (int64_t)min(step_, S - 1) * 32);                    \
   }
-#define XL_STORE_X(buf) \
-  _Pragma("unroll") for (int j = 0; j < UPT; ++j) *reinterpret_cast<uint4*>(xbuf + (buf) * XBUF + xdst[j]) = xr[j];
-#define XL_LOAD_A(c, av)                                                         \
-  _Pragma("unroll") for (int si = 0; si < CS; ++si) {                            \
-    const int step_ = kq * SP + (c) * CS + si;                                   \
-    _Pragma("unroll") for (int r = 0; r < R; ++r) {                              \
-      const uint4 v_ = ldg16(wrow[r] + (int64_t)min(step_, S - 1) * 32);         \
-      av[si][r] = keep_if(step_ < S, v_);                                        \
-    }                                                                            \
+#define XL_STORE_X(c, buf)                                                       \
+  _Pragma("unroll") for (int j = 0; j < UPT; ++j) {                              \
+    const int step_ = xkq[j] * SP + (c) * CS + (xpart[j] >> 2);                  \
+    *reinterpret_cast<uint4*>(xbuf + (buf) * XBUF + xdst[j]) = keep_if(step_ < S, xr[j]); \
+  }
+// AST: av[q][r] = rows 4q + (lane >> 4) of block r, k = chunk + (lane & 15) * 8
+#define XL_LOAD_A(c, av)                                                                         \
+  _Pragma("unroll") for (int si = 0; si < CS; ++si) {                                            \
+    const int step_ = kq * SP + (c) * CS + (AST ? ((lane & 15) >> 2) : si);                      \
+    _Pragma("unroll") for (int r = 0; r < R; ++r)                                                \
+      av[si][r] = ldg16(wrow[r] + (AST ? (int64_t)si * 4 * K : 0) + (int64_t)min(step_, S - 1) * 32); \
   }
 
   floatx4_t acc[R][TB];
@@ -224,34 +240,57 @@ __global__ __launch_bounds__(512) void gemm_xlds_kernel(const GemmArgs a) {
 #pragma unroll
     for (int tb = 0; tb < TB; ++tb) acc[r][tb] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 
-  uint4 a0[CS][R], a1[CS][R], xr[UPT];
-  XL_LOAD_A(0, a0)
+  // Weight chunks are requested DEPTH - 1 chunks ahead of the one being multiplied, token
+  // chunks one ahead and before the weight loads (loads complete in issue order, so the wait
+  // for a token chunk before its LDS store leaves the later weight loads in flight).  The
+  // chunk loop is unrolled by DEPTH (nch is a multiple of it) so every register buffer index
+  // is a constant, and no load sits behind a branch: requests past the last chunk repeat it
+  // (L2 hits), so the compiler's wait counts stay exact.
+  uint4 ab[DEPTH][CS][R], xr[UPT];
   XL_LOAD_X(0)
-  XL_STORE_X(0)
+#pragma unroll
+  for (int p = 0; p + 1 < DEPTH; ++p) XL_LOAD_A(p, ab[p])
+  XL_STORE_X(0, 0)
   __syncthreads();
-  for (int c = 0; c < nch; ++c) {
-    const bool more = c + 1 < nch;
-    if (more) {
-      XL_LOAD_A(c + 1, a1)
-      XL_LOAD_X(c + 1)
-    }
-    const bf16_t* xb = xbuf + (c & 1) * XBUF + (kq * TOK + li) * XROW + kg * 8;
+  for (int c0 = 0; c0 < nch; c0 += DEPTH) {
 #pragma unroll
-    for (int si = 0; si < CS; ++si)
+    for (int i = 0; i < DEPTH; ++i) {
+      const int c = c0 + i;
+      XL_LOAD_X(min(c + 1, nch - 1))
+      XL_LOAD_A(min(c + DEPTH - 1, nch - 1), ab[(i + DEPTH - 1) % DEPTH])
+      const bf16_t* xb = xbuf + (c & 1) * XBUF + (kq * TOK + li) * XROW + kg * 8;
+      bf16x8_t afr[CS][R];
+      if (AST) {
+        // each row block's 16 rows x 128 k through the wave's LDS tile into MFMA fragments
 #pragma unroll
-      for (int tb = 0; tb < TB; ++tb) {
-        const bf16x8_t bfr = *reinterpret_cast<const bf16x8_t*>(xb + tb * 16 * XROW + si * 32);
+        for (int r = 0; r < R; ++r) {
 #pragma unroll
-        for (int r = 0; r < R; ++r) acc[r][tb] = mfma16x16x32(as_bf16x8(a0[si][r]), bfr, acc[r][tb]);
+          for (int q = 0; q < CS; ++q)
+            *reinterpret_cast<uint4*>(atile + (4 * q + (lane >> 4)) * AROW + (lane & 15) * 8) = ab[i][q][r];
+          __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+#pragma unroll
+          for (int si = 0; si < CS; ++si)
+            afr[si][r] = *reinterpret_cast<const bf16x8_t*>(atile + li * AROW + si * 32 + kg * 8);
+          __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        }
+      } else {
+#pragma unroll
+        for (int si = 0; si < CS; ++si)
+#pragma unroll
+          for (int r = 0; r < R; ++r) afr[si][r] = as_bf16x8(ab[i][si][r]);
       }
-    if (more) {
-      XL_STORE_X((c + 1) & 1)
+#pragma unroll
+      for (int si = 0; si < CS; ++si)
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb) {
+          const bf16x8_t bfr = *reinterpret_cast<const bf16x8_t*>(xb + tb * 16 * XROW + si * 32);
+#pragma unroll
+          for (int r = 0; r < R; ++r) acc[r][tb] = mfma16x16x32(afr[si][r], bfr, acc[r][tb]);
+        }
+      // the last chunk's store fills the idle buffer with a repeat (never read)
+      XL_STORE_X(c + 1, (c + 1) & 1)
+      __syncthreads();
     }
-    __syncthreads();
-#pragma unroll
-    for (int si = 0; si < CS; ++si)
-#pragma unroll
-      for (int r = 0; r < R; ++r) a0[si][r] = a1[si][r];
   }
 
 #undef XL_LOAD_X
@@ -299,23 +338,209 @@ __global__ __launch_bounds__(512) void gemm_xlds_kernel(const GemmArgs a) {
   }
 }
 
+// Four consecutive outputs (features n..n+3) of token slot `slot`: optional residual add,
+// then a bf16 or fp32 store.
+__device__ __forceinline__ void gemm_store4(const GemmArgs& a, int g, int slot, int n, float* v) {
+  if (a.res) {
+    const uint2 r2 = *reinterpret_cast<const uint2*>(a.res + slot * a.rs + n);
+    v[0] = rbf(__uint_as_float(r2.x << 16) + v[0]);
+    v[1] = rbf(__uint_as_float(r2.x & 0xffff0000u) + v[1]);
+    v[2] = rbf(__uint_as_float(r2.y << 16) + v[2]);
+    v[3] = rbf(__uint_as_float(r2.y & 0xffff0000u) + v[3]);
+  }
+  const int64_t off = g * a.yg + (int64_t)slot * a.ys + n;
+  if (a.out_f32) {
+    *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.Y) + off) = make_float4(v[0], v[1], v[2], v[3]);
+  } else {
+    uint2 o;
+    o.x = pack2(v[0], v[1]);
+    o.y = pack2(v[2], v[3]);
+    *reinterpret_cast<uint2*>(reinterpret_cast<bf16_t*>(a.Y) + off) = o;
+  }
+}
+
+// One-shot shape for dense weights and few tokens (the row blocks alone cannot fill the
+// chip): a workgroup owns RBW blocks of 16 features for one tile of 16*TB tokens, and
+// KW waves per block split K into 128-wide chunks (wave kw takes chunks kw, kw + KW, ...,
+// J of them).  Every wave requests all of its weight chunks at once, in the row-contiguous
+// pattern (4 rows x 256 B per load) that streams fastest from HBM, and forms the MFMA A
+// fragments through its own LDS tile; token fragments come from L2.  The KW partial tiles
+// are summed through LDS in kw order.  The 1-D grid is laid out so the token tiles of one
+// row block run on the same XCD (workgroups go round-robin over the 8 XCDs): the first
+// tile's weight reads fill that XCD's L2 for the others.
+struct OsShape {
+  int rbw, kw, row_blocks, tiles, groups, nwg;
+};
+
+template <int TB, bool SWIGLU, int J>
+__global__ __launch_bounds__(1024) void gemm_os_kernel(const GemmArgs a, const OsShape sh) {
+  constexpr int R = SWIGLU ? 2 : 1;
+  constexpr int AROW = 136;  // LDS tile row (128 k + 8 pad), elements
+  // dynamic LDS, os_lds_bytes(): per wave a 16 x AROW tile, reused for the partial tiles
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int li = lane & 15, kg = lane >> 4;
+  // XCD-aware work index: XCD x = blockIdx.x % 8 takes work items [x*per, (x+1)*per)
+  const int per = sh.nwg / 8;
+  const int w = (blockIdx.x % 8) * per + blockIdx.x / 8;
+  const int total = sh.row_blocks * sh.tiles * sh.groups;
+  if (w >= total) return;
+  const int tile = w % sh.tiles, rbg = w / sh.tiles;  // tiles of one row block are adjacent
+  const int g = rbg / sh.row_blocks, rblk = rbg % sh.row_blocks;
+  const int rb = wv % sh.rbw, kw = wv / sh.rbw;
+  const int start = tile * 16 * TB, count = min(16 * TB, a.rows - start);
+  const int K = a.K, S = K >> 5;
+  const int f0 = (rblk * sh.rbw + rb) * 16;
+
+  // weight chunks: ab[j][q][r] = rows 4q + (lane >> 4) of block r, k = 128 c_j + (lane & 15) * 8
+  uint4 ab[J][4][R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const bf16_t* wp = a.W + g * a.wg + (int64_t)(f0 + r * a.N + (lane >> 4)) * K + (lane & 3) * 8;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int step = (kw + j * sh.kw) * 4 + ((lane & 15) >> 2);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) ab[j][q][r] = ldg16(wp + (int64_t)q * 4 * K + (int64_t)min(step, S - 1) * 32);
+    }
+  }
+  // token rows in the same pattern: xrow[tb] + q*4 rows = token 16 tb + 4q + (lane >> 4)
+  const bf16_t* xrow[TB][4];
+#pragma unroll
+  for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int t0 = tb * 16 + 4 * q + (lane >> 4);
+      const int t = t0 < count ? t0 : 0;
+      xrow[tb][q] = a.X + g * a.xg + (int64_t)(start + t) * a.xs + (lane & 3) * 8;
+    }
+  floatx4_t acc[R][TB];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) acc[r][tb] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+
+  bf16_t* atile = reinterpret_cast<bf16_t*>(lds) + wv * 16 * AROW;
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int s0 = (kw + j * sh.kw) * 4;
+    const int step = s0 + ((lane & 15) >> 2);
+    // token chunk rows (steps past K: clamped address, zeroed before the LDS store)
+    uint4 bx[TB][4];
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) bx[tb][q] = ldg16(xrow[tb][q] + (int64_t)min(step, S - 1) * 32);
+    // weight and token 16 x 128 tiles through the wave's LDS tile into MFMA fragments
+    bf16x8_t afr[4][R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<uint4*>(atile + (4 * q + (lane >> 4)) * AROW + (lane & 15) * 8) = ab[j][q][r];
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+#pragma unroll
+      for (int si = 0; si < 4; ++si)
+        afr[si][r] = *reinterpret_cast<const bf16x8_t*>(atile + li * AROW + si * 32 + kg * 8);
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    }
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<uint4*>(atile + (4 * q + (lane >> 4)) * AROW + (lane & 15) * 8) = keep_if(step < S, bx[tb][q]);
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+#pragma unroll
+      for (int si = 0; si < 4; ++si) {
+        const bf16x8_t bfr = *reinterpret_cast<const bf16x8_t*>(atile + li * AROW + si * 32 + kg * 8);
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r][tb] = mfma16x16x32(afr[si][r], bfr, acc[r][tb]);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    }
+  }
+
+  // sum the KW partial tiles in kw order (the A tiles are dead after the barrier); the
+  // RBW * TB (row block, token block) outputs are spread over the waves
+  floatx4_t* red = reinterpret_cast<floatx4_t*>(lds);
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) red[(((kw * sh.rbw + rb) * R + r) * TB + tb) * 64 + lane] = acc[r][tb];
+  __syncthreads();
+  const int nw = sh.rbw * sh.kw;
+  for (int u = wv; u < sh.rbw * TB; u += nw) {
+    const int urb = u % sh.rbw, tb = u / sh.rbw;
+    if (tb * 16 + li >= count) continue;
+    floatx4_t sum[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      sum[r] = red[((urb * R + r) * TB + tb) * 64 + lane];
+      for (int q = 1; q < sh.kw; ++q) sum[r] += red[(((q * sh.rbw + urb) * R + r) * TB + tb) * 64 + lane];
+    }
+    float v[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = SWIGLU ? swiglu_bf(sum[0][e], sum[R - 1][e]) : rbf(sum[0][e]);
+    gemm_store4(a, g, start + tb * 16 + li, (rblk * sh.rbw + urb) * 16 + 4 * kg, v);
+  }
+}
+
+// Shape of a one-shot launch for an implicit-tile GEMM, or rbw = 0 if it does not apply.
+static OsShape os_shape(const GemmArgs& a, int tb, bool swiglu, int groups, int* j_out, int kwmax = 16) {
+  OsShape sh{};
+  const int nc = ((a.K >> 5) + 3) / 4;  // 128-wide chunks
+  const int jmax = (swiglu || tb >= 4) ? 1 : 2;  // register budget of gemm_os_kernel
+  int j = (nc + kwmax - 1) / kwmax;
+  if (j > jmax) return sh;
+  int kw = (nc + j - 1) / j;
+  int rbw = 1;
+  while (rbw * kw * 2 <= 8 && a.N % (16 * rbw * 2) == 0) rbw *= 2;  // at least ~8 waves when K is short
+  if (a.N % (16 * rbw) != 0) return sh;
+  sh.rbw = rbw;
+  sh.kw = kw;
+  sh.row_blocks = a.N / (16 * rbw);
+  sh.tiles = a.tiles_per_group;
+  sh.groups = groups;
+  const int total = sh.row_blocks * sh.tiles * groups;
+  sh.nwg = (total + 7) / 8 * 8;
+  *j_out = j;
+  return sh;
+}
+
+static int os_lds_bytes(const OsShape& sh, int tb, bool swiglu) {
+  const int nw = sh.rbw * sh.kw;
+  const int tiles = nw * 16 * 136 * 2, red = nw * (swiglu ? 2 : 1) * tb * 1024;
+  return tiles > red ? tiles : red;
+}
+
+template <int TB, bool SWIGLU, int J>
+static void launch_os_variant(const GemmArgs& a, const OsShape& sh, hipStream_t st) {
+  hipLaunchKernelGGL((gemm_os_kernel<TB, SWIGLU, J>), dim3(sh.nwg), dim3(sh.rbw * sh.kw * 64),
+                     os_lds_bytes(sh, TB, SWIGLU), st, a, sh);
+}
+
 // features per workgroup of gemm_xlds_kernel
 static int xlds_features(bool swiglu) { return swiglu ? 32 : 64; }
 
+template <int TB, bool SWIGLU, int CS, bool AST, int DEPTH>
+static void launch_xlds_variant(const GemmArgs& a, int grid_y, hipStream_t st) {
+  hipLaunchKernelGGL((gemm_xlds_kernel<TB, SWIGLU, CS, AST, DEPTH>), dim3(a.N / xlds_features(SWIGLU), grid_y),
+                     dim3(512), 0, st, a);
+}
+
 static int launch_gemm_xlds(const GemmArgs& a, int tb, bool swiglu, int grid_y, hipStream_t st) {
-  const dim3 grid(a.N / xlds_features(swiglu), grid_y);
-#define DSV2_XL(TBV, SWV, CSV) hipLaunchKernelGGL((gemm_xlds_kernel<TBV, SWV, CSV>), grid, dim3(512), 0, st, a)
+  // row-contiguous weight staging wherever its LDS tiles fit next to the token chunks
   if (swiglu) {
-    if (tb == 1) DSV2_XL(1, true, 4);
-    else if (tb == 2) DSV2_XL(2, true, 4);
-    else DSV2_XL(4, true, 2);
+    if (tb == 1) launch_xlds_variant<1, true, 4, true, 2>(a, grid_y, st);
+    else if (tb == 2) launch_xlds_variant<2, true, 4, true, 2>(a, grid_y, st);
+    else launch_xlds_variant<4, true, 2, false, 2>(a, grid_y, st);
   } else {
-    if (tb == 1) DSV2_XL(1, false, 8);
-    else if (tb == 2) DSV2_XL(2, false, 8);
-    else if (tb == 4) DSV2_XL(4, false, 4);
-    else DSV2_XL(8, false, 2);
+    if (tb == 1) launch_xlds_variant<1, false, 4, true, 2>(a, grid_y, st);
+    else if (tb == 2) launch_xlds_variant<2, false, 4, true, 2>(a, grid_y, st);
+    else if (tb == 4) launch_xlds_variant<4, false, 4, true, 2>(a, grid_y, st);
+    else launch_xlds_variant<8, false, 2, false, 2>(a, grid_y, st);
   }
-#undef DSV2_XL
   return dsv2_launch_status("gemm");
 }
 
@@ -348,6 +573,43 @@ static int launch_gemm(const GemmArgs& a, int tb, bool swiglu, int grid_y, hipSt
 }
 
 static int pick_tb(int rows) { return rows <= 16 ? 1 : (rows <= 32 ? 2 : (rows <= 64 ? 4 : 8)); }
+
+// Dense (implicit-tile) shapes whose row blocks alone cannot fill the chip, measured on
+// MI355X at 16..256 tokens: the one-shot kernel for short K, SwiGLU and up to 64 tokens;
+// the token-rows-in-LDS kernel (64-row workgroups sharing token chunks) for more tokens,
+// with the largest token tile that still gives ~200 workgroups.  Returns false (nothing
+// launched) for shapes left to launch_gemm: long K, huge N, or N not a multiple of 16*rbw.
+static bool launch_dense_os(GemmArgs a, int groups, bool swiglu, hipStream_t st) {
+  const int rows = a.rows, K = a.K;
+  if (K > 4096 || (int64_t)a.N * groups >= 16384) return false;
+  if (!swiglu && K > 512 && rows > 64 && a.N % 64 == 0) {
+    int tb = 1;
+    for (int t : {2, 4}) {
+      const int64_t tiles = (rows + 16 * t - 1) / (16 * t);
+      if ((int64_t)(a.N / 64) * tiles * groups >= 200) tb = t;
+    }
+    a.tiles_per_group = (rows + 16 * tb - 1) / (16 * tb);
+    const int64_t gy = (int64_t)a.tiles_per_group * groups;
+    if (gy > 65535) return false;
+    if (tb == 1) launch_xlds_variant<1, false, 4, true, 2>(a, (int)gy, st);
+    else if (tb == 2) launch_xlds_variant<2, false, 4, true, 2>(a, (int)gy, st);
+    else launch_xlds_variant<4, false, 4, true, 2>(a, (int)gy, st);
+    return true;
+  }
+  const int tb = K <= 512 ? (rows <= 64 ? 1 : 2) : (swiglu ? (rows <= 16 ? 1 : (rows <= 32 ? 2 : 4)) : (rows <= 16 ? 1 : 2));
+  a.tiles_per_group = (rows + 16 * tb - 1) / (16 * tb);
+  int j = 0;
+  OsShape sh = os_shape(a, tb, swiglu, groups, &j, swiglu ? 16 : 8);
+  if (!sh.rbw) sh = os_shape(a, tb, swiglu, groups, &j, 16);
+  if (!sh.rbw || (int64_t)sh.nwg > (int64_t)1 << 30) return false;
+#define DSV2_OS(TBV, JV)                                                          \
+  (swiglu ? launch_os_variant<TBV, true, 1>(a, sh, st) : launch_os_variant<TBV, false, JV>(a, sh, st))
+  if (tb == 1) { if (j == 1) DSV2_OS(1, 1); else DSV2_OS(1, 2); }
+  else if (tb == 2) { if (j == 1) DSV2_OS(2, 1); else DSV2_OS(2, 2); }
+  else DSV2_OS(4, 1);
+#undef DSV2_OS
+  return true;
+}
 
 extern "C" int dsv2_gemm_bf16(const void* x, int64_t x_stride, int64_t x_gstride, int rows, int K, const void* W,
                               int64_t w_gstride, int N, int n_groups, const void* residual, int64_t res_stride,
@@ -384,9 +646,11 @@ extern "C" int dsv2_gemm_bf16(const void* x, int64_t x_stride, int64_t x_gstride
   a.ys = y_stride;
   a.yg = y_gstride;
   a.out_f32 = flags & DSV2_LINEAR_OUT_F32;
+  const bool swiglu = flags & DSV2_LINEAR_SWIGLU;
+  if (launch_dense_os(a, n_groups, swiglu, (hipStream_t)stream)) return dsv2_launch_status("gemm");
   const int64_t grid_y = (int64_t)a.tiles_per_group * n_groups;
   DSV2_REQUIRE(grid_y <= 65535, DSV2_E_SHAPE, "gemm: too many row tiles (%lld)", (long long)grid_y);
-  return launch_gemm(a, tb, flags & DSV2_LINEAR_SWIGLU, (int)grid_y, (hipStream_t)stream);
+  return launch_gemm(a, tb, swiglu, (int)grid_y, (hipStream_t)stream);
 }
 
 static int tile_tb(int tile_tokens) { return tile_tokens == 16 ? 1 : (tile_tokens == 32 ? 2 : 4); }

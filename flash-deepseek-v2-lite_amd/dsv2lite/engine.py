@@ -47,8 +47,11 @@ def plan_splits(rows: int, max_ctx: int, target_wgs: int = 1024) -> tuple[int, i
 
 
 def moe_tile_tokens(rows: int, n_experts: int = 64, top_k: int = 6) -> int:
+    """Token tile of the expert-grouped MoE GEMMs from the mean routes per expert.  Measured
+    on MI355X (gate_up + down per layer): 16-token tiles at 6 routes/expert (bsz=64), 32-token
+    tiles at 24 (bsz=256: 250 us vs 289 us with 16 and 313 us with 64)."""
     avg = rows * top_k / n_experts
-    return 16 if avg <= 6 else (32 if avg <= 16 else 64)
+    return 16 if avg <= 10 else (32 if avg <= 40 else 64)
 
 
 class RowBuffers:

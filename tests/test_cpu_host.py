@@ -90,7 +90,8 @@ def test_moe_tile_choice_and_cache_layout():
     from dsv2lite.cache import CompressedKVCache
     from dsv2lite.engine import moe_tile_tokens
 
-    assert moe_tile_tokens(1) == 16 and moe_tile_tokens(64) == 16 and moe_tile_tokens(256) == 64
+    assert moe_tile_tokens(1) == 16 and moe_tile_tokens(64) == 16 and moe_tile_tokens(256) == 32
+    assert moe_tile_tokens(512) == 64
     c = CompressedKVCache(2, [5, 7, 3], device="cpu")
     assert c.base.tolist() == [0, 5, 12] and c.total == 15 and c.data.shape == (2, 15, 576)
     c.pos.copy_(torch.tensor([1, 2, 3], dtype=torch.int32))

@@ -151,7 +151,31 @@ def test_gemm_k_split_shapes(rows, K, N, swiglu):
     assert rel_err(y.float(), ref) < 1e-2
 
 
-@pytest.mark.parametrize("rows", [1, 5, 64])
+@pytest.mark.parametrize("rows", [16, 64, 130, 256])
+@pytest.mark.parametrize("K,N,mode", [(2048, 3648, "plain"), (2048, 2048, "residual"), (2048, 2816, "swiglu"),
+                                      (2816, 2048, "plain"), (2048, 10944, "swiglu"), (2048, 2048, "f32")])
+def test_gemm_dense_model_shapes(rows, K, N, mode):
+    """The batch family's dense projections (qkv_a, o_proj + residual, shared-expert
+    gate_up / down, layer-0 MLP gate_up) at the token counts where the one-shot and the
+    token-rows-in-LDS shapes take over from the k-split kernel."""
+    x = rnd(rows, K, seed=K + N + rows)
+    W = rnd(2 * N if mode == "swiglu" else N, K, std=0.02, seed=K + N)
+    res = rnd(rows, N, seed=3 * rows) if mode == "residual" else None
+    flags = LINEAR_SWIGLU if mode == "swiglu" else (LINEAR_OUT_F32 if mode == "f32" else 0)
+    y = torch.empty(rows, N, dtype=torch.float32 if mode == "f32" else BF, device=DEV)
+    call("dsv2_gemm_bf16", x.data_ptr(), K, 0, rows, K, W.data_ptr(), 0, N, 1, _hip.ptr(res), N, y.data_ptr(), N, 0,
+         flags, st())
+    acc = x.float() @ W.float().t()
+    if mode == "swiglu":
+        ref = rb(rb(torch.nn.functional.silu(rb(acc[:, :N]))) * rb(acc[:, N:]))
+    elif mode == "residual":
+        ref = rb(res.float() + rb(acc))
+    else:
+        ref = rb(acc)
+    assert rel_err(y.float(), ref) < 1e-2
+
+
+@pytest.mark.parametrize("rows", [1, 5, 64, 200, 256])
 def test_gemm_grouped_heads_absorption(rows):
     # q_lat[r, h, :512] = W_UK_h^T q_nope[r, h]   and   attn[r, h*128+i] = W_UV_h o_lat[r, h]
     qkva = rnd(rows, 3648, seed=12)
