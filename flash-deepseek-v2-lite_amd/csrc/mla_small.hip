@@ -1,12 +1,17 @@
 // Fused absorbed-MLA decode for a few rows (the small family): one 1024-thread
 // workgroup per (row, head) does the whole head:
-//   1. q_lat_h = W_UK_h^T q_nope_h        (16 lanes per output, all loads in flight)
+//   1. q_lat_h = W_UK_h^T q_nope_h        (16 lanes per output)
 //   2. new cache row (kv-norm + RoPE(k_pe)) into LDS; the h == 0 workgroup stores it
-//   3. RoPE(q_pe_h); per-wave online softmax over 4-token batches of the cached rows
-//      (one 16-byte load per lane serves both q.k and p.v), the new token from LDS
+//   3. RoPE(q_pe_h); per-wave online softmax over kBatch-token batches of the cached rows
+//      (a lane's 16-byte latent load serves both q.k and p.v, plus one rope element), the
+//      new token from LDS
 //   4. log-sum-exp merge of the 16 waves -> o_lat_h (fp32)
 //   5. attn[row, h*128 + i] = W_UV_h o_lat_h
-// Replaces prepare + split decode + combine (three launches) when the batch is small.
+// Every load that depends on nothing -- W_UK, q, the new row's inputs and each wave's first
+// batch of cached rows -- is requested at entry, so the kernel pays one memory round trip
+// before the attention instead of three; W_UV is requested when the attention loop ends and
+// arrives while the waves are merged.  Replaces prepare + split decode + combine (three
+// launches) when the batch is small.
 #include "common.h"
 
 namespace {
@@ -33,45 +38,72 @@ __global__ __launch_bounds__(1024) void mla_fused_kernel(const bf16_t* __restric
   const int pc = p < 0 ? 0 : (p >= max_pos ? max_pos - 1 : p);
   const bf16_t* cs = cosT + (int64_t)pc * 64;
   const bf16_t* sn = sinT + (int64_t)pc * 64;
+  const bf16_t* crow0 = cache + base[b] * kRow;
 
-  // W_UV rows of step 5 (wave wv: rows wv*8 .. wv*8+7 of head h) are requested first: they
-  // depend on nothing, so their HBM latency overlaps steps 1-4
-  uint4 wuv[8];
+  // ---- entry loads -------------------------------------------------------------------
+  // absorption: thread (gi = tid / 16, k = tid % 16) owns rows u*64 + gi of W_UKT_h, K slice k
+  const int gi = tid >> 4, k = tid & 15;
+  const uint4 qn4 = ldg16(q + h * 192 + k * 8);
+  uint4 wr[8];
   {
-    const bf16_t* wp = w_uv + ((int64_t)h * 128 + wv * 8) * kLat + lane * 8;
-#pragma unroll
-    for (int r = 0; r < 8; ++r) wuv[r] = ldg16(wp + (int64_t)r * kLat);
-  }
-
-  // 1. absorption: row j = u*64 + gi of W_UKT_h (K = 128 split over 16 lanes)
-  {
-    const int gi = tid >> 4, k = tid & 15;
-    float qn[8];
-    unpack8(ldg16(q + h * 192 + k * 8), qn);
-    uint4 wr[8];
     const bf16_t* wk = w_ukt + ((int64_t)h * kLat + gi) * 128 + k * 8;
 #pragma unroll
     for (int u = 0; u < 8; ++u) wr[u] = ldg16(wk + (int64_t)u * 64 * 128);
+  }
+  // this wave's first batch of cached rows (rows clamped into [0, p-1]; rows past p are
+  // masked out of the softmax): lane l holds latent elements 8l..8l+7 and rope element l
+  uint4 va[kBatch];
+  bf16_t vr[kBatch];
+  const int t_first = wv * kBatch;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      float s = dot8(wr[u], qn);
-      s += __shfl_xor(s, 8, 64);
-      s += __shfl_xor(s, 4, 64);
-      s += __shfl_xor(s, 2, 64);
-      s += __shfl_xor(s, 1, 64);
-      if (k == 0) qv[u * 64 + gi] = rbf(s);
+  for (int u = 0; u < kBatch; ++u) {
+    const int t = max(min(t_first + u, p - 1), 0);
+    va[u] = ldg16(crow0 + (int64_t)t * kRow + lane * 8);
+    vr[u] = crow0[(int64_t)t * kRow + kLat + lane];
+  }
+  // new row (wave 0) / q_pe (wave 1) inputs
+  uint4 kv4 = {0u, 0u, 0u, 0u}, kw4 = {0u, 0u, 0u, 0u};
+  float re = 0.f, ro = 0.f, c0 = 0.f, c1 = 0.f, s0 = 0.f, s1 = 0.f;
+  if (wv <= 1) {
+    if (wv == 0) {
+      kv4 = ldg16(q + 3072 + lane * 8);
+      kw4 = ldg16(kvw + lane * 8);
+    }
+    if (lane < 32) {
+      const bf16_t* rp = wv == 0 ? q + 3584 : q + h * 192 + 128;
+      re = bf2f(rp[2 * lane]);
+      ro = bf2f(rp[2 * lane + 1]);
+      c0 = bf2f(cs[lane]);
+      c1 = bf2f(cs[32 + lane]);
+      s0 = bf2f(sn[lane]);
+      s1 = bf2f(sn[32 + lane]);
     }
   }
-  // 2./3a. new row (wave 0) and RoPE(q_pe) (wave 1)
+
+  // ---- 1. absorption ----------------------------------------------------------------
+  {
+    float qn[8];
+    unpack8(qn4, qn);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      float sdot = dot8(wr[u], qn);
+      sdot += __shfl_xor(sdot, 8, 64);
+      sdot += __shfl_xor(sdot, 4, 64);
+      sdot += __shfl_xor(sdot, 2, 64);
+      sdot += __shfl_xor(sdot, 1, 64);
+      if (k == 0) qv[u * 64 + gi] = rbf(sdot);
+    }
+  }
+  // ---- 2./3a. new row (wave 0) and RoPE(q_pe) (wave 1) --------------------------------
   if (wv == 0) {
     float f[8], g[8];
-    unpack8(ldg16(q + 3072 + lane * 8), f);
+    unpack8(kv4, f);
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(f[i], f[i], ss);
     ss = wave_sum(ss);
     const float rs = rsqrtf(ss / static_cast<float>(kLat) + eps);
-    unpack8(ldg16(kvw + lane * 8), g);
+    unpack8(kw4, g);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       f[i] = rbf(g[i] * rbf(f[i] * rs));
@@ -80,9 +112,8 @@ __global__ __launch_bounds__(1024) void mla_fused_kernel(const bf16_t* __restric
     bf16_t* crow = cache + (base[b] + p) * kRow;
     if (h == 0) *reinterpret_cast<uint4*>(crow + lane * 8) = pack8(f);
     if (lane < 32) {
-      const float e = bf2f(q[3584 + 2 * lane]), o = bf2f(q[3585 + 2 * lane]);
-      const float v0 = rbf(e * bf2f(cs[lane]) - o * bf2f(sn[lane]));
-      const float v1 = rbf(o * bf2f(cs[32 + lane]) + e * bf2f(sn[32 + lane]));
+      const float v0 = rbf(re * c0 - ro * s0);
+      const float v1 = rbf(ro * c1 + re * s1);
       nrow[kLat + lane] = v0;
       nrow[kLat + 32 + lane] = v1;
       if (h == 0) {
@@ -91,45 +122,32 @@ __global__ __launch_bounds__(1024) void mla_fused_kernel(const bf16_t* __restric
       }
     }
   } else if (wv == 1 && lane < 32) {
-    const bf16_t* qp = q + h * 192 + 128;
-    const float e = bf2f(qp[2 * lane]), o = bf2f(qp[2 * lane + 1]);
-    qv[kLat + lane] = rbf(e * bf2f(cs[lane]) - o * bf2f(sn[lane]));
-    qv[kLat + 32 + lane] = rbf(o * bf2f(cs[32 + lane]) + e * bf2f(sn[32 + lane]));
+    qv[kLat + lane] = rbf(re * c0 - ro * s0);
+    qv[kLat + 32 + lane] = rbf(ro * c1 + re * s1);
   }
   __syncthreads();
 
-  // 3b. attention: wave wv takes token batches [wv*kBatch + n*kWaves*kBatch, +kBatch)
-  float qa[8], qb[8];
+  // ---- 3b. attention: wave wv takes token batches [wv*kBatch + n*kWaves*kBatch, +kBatch) --
+  float qa[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    qa[i] = qv[lane * 8 + i];
-    qb[i] = lane < 8 ? qv[kLat + lane * 8 + i] : 0.f;
-  }
-  const bf16_t* crow0 = cache + base[b] * kRow;
+  for (int i = 0; i < 8; ++i) qa[i] = qv[lane * 8 + i];
+  const float qb = qv[kLat + lane];
   float m = -INFINITY, l = 0.f, o[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) o[i] = 0.f;
-  const uint4 zero = {0u, 0u, 0u, 0u};
-  for (int t0 = wv * kBatch; t0 < p; t0 += kWaves * kBatch) {
-    uint4 va[kBatch], vb[kBatch];
+  for (int t0 = t_first; t0 < p; t0 += kWaves * kBatch) {
+    float sc[kBatch];
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      const int t = min(t0 + u, p - 1);
-      va[u] = ldg16(crow0 + (int64_t)t * kRow + lane * 8);
-      vb[u] = lane < 8 ? ldg16(crow0 + (int64_t)t * kRow + kLat + lane * 8) : zero;
-    }
-    float s[kBatch];
-#pragma unroll
-    for (int u = 0; u < kBatch; ++u) s[u] = dot8(va[u], qa) + dot8(vb[u], qb);
+    for (int u = 0; u < kBatch; ++u) sc[u] = __builtin_fmaf(bf2f(vr[u]), qb, dot8(va[u], qa));
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1)
 #pragma unroll
-      for (int u = 0; u < kBatch; ++u) s[u] += __shfl_xor(s[u], off, 64);
+      for (int u = 0; u < kBatch; ++u) sc[u] += __shfl_xor(sc[u], off, 64);
     float mx = m;
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
-      s[u] = (t0 + u < p) ? s[u] * scale_log2 : -INFINITY;
-      mx = fmaxf(mx, s[u]);
+      sc[u] = (t0 + u < p) ? sc[u] * scale_log2 : -INFINITY;
+      mx = fmaxf(mx, sc[u]);
     }
     const float alpha = exp2f(m - mx);
     m = mx;
@@ -138,22 +156,34 @@ __global__ __launch_bounds__(1024) void mla_fused_kernel(const bf16_t* __restric
     for (int i = 0; i < 8; ++i) o[i] *= alpha;
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
-      const float pu = exp2f(s[u] - m);
+      const float pu = exp2f(sc[u] - m);
       l += pu;
       float v[8];
       unpack8(va[u], v);
 #pragma unroll
       for (int i = 0; i < 8; ++i) o[i] = __builtin_fmaf(pu, v[i], o[i]);
     }
+    const int tn = t0 + kWaves * kBatch;
+    if (tn < p) {
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int t = min(tn + u, p - 1);
+        va[u] = ldg16(crow0 + (int64_t)t * kRow + lane * 8);
+        vr[u] = crow0[(int64_t)t * kRow + kLat + lane];
+      }
+    }
+  }
+  // W_UV rows of step 5 (wave wv: rows wv*8 .. wv*8+7 of head h), in flight during the merge
+  uint4 wuv[8];
+  {
+    const bf16_t* wp = w_uv + ((int64_t)h * 128 + wv * 8) * kLat + lane * 8;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) wuv[r] = ldg16(wp + (int64_t)r * kLat);
   }
   if (wv == 0) {  // the new token (position p) from LDS
-    float sp = 0.f;
+    float sp = qb * nrow[kLat + lane];
 #pragma unroll
     for (int i = 0; i < 8; ++i) sp = __builtin_fmaf(qa[i], nrow[lane * 8 + i], sp);
-    if (lane < 8) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) sp = __builtin_fmaf(qb[i], nrow[kLat + lane * 8 + i], sp);
-    }
     sp = wave_sum(sp) * scale_log2;
     const float mx = fmaxf(m, sp);
     const float alpha = exp2f(m - mx), pu = exp2f(sp - mx);
@@ -170,7 +200,7 @@ __global__ __launch_bounds__(1024) void mla_fused_kernel(const bf16_t* __restric
   for (int i = 0; i < 8; ++i) wo[wv][lane * 8 + i] = o[i];
   __syncthreads();
 
-  // 4. merge the waves
+  // ---- 4. merge the waves -------------------------------------------------------------
   if (tid < kLat) {
     float M = -INFINITY;
 #pragma unroll
@@ -186,7 +216,7 @@ __global__ __launch_bounds__(1024) void mla_fused_kernel(const bf16_t* __restric
   }
   __syncthreads();
 
-  // 5. W_UV: wave wv computes rows wv*8 .. wv*8+7 of head h
+  // ---- 5. W_UV: wave wv computes rows wv*8 .. wv*8+7 of head h ------------------------
   float xo[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) xo[i] = olat[lane * 8 + i];
