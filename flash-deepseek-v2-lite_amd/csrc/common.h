@@ -73,6 +73,14 @@ __device__ __forceinline__ uint4 keep_if(bool ok, const uint4& v) {
   return make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
 }
 
+// Holds a loaded value at this point of the program.  Loads complete in issue order, and
+// the compiler moves a load that is used only inside a branch into that branch (or turns a
+// select between two loads into one); the wait for it there also waits for every load
+// issued before it -- typically a weight stream.  Pinning an early operand (x, norm weights,
+// residuals) right after the weight loads are issued keeps its load ahead of them, and the
+// wait here covers only the loads issued before it.
+__device__ __forceinline__ void pin(uint32_t v) { asm volatile("" ::"v"(v)); }
+
 __device__ __forceinline__ float dot8(const uint4& w, const float* x) {
   float f[8];
   unpack8(w, f);

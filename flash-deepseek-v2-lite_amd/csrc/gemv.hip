@@ -7,8 +7,10 @@
 // K <= 2048: one batch of chunks per row (lane l owns chunks l, l+64, l+128, l+192).
 // Grid-stride over groups of RPW rows so at most ~4 workgroups per CU live long enough
 // to keep HBM busy; the next group's weights are requested before the current group is
-// reduced.  x' (normalised when nw != null) is built once per workgroup in LDS while the
-// first group's weights are in flight; residuals are fetched before the dot products.
+// reduced.  x' (normalised when nw != null) is built once per workgroup in LDS.  Every
+// load is unconditional (indices clamped, masked where used) and issued in the order it is
+// consumed -- x and the norm weights, then the weight rows, then the residuals -- since
+// loads complete in issue order: no wait for an early operand waits for the weight stream.
 template <int NB, int RPW, bool SWIGLU>
 __global__ __launch_bounds__(256) void gemv_k2048_kernel(const bf16_t* __restrict__ x, int64_t xs, int B, int K,
                                                          const bf16_t* __restrict__ W, int N,
@@ -25,38 +27,55 @@ __global__ __launch_bounds__(256) void gemv_k2048_kernel(const bf16_t* __restric
   const int tw = gridDim.x * 4;
   int g = blockIdx.x * 4 + wv;
 
+  // thread t owns chunk t of every row (clamped; threads past nch are masked below)
+  const bool own = tid < nch;
+  const int tc = own ? tid : nch - 1;
+  // (no branch around a load -- the wait counts after a conditional load become
+  // conservative: a missing norm / residual operand reads x instead and is ignored)
+  uint4 xv4[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) xv4[b] = ldg16(x + (b < B ? b : 0) * xs + tc * 8);
+  const uint4 g4 = ldg16((nw ? nw : x) + tc * 8);
+
   uint4 wg[U][RPW], wu[U][RPW];
-  auto load = [&](int grp) {
+  bf16_t rvb[RPW][NB];
+  auto load = [&](int grp) {  // the group's residuals (or a harmless read of x), then its weights
+    {
+      const bf16_t* rp = res ? res + grp * RPW : x;
+#pragma unroll
+      for (int r = 0; r < RPW; ++r)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) rvb[r][b] = rp[res ? (b < B ? b : 0) * rs + r : 0];
+    }
     const bf16_t* wr = W + (int64_t)grp * RPW * K;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int c = lane + 64 * u;
-      if (c < nch) {
+      const int c = min(lane + 64 * u, nch - 1);
 #pragma unroll
-        for (int r = 0; r < RPW; ++r) {
-          wg[u][r] = ldg16(wr + (int64_t)r * K + c * 8);
-          if (SWIGLU) wu[u][r] = ldg16(wr + (int64_t)(N + r) * K + c * 8);
-        }
+      for (int r = 0; r < RPW; ++r) {
+        wg[u][r] = ldg16(wr + (int64_t)r * K + c * 8);
+        if (SWIGLU) wu[u][r] = ldg16(wr + (int64_t)(N + r) * K + c * 8);
       }
     }
   };
-  if (g < ngroups) load(g);
+  load(min(g, ngroups - 1));  // unconditional: a wave without a group reloads the last one
+  pin(g4.x);
+#pragma unroll
+  for (int b = 0; b < NB; ++b) pin(xv4[b].x);
 
-  // x' -> LDS (fp32), one pass over x per row; thread t owns chunk t of every row
+  // x' -> LDS (fp32), one pass over x per row
   {
-    const bool own = tid < nch;
     float g8[8];
-    if (nw && own) unpack8(ldg16(nw + tid * 8), g8);
+    if (nw) unpack8(g4, g8);
     float xv[NB][8];
     float ss[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
+      unpack8(xv4[b], xv[b]);
       ss[b] = 0.f;
-      if (b < B && own) {
-        unpack8(ldg16(x + b * xs + tid * 8), xv[b]);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) ss[b] = __builtin_fmaf(xv[b][i], xv[b][i], ss[b]);
-      }
+      for (int i = 0; i < 8; ++i) ss[b] = __builtin_fmaf(xv[b][i], xv[b][i], ss[b]);
+      if (!own) ss[b] = 0.f;
     }
     if (nw) {
 #pragma unroll
@@ -68,10 +87,8 @@ __global__ __launch_bounds__(256) void gemv_k2048_kernel(const bf16_t* __restric
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
         const float rn = rsqrtf((red[b][0] + red[b][1] + red[b][2] + red[b][3]) / static_cast<float>(K) + eps);
-        if (b < B && own) {
 #pragma unroll
-          for (int i = 0; i < 8; ++i) xv[b][i] = rbf(g8[i] * rbf(xv[b][i] * rn));
-        }
+        for (int i = 0; i < 8; ++i) xv[b][i] = rbf(g8[i] * rbf(xv[b][i] * rn));
       }
     }
 #pragma unroll
@@ -94,13 +111,6 @@ __global__ __launch_bounds__(256) void gemv_k2048_kernel(const bf16_t* __restric
   }
   while (g < ngroups) {
     const int n0 = g * RPW;
-    float rv[RPW][NB];
-    if (res && lane == 0) {
-#pragma unroll
-      for (int r = 0; r < RPW; ++r)
-#pragma unroll
-        for (int b = 0; b < NB; ++b) rv[r][b] = b < B ? bf2f(res[b * rs + n0 + r]) : 0.f;
-    }
     float acc[RPW][NB], accu[RPW][NB];
 #pragma unroll
     for (int r = 0; r < RPW; ++r)
@@ -122,8 +132,15 @@ __global__ __launch_bounds__(256) void gemv_k2048_kernel(const bf16_t* __restric
         }
       }
     }
+    float rv[RPW][NB];
+    if (res) {
+#pragma unroll
+      for (int r = 0; r < RPW; ++r)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) rv[r][b] = bf2f(rvb[r][b]);
+    }
     g += tw;
-    if (g < ngroups) load(g);  // next group's weights in flight during the reduction
+    load(min(g, ngroups - 1));  // next group's weights in flight during the reduction
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1)
 #pragma unroll
@@ -178,6 +195,23 @@ __global__ __launch_bounds__(256) void gemv_b1_kernel(const bf16_t* __restrict__
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int n0 = (blockIdx.x * 4 + wv) * RPW;
   if (n0 >= N) return;
+  // x (and the norm weights) are requested before the weight rows: loads complete in issue
+  // order, so the wait for x does not wait for the weight stream behind it.  Every load is
+  // unconditional and converted only where it is used.
+  uint4 xr[4], gr[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) xr[j] = ldg16(x + (lane + 64 * j) * 8);
+  if (NORM) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) gr[j] = ldg16(nw + (lane + 64 * j) * 8);
+  }
+  // residual (or, without one, a harmless read of x), also ahead of the weights
+  bf16_t rvb[RPW];
+  {
+    const bf16_t* rp = res ? res + n0 : x;
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) rvb[r] = rp[res ? r : 0];
+  }
   uint4 wg[RPW][4], wu[RPW][4];
 #pragma unroll
   for (int r = 0; r < RPW; ++r)
@@ -186,18 +220,16 @@ __global__ __launch_bounds__(256) void gemv_b1_kernel(const bf16_t* __restrict__
       wg[r][j] = ldg16(W + (int64_t)(n0 + r) * 2048 + (lane + 64 * j) * 8);
       if (SW) wu[r][j] = ldg16(W + (int64_t)(N + n0 + r) * 2048 + (lane + 64 * j) * 8);
     }
-  float rv[RPW];
-  if (res && lane == 0) {
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) rv[r] = bf2f(res[n0 + r]);
-  }
+  for (int r = 0; r < RPW; ++r) pin(rvb[r]);
+  if (NORM) pin(gr[0].x);
   float xf[32];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) unpack8(ldg16(x + (lane + 64 * j) * 8), xf + 8 * j);
+  for (int j = 0; j < 4; ++j) unpack8(xr[j], xf + 8 * j);
   if (NORM) {
     float g8[32];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) unpack8(ldg16(nw + (lane + 64 * j) * 8), g8 + 8 * j);
+    for (int j = 0; j < 4; ++j) unpack8(gr[j], g8 + 8 * j);
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < 32; ++i) ss = __builtin_fmaf(xf[i], xf[i], ss);
@@ -223,15 +255,21 @@ __global__ __launch_bounds__(256) void gemv_b1_kernel(const bf16_t* __restrict__
       ag[r] += __shfl_xor(ag[r], off, 64);
       if (SW) au[r] += __shfl_xor(au[r], off, 64);
     }
+  // every lane forms the outputs (the residual is consumed in this block, so its load stays
+  // where it was issued, in flight with the weights); lane 0 stores them
+  float v[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const float t = SW ? swiglu_bf(ag[r], au[r]) : rbf(ag[r]);
+    v[r] = res ? rbf(bf2f(rvb[r]) + t) : t;
+  }
   if (lane == 0) {
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
-      float v = SW ? swiglu_bf(ag[r], au[r]) : rbf(ag[r]);
-      if (res) v = rbf(rv[r] + v);
       if (out_f32)
-        reinterpret_cast<float*>(y)[n0 + r] = v;
+        reinterpret_cast<float*>(y)[n0 + r] = v[r];
       else
-        reinterpret_cast<bf16_t*>(y)[n0 + r] = f2bf(v);
+        reinterpret_cast<bf16_t*>(y)[n0 + r] = f2bf(v[r]);
     }
   }
 }
@@ -264,12 +302,13 @@ __global__ __launch_bounds__(256) void gemv_klong_kernel(const bf16_t* __restric
   const int n0 = (blockIdx.x * 4 + wv) * RPW;
   if (n0 >= N) return;
   const bf16_t* wr = W + (int64_t)n0 * K;
-  float rv[RPW][NB];
-  if (res && lane == 0) {
+  bf16_t rvb[RPW][NB];
+  {
+    const bf16_t* rp = res ? res + n0 : x;  // no branch around a load
 #pragma unroll
     for (int r = 0; r < RPW; ++r)
 #pragma unroll
-      for (int b = 0; b < NB; ++b) rv[r][b] = b < B ? bf2f(res[b * rs + n0 + r]) : 0.f;
+      for (int b = 0; b < NB; ++b) rvb[r][b] = rp[res ? (b < B ? b : 0) * rs + r : 0];
   }
   float acc[RPW][NB];
 #pragma unroll
@@ -277,14 +316,16 @@ __global__ __launch_bounds__(256) void gemv_klong_kernel(const bf16_t* __restric
 #pragma unroll
     for (int b = 0; b < NB; ++b) acc[r][b] = 0.f;
   for (int c0 = lane; c0 < nch; c0 += 64 * U) {
-    uint4 wg[U][RPW];
+    // the chunk batch's x and weights all requested before any is used (clamped chunks,
+    // masked below)
+    uint4 wg[U][RPW], xb[U][NB];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int c = c0 + 64 * u;
-      if (c < nch) {
+      const int c = min(c0 + 64 * u, nch - 1);
 #pragma unroll
-        for (int r = 0; r < RPW; ++r) wg[u][r] = ldg16(wr + (int64_t)r * K + c * 8);
-      }
+      for (int b = 0; b < NB; ++b) xb[u][b] = ldg16(x + (b < B ? b : 0) * xs + c * 8);
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) wg[u][r] = ldg16(wr + (int64_t)r * K + c * 8);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -294,7 +335,7 @@ __global__ __launch_bounds__(256) void gemv_klong_kernel(const bf16_t* __restric
       for (int b = 0; b < NB; ++b) {
         if (b < B) {
           float xf[8];
-          unpack8(ldg16(x + b * xs + c * 8), xf);
+          unpack8(xb[u][b], xf);
 #pragma unroll
           for (int r = 0; r < RPW; ++r) acc[r][b] += dot8(wg[u][r], xf);
         }
@@ -315,7 +356,7 @@ __global__ __launch_bounds__(256) void gemv_klong_kernel(const bf16_t* __restric
       for (int r = 0; r < RPW; ++r) {
         const int n = n0 + r;
         float v = rbf(acc[r][b]);
-        if (res) v = rbf(rv[r][b] + v);
+        if (res) v = rbf(bf2f(rvb[r][b]) + v);
         if (out_f32)
           reinterpret_cast<float*>(y)[b * ys + n] = v;
         else

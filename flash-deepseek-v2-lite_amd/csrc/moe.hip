@@ -110,38 +110,16 @@ extern "C" int dsv2_router_topk6_from_logits(const float* logits, int rows, floa
 }
 
 // ---------------------------------------------------------------------------
-// router logits spread over 8 workgroups per token (8 experts each); the softmax +
-// top-6 is done by the consumers (route_gateup_kernel) from the 64 fp32 logits.
-// ---------------------------------------------------------------------------
-// softmax over 64 logits + top-6 (descending, ties -> lower index) in one wave: lane e
-// holds logit e and counts the lanes that beat it (a larger logit, or an equal one at a
-// lower index); the lanes with rank < 6 publish themselves.  Same selection as repeated
-// argmax, without six serial reductions.
-__device__ __forceinline__ void topk6_wave(const float* __restrict__ lg, float scaling, int* ids, float* w) {
-  const int lane = threadIdx.x & 63;
-  const float x = lg[lane];
-  int rank = 0;
-#pragma unroll 16
-  for (int j = 0; j < kE; ++j) {
-    const float xj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), j));
-    rank += (xj > x || (xj == x && j < lane)) ? 1 : 0;
-  }
-  const float mx = wave_max(x);
-  const float ex = expf(x - mx);
-  const float sm = wave_sum(ex);
-  if (rank < kTopK) {
-    ids[rank] = lane;
-    w[rank] = ex / sm * scaling;
-  }
-}
-
 // router logits over 16 workgroups per token (one expert per wave, its 4 KB row requested
 // before the norm); the softmax + top-6 runs in the consumers (route_gateup_kernel).
-// xs: kH floats of LDS, red: 4 floats of LDS (owned by the calling kernel)
-__device__ __forceinline__ void router_logits_block(int b, int part, const bf16_t* __restrict__ h, int64_t hs,
-                                                    const bf16_t* __restrict__ nw, float eps,
-                                                    const bf16_t* __restrict__ wr, bf16_t* __restrict__ xn_out,
-                                                    float* __restrict__ logits, float* xs, float* red) {
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void router_logits_kernel(const bf16_t* __restrict__ h, int64_t hs,
+                                                            const bf16_t* __restrict__ nw, float eps,
+                                                            const bf16_t* __restrict__ wr,
+                                                            bf16_t* __restrict__ xn_out, float* __restrict__ logits) {
+  __shared__ float xs[kH];
+  __shared__ float red[4];
+  const int b = blockIdx.x >> 4, part = blockIdx.x & 15;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int e = part * 4 + wv;
   uint4 wa[4];
@@ -169,33 +147,55 @@ __device__ __forceinline__ void router_logits_block(int b, int part, const bf16_
   if (lane == 0) logits[(int64_t)b * kE + e] = acc;
 }
 
+extern "C" int dsv2_router_logits(const void* h, int64_t h_stride, const void* norm_w, float eps,
+                                  const void* w_router, int rows, void* xn_out, float* logits, void* stream) {
+  DSV2_REQUIRE(h && norm_w && w_router && logits, DSV2_E_NULL, "router_logits: null pointer");
+  DSV2_REQUIRE(rows >= 0 && rows <= 0x7fffffff / kE, DSV2_E_SHAPE, "router_logits: bad rows");
+  DSV2_REQUIRE(dsv2_aligned16(h) && h_stride % 8 == 0 && dsv2_aligned16(norm_w) && dsv2_aligned16(w_router) &&
+                   (!xn_out || dsv2_aligned16(xn_out)),
+               DSV2_E_ALIGN, "router_logits: alignment");
+  if (rows == 0) return DSV2_OK;
+  hipLaunchKernelGGL(router_logits_kernel, dim3(rows * 16), dim3(256), 0, (hipStream_t)stream, (const bf16_t*)h,
+                     h_stride, (const bf16_t*)norm_w, eps, (const bf16_t*)w_router, (bf16_t*)xn_out, logits);
+  return dsv2_launch_status("router_logits");
+}
 
 // ---------------------------------------------------------------------------
-// small family: route-local gate_up + SwiGLU.  grid (inter/(4*RPW), rows*NR)
-// route r*NR+s: s < 6 -> routed expert ids[r,s]; s = 6, 7 -> shared-expert half.
+// small family: route-local gate_up + SwiGLU.  One workgroup per (route, block of 4*RPW
+// output rows); route r: row b = r / nr, slot s = r % nr (s < 6: routed expert, s = 6, 7:
+// the shared-expert halves), output row (b * hbuf_routes + s) of hbuf.  Each wave owns RPW
+// gate rows and the RPW matching up rows, all requested at once; the row's x is staged in
+// LDS once per workgroup.  Only the gate_up body lives in this kernel, so its register
+// budget lets every workgroup of a bsz=1 launch be resident at once on MI355X.
 // ---------------------------------------------------------------------------
+struct RouteGateupArgs {
+  int gu_blocks, nr, hbuf_routes, inter;
+  const bf16_t* xn;
+  int32_t* ids;          // [rows, 6]: read (logits == null) or written (logits != null)
+  const float* logits;   // non-null: the row's fp32 router logits, ranked here
+  float scaling;
+  float* wts;            // written with ids when logits != null
+  const bf16_t* wgu;
+  const bf16_t* shgu;
+  bf16_t* hbuf;
+};
+
+// 6 waves per SIMD: all 1408 workgroups of a bsz=1 launch (8 routes x 176) resident together
 template <int RPW>
-__device__ __forceinline__ void route_gateup_block(int bx, int route, const bf16_t* __restrict__ xn,
-                                                   int32_t* __restrict__ ids, int nr, int s_off, int hbuf_routes,
-                                                   const float* __restrict__ logits, float scaling,
-                                                   float* __restrict__ wts, const bf16_t* __restrict__ h, int64_t hs,
-                                                   const bf16_t* __restrict__ nw, float eps,
-                                                   const bf16_t* __restrict__ wgu, const bf16_t* __restrict__ shgu,
-                                                   int inter, bf16_t* __restrict__ hbuf) {
-  // route r = blockIdx.y: row b = r / nr, route slot s = r % nr + s_off (s < 6 routed,
-  // s = 6, 7 the shared-expert halves); output row (b * hbuf_routes + s) of hbuf.
-  // With h != null the input is RMSNorm(h; nw) computed here (each wave from its own
-  // chunks), so shared-expert launches need nothing from the router.
-  const int b = route / nr, s = route % nr + s_off;
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) void route_gateup_kernel(
+    const RouteGateupArgs a) {
+  __shared__ float xs[kH];
+  const int bx = blockIdx.x % a.gu_blocks, route = blockIdx.x / a.gu_blocks;
+  const int b = route / a.nr, s = route % a.nr;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int i0 = (bx * 4 + wv) * RPW;
   int e = 0;
-  if (s < kTopK && logits) {
+  if (s < kTopK && a.logits) {
     // every wave ranks the 64 logits itself (no LDS, no barrier): lane j holds logit j,
     // rank = number of lanes with a larger logit or an equal one at a lower index;
     // route slot s takes the lane of rank s (softmax is monotonic, so this is the top-6
     // of the router scores, descending, ties to the lower index)
-    const float x = logits[(int64_t)b * kE + lane];
+    const float x = a.logits[(int64_t)b * kE + lane];
     int rank = 0;
 #pragma unroll 16
     for (int j = 0; j < kE; ++j) {
@@ -209,192 +209,77 @@ __device__ __forceinline__ void route_gateup_block(int bx, int route, const bf16
       const float ex = expf(x - mx);
       const float sm = wave_sum(ex);
       if (rank < kTopK) {
-        ids[b * kTopK + rank] = lane;
-        wts[b * kTopK + rank] = ex / sm * scaling;
+        a.ids[b * kTopK + rank] = lane;
+        a.wts[b * kTopK + rank] = ex / sm * a.scaling;
       }
     }
   } else if (s < kTopK) {
-    e = min(max(ids[b * kTopK + s], 0), kE - 1);
+    e = min(max(a.ids[b * kTopK + s], 0), kE - 1);
   }
-  if (i0 >= inter) return;
-  const bf16_t *gp, *up;
-  if (s < kTopK) {
-    gp = wgu + (int64_t)e * 2 * inter * kH;
-    up = gp + (int64_t)inter * kH;
-  } else {
-    const int half = s - kTopK;
-    gp = shgu + (int64_t)half * inter * kH;
-    up = shgu + (int64_t)(2 * inter + half * inter) * kH;
-  }
-  gp += (int64_t)i0 * kH;
-  up += (int64_t)i0 * kH;
+  const bool live = i0 < a.inter;  // inter % RPW == 0: a live wave owns RPW whole rows
   uint4 wg[RPW][4], wu[RPW][4];
-#pragma unroll
-  for (int r = 0; r < RPW; ++r)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      wg[r][j] = ldg16(gp + (int64_t)r * kH + (lane + 64 * j) * 8);
-      wu[r][j] = ldg16(up + (int64_t)r * kH + (lane + 64 * j) * 8);
+  if (live) {
+    const bf16_t *gp, *up;
+    if (s < kTopK) {
+      gp = a.wgu + (int64_t)e * 2 * a.inter * kH;
+      up = gp + (int64_t)a.inter * kH;
+    } else {
+      const int half = s - kTopK;
+      gp = a.shgu + (int64_t)half * a.inter * kH;
+      up = a.shgu + (int64_t)(2 * a.inter + half * a.inter) * kH;
     }
-  float xf[32];
-  if (h) {
-    float g8[32];
-    float ss = 0.f;
+    gp += (int64_t)i0 * kH;
+    up += (int64_t)i0 * kH;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      unpack8(ldg16(h + b * hs + (lane + 64 * j) * 8), xf + j * 8);
-      unpack8(ldg16(nw + (lane + 64 * j) * 8), g8 + j * 8);
-    }
+    for (int r = 0; r < RPW; ++r)
 #pragma unroll
-    for (int i = 0; i < 32; ++i) ss = __builtin_fmaf(xf[i], xf[i], ss);
-    ss = wave_sum(ss);
-    const float rn = rsqrtf(ss / static_cast<float>(kH) + eps);
-#pragma unroll
-    for (int i = 0; i < 32; ++i) xf[i] = rbf(g8[i] * rbf(xf[i] * rn));
-  } else {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) unpack8(ldg16(xn + (int64_t)b * kH + (lane + 64 * j) * 8), xf + j * 8);
+      for (int j = 0; j < 4; ++j) {
+        wg[r][j] = ldg16(gp + (int64_t)r * kH + (lane + 64 * j) * 8);
+        wu[r][j] = ldg16(up + (int64_t)r * kH + (lane + 64 * j) * 8);
+      }
   }
+  {
+    float f[8];
+    unpack8(ldg16(a.xn + (int64_t)b * kH + tid * 8), f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xs[tid * 8 + i] = f[i];
+  }
+  __syncthreads();
+  if (!live) return;
   float ag[RPW], au[RPW];
 #pragma unroll
-  for (int r = 0; r < RPW; ++r) {
-    ag[r] = au[r] = 0.f;
+  for (int r = 0; r < RPW; ++r) ag[r] = au[r] = 0.f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      ag[r] += dot8(wg[r][j], xf + j * 8);
-      au[r] += dot8(wu[r][j], xf + j * 8);
+  for (int j = 0; j < 4; ++j) {
+    const float* xl = &xs[(lane + 64 * j) * 8];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      ag[r] += dot8(wg[r][j], xl);
+      au[r] += dot8(wu[r][j], xl);
     }
-    ag[r] = wave_sum(ag[r]);
-    au[r] = wave_sum(au[r]);
   }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1)
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      ag[r] += __shfl_xor(ag[r], off, 64);
+      au[r] += __shfl_xor(au[r], off, 64);
+    }
   if (lane == 0) {
 #pragma unroll
     for (int r = 0; r < RPW; ++r)
-      hbuf[((int64_t)b * hbuf_routes + s) * inter + i0 + r] = f2bf(swiglu_bf(ag[r], au[r]));
+      a.hbuf[((int64_t)b * a.hbuf_routes + s) * a.inter + i0 + r] = f2bf(swiglu_bf(ag[r], au[r]));
   }
 }
 
-// shared-expert down projection, one wave per output row j of token b:
-// shared_y[b, j] = bf16(hbuf[b, 6:8, :] . sh_down[j, :])   (K = 2 * inter)
-__device__ __forceinline__ void shared_down_block(int blk, int b, const bf16_t* __restrict__ hbuf,
-                                                  const bf16_t* __restrict__ shd, int inter,
-                                                  bf16_t* __restrict__ shared_y) {
-  constexpr int kMaxCh = 6;  // ceil(2 * 1408 / 8 / 64)
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int j = blk * 4 + wv;
-  const int K = 2 * inter, nch = K >> 3;
-  const bf16_t* w = shd + (int64_t)j * K;
-  const bf16_t* x = hbuf + ((int64_t)b * (kTopK + 2) + kTopK) * inter;
-  const uint4 zero = {0u, 0u, 0u, 0u};
-  uint4 wv4[kMaxCh], xv4[kMaxCh];
-#pragma unroll
-  for (int k = 0; k < kMaxCh; ++k) {
-    const int c = lane + 64 * k;
-    wv4[k] = c < nch ? ldg16(w + c * 8) : zero;
-    xv4[k] = c < nch ? ldg16(x + c * 8) : zero;
-  }
-  float a = 0.f;
-#pragma unroll
-  for (int k = 0; k < kMaxCh; ++k) {
-    float xf[8];
-    unpack8(xv4[k], xf);
-    a += dot8(wv4[k], xf);
-  }
-  a = wave_sum(a);
-  if (lane == 0) shared_y[(int64_t)b * kH + j] = f2bf(a);
-}
-
-// The MoE "gate" kernels.  Workgroup ranges, in dispatch order:
-//   [0, n_router)              router logits, 16 workgroups per token
-//   [n_router, + n_gate)       gate_up + SwiGLU, gu_blocks workgroups per (token, route)
-//   [.., + n_sdown)            shared-expert down, 512 workgroups per token
-// The router entry point launches router_logits_kernel (gate ranges empty), the route-local
-// gate_up entry points launch route_gateup_kernel (router range empty).
-struct MoeGateArgs {
-  int n_router, n_gate, n_sdown;
-  // router
-  const bf16_t* h;
-  int64_t hs;
-  const bf16_t* nw;
-  float eps;
-  const bf16_t* wr;
-  bf16_t* xn_out;
-  float* logits_out;
-  // gate_up
-  int gu_blocks, nr, s_off, hbuf_routes;
-  const bf16_t* xn;
-  int32_t* ids;
-  const float* logits_in;
-  float scaling;
-  float* wts;
-  const bf16_t* gate_h;  // non-null: the gate_up input is RMSNorm(gate_h; nw) (shared halves)
-  const bf16_t* wgu;
-  const bf16_t* shgu;
-  int inter;
-  bf16_t* hbuf;
-  // shared down
-  const bf16_t* shd;
-  bf16_t* shared_y;
-};
-
-__device__ __forceinline__ void moe_gate_body(const MoeGateArgs& a, int v, float* xs, float* red) {
-  if (v < a.n_router) {
-    router_logits_block(v >> 4, v & 15, a.h, a.hs, a.nw, a.eps, a.wr, a.xn_out, a.logits_out, xs, red);
-    return;
-  }
-  v -= a.n_router;
-  if (v < a.n_gate) {
-    route_gateup_block<kGateRPW>(v % a.gu_blocks, v / a.gu_blocks, a.xn, a.ids, a.nr, a.s_off, a.hbuf_routes, a.logits_in,
-                          a.scaling, a.wts, a.gate_h, a.hs, a.nw, a.eps, a.wgu, a.shgu, a.inter, a.hbuf);
-    return;
-  }
-  v -= a.n_gate;
-  shared_down_block(v % (kH / 4), v / (kH / 4), a.hbuf, a.shd, a.inter, a.shared_y);
-}
-
-// Two entry symbols over the same body so that profiles name the router launch and the
-// gate_up launch apart.
-__global__ __launch_bounds__(256) void router_logits_kernel(const MoeGateArgs a) {
-  __shared__ float xs[kH];
-  __shared__ float red[4];
-  moe_gate_body(a, blockIdx.x, xs, red);
-}
-
-__global__ __launch_bounds__(256) void route_gateup_kernel(const MoeGateArgs a) {
-  __shared__ float xs[kH];
-  __shared__ float red[4];
-  moe_gate_body(a, blockIdx.x, xs, red);
-}
-
-static int launch_moe_gate(const MoeGateArgs& a, hipStream_t st, const char* what) {
-  const int64_t grid = (int64_t)a.n_router + a.n_gate + a.n_sdown;
+static int launch_route_gateup(RouteGateupArgs& a, int rows, hipStream_t st, const char* what) {
+  constexpr int RPW = kGateRPW;
+  DSV2_REQUIRE(a.inter % RPW == 0, DSV2_E_SHAPE, "%s: inter %% %d required", what, RPW);
+  a.gu_blocks = (a.inter + 4 * RPW - 1) / (4 * RPW);
+  const int64_t grid = (int64_t)rows * a.nr * a.gu_blocks;
   DSV2_REQUIRE(grid <= 0x7fffffff, DSV2_E_SHAPE, "%s: too many rows", what);
-  if (grid == 0) return DSV2_OK;
-  if (a.n_router)
-    hipLaunchKernelGGL(router_logits_kernel, dim3((unsigned)grid), dim3(256), 0, st, a);
-  else
-    hipLaunchKernelGGL(route_gateup_kernel, dim3((unsigned)grid), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(route_gateup_kernel<RPW>, dim3((unsigned)grid), dim3(256), 0, st, a);
   return dsv2_launch_status(what);
-}
-
-extern "C" int dsv2_router_logits(const void* h, int64_t h_stride, const void* norm_w, float eps,
-                                  const void* w_router, int rows, void* xn_out, float* logits, void* stream) {
-  DSV2_REQUIRE(h && norm_w && w_router && logits, DSV2_E_NULL, "router_logits: null pointer");
-  DSV2_REQUIRE(rows >= 0 && rows <= 0x7fffffff / kE, DSV2_E_SHAPE, "router_logits: bad rows");
-  DSV2_REQUIRE(dsv2_aligned16(h) && h_stride % 8 == 0 && dsv2_aligned16(norm_w) && dsv2_aligned16(w_router) &&
-                   (!xn_out || dsv2_aligned16(xn_out)),
-               DSV2_E_ALIGN, "router_logits: alignment");
-  if (rows == 0) return DSV2_OK;
-  MoeGateArgs a{};
-  a.n_router = rows * 16;
-  a.h = (const bf16_t*)h;
-  a.hs = h_stride;
-  a.nw = (const bf16_t*)norm_w;
-  a.eps = eps;
-  a.wr = (const bf16_t*)w_router;
-  a.xn_out = (bf16_t*)xn_out;
-  a.logits_out = logits;
-  return launch_moe_gate(a, (hipStream_t)stream, "router_logits");
 }
 
 extern "C" int dsv2_moe_route_gateup(const void* xn, int rows, const int32_t* ids, const void* w_gate_up,
@@ -406,23 +291,17 @@ extern "C" int dsv2_moe_route_gateup(const void* xn, int rows, const int32_t* id
   DSV2_REQUIRE(dsv2_aligned16(xn) && dsv2_aligned16(w_gate_up) && (!sh_gate_up || dsv2_aligned16(sh_gate_up)),
                DSV2_E_ALIGN, "moe_route_gateup: alignment");
   if (rows == 0) return DSV2_OK;
-  constexpr int RPW = kGateRPW;
-  MoeGateArgs a{};
-  a.gu_blocks = (inter + 4 * RPW - 1) / (4 * RPW);
-  a.n_gate = rows * nr * a.gu_blocks;
+  RouteGateupArgs a{};
   a.nr = nr;
   a.hbuf_routes = nr;
+  a.inter = inter;
   a.xn = (const bf16_t*)xn;
   a.ids = const_cast<int32_t*>(ids);
   a.wgu = (const bf16_t*)w_gate_up;
   a.shgu = (const bf16_t*)sh_gate_up;
-  a.inter = inter;
   a.hbuf = (bf16_t*)hbuf;
-  return launch_moe_gate(a, (hipStream_t)stream, "moe_route_gateup");
+  return launch_route_gateup(a, rows, (hipStream_t)stream, "moe_route_gateup");
 }
-
-
-
 
 extern "C" int dsv2_moe_route_gateup_logits(const void* xn, int rows, const float* logits, float scaling,
                                             int32_t* ids, float* weights, const void* w_gate_up,
@@ -435,22 +314,19 @@ extern "C" int dsv2_moe_route_gateup_logits(const void* xn, int rows, const floa
   DSV2_REQUIRE(dsv2_aligned16(xn) && dsv2_aligned16(w_gate_up) && (!sh_gate_up || dsv2_aligned16(sh_gate_up)),
                DSV2_E_ALIGN, "moe_route_gateup_logits: alignment");
   if (rows == 0) return DSV2_OK;
-  constexpr int RPW = kGateRPW;
-  MoeGateArgs a{};
-  a.gu_blocks = (inter + 4 * RPW - 1) / (4 * RPW);
-  a.n_gate = rows * nr * a.gu_blocks;
+  RouteGateupArgs a{};
   a.nr = nr;
   a.hbuf_routes = kTopK + 2;
+  a.inter = inter;
   a.xn = (const bf16_t*)xn;
   a.ids = ids;
-  a.logits_in = logits;
+  a.logits = logits;
   a.scaling = scaling;
   a.wts = weights;
   a.wgu = (const bf16_t*)w_gate_up;
   a.shgu = (const bf16_t*)sh_gate_up;
-  a.inter = inter;
   a.hbuf = (bf16_t*)hbuf;
-  return launch_moe_gate(a, (hipStream_t)stream, "moe_route_gateup_logits");
+  return launch_route_gateup(a, rows, (hipStream_t)stream, "moe_route_gateup_logits");
 }
 
 // ---------------------------------------------------------------------------
@@ -472,9 +348,17 @@ __global__ __launch_bounds__(256) void route_down_kernel(const bf16_t* __restric
   const int j0 = blockIdx.x * 2;
   const int nch = inter >> 3;
   constexpr int kMaxCh = 3;  // chunks per lane: ceil(176 / 64) for inter = 1408
-  // the residual is requested up front, not after the dot products
-  const float resv = (res && threadIdx.x < 2) ? bf2f(res[(int64_t)b * kH + j0 + threadIdx.x]) : 0.f;
-  const float shv = (shared_y && threadIdx.x < 2) ? bf2f(shared_y[(int64_t)b * kH + j0 + threadIdx.x]) : 0.f;
+  // Loads are issued in dependency order with no wait between independent ones: both
+  // routes' expert ids (slots clamped), the residual / shared output (pinned, so they stay
+  // ahead of the weights), then every weight and hbuf chunk (chunk indices clamped, masked
+  // where used).
+  int eid[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) eid[q] = ids[b * kTopK + min(2 * wv + q, kTopK - 1)];
+  const int jr = j0 + (threadIdx.x & 1);
+  bf16_t resb = 0, shb = 0;
+  resb = (res ? res : hbuf)[res ? (int64_t)b * kH + jr : 0];
+  shb = (shared_y ? shared_y : hbuf)[shared_y ? (int64_t)b * kH + jr : 0];
   if (2 * wv < NR) {
     const bf16_t* wrow[2];
     int64_t wstride[2];
@@ -482,26 +366,26 @@ __global__ __launch_bounds__(256) void route_down_kernel(const bf16_t* __restric
     for (int q = 0; q < 2; ++q) {
       const int s = 2 * wv + q;
       if (s < kTopK) {
-        wrow[q] = wd + (int64_t)min(max(ids[b * kTopK + s], 0), kE - 1) * kH * inter + (int64_t)j0 * inter;
+        wrow[q] = wd + (int64_t)min(max(eid[q], 0), kE - 1) * kH * inter + (int64_t)j0 * inter;
         wstride[q] = inter;
       } else {
         wrow[q] = shd + (int64_t)(s - kTopK) * inter + (int64_t)j0 * 2 * inter;
         wstride[q] = 2 * inter;
       }
     }
-    const uint4 zero = {0u, 0u, 0u, 0u};
     uint4 w[2][2][kMaxCh], x[2][kMaxCh];
 #pragma unroll
     for (int k = 0; k < kMaxCh; ++k) {
-      const int c = lane + 64 * k;
-      const bool ok = c < nch;
+      const int c = min(lane + 64 * k, nch - 1);
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
-        x[q][k] = ok ? ldg16(hbuf + ((int64_t)b * hbuf_routes + 2 * wv + q) * inter + c * 8) : zero;
+        x[q][k] = ldg16(hbuf + ((int64_t)b * hbuf_routes + 2 * wv + q) * inter + c * 8);
 #pragma unroll
-        for (int r = 0; r < 2; ++r) w[q][r][k] = ok ? ldg16(wrow[q] + r * wstride[q] + c * 8) : zero;
+        for (int r = 0; r < 2; ++r) w[q][r][k] = ldg16(wrow[q] + r * wstride[q] + c * 8);
       }
     }
+    pin(resb);
+    pin(shb);
     float acc[2][2];
 #pragma unroll
     for (int q = 0; q < 2; ++q)
@@ -512,7 +396,8 @@ __global__ __launch_bounds__(256) void route_down_kernel(const bf16_t* __restric
         for (int k = 0; k < kMaxCh; ++k) {
           float hx[8];
           unpack8(x[q][k], hx);
-          a += dot8(w[q][r][k], hx);
+          const float d = dot8(w[q][r][k], hx);
+          a += lane + 64 * k < nch ? d : 0.f;
         }
         acc[q][r] = a;
       }
@@ -533,7 +418,8 @@ __global__ __launch_bounds__(256) void route_down_kernel(const bf16_t* __restric
   if (threadIdx.x < 2) {
     const int r = threadIdx.x;
     float routed = 0.f;
-    const float rv = res ? resv : 0.f;
+    const float rv = res ? bf2f(resb) : 0.f;
+    const float shv = shared_y ? bf2f(shb) : 0.f;
 #pragma unroll
     for (int s = 0; s < kTopK; ++s) routed += wts[b * kTopK + s] * rbf(part[s][r]);
     float y = rbf(routed);
