@@ -180,72 +180,94 @@ struct RouteGateupArgs {
   bf16_t* hbuf;
 };
 
+// Expert of routed slot s < 6 from the row's 64 fp32 router logits (lane j holds logit j):
+// the lane whose rank -- the number of lanes with a larger logit, or an equal one at a lower
+// index -- is s (softmax is monotonic, so rank order is the router's top-6 order, ties to
+// the lower index).  Fast path: count only the strictly larger logits; when exactly one lane
+// has count s there is no tie at rank s and that lane is the answer.  Otherwise (ties) the
+// exact count decides.
+__device__ __forceinline__ int routed_expert(float x, int s) {
+  const int lane = threadIdx.x & 63;
+  int gt = 0;
+#pragma unroll 16
+  for (int j = 0; j < kE; ++j) gt += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), j)) > x ? 1 : 0;
+  const unsigned long long m = __ballot(gt == s);
+  if (__popcll(m) == 1) return __ffsll(m) - 1;
+  int rank = 0;
+  for (int j = 0; j < kE; ++j) {
+    const float xj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), j));
+    rank += (xj > x || (xj == x && j < lane)) ? 1 : 0;
+  }
+  return __ffsll(__ballot(rank == s)) - 1;
+}
+
 // 6 waves per SIMD: all 1408 workgroups of a bsz=1 launch (8 routes x 176) resident together
 template <int RPW>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) void route_gateup_kernel(
     const RouteGateupArgs a) {
   __shared__ float xs[kH];
+  __shared__ int eid;
   const int bx = blockIdx.x % a.gu_blocks, route = blockIdx.x / a.gu_blocks;
   const int b = route / a.nr, s = route % a.nr;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int i0 = (bx * 4 + wv) * RPW;
-  int e = 0;
-  if (s < kTopK && a.logits) {
-    // every wave ranks the 64 logits itself (no LDS, no barrier): lane j holds logit j,
-    // rank = number of lanes with a larger logit or an equal one at a lower index;
-    // route slot s takes the lane of rank s (softmax is monotonic, so this is the top-6
-    // of the router scores, descending, ties to the lower index)
-    const float x = a.logits[(int64_t)b * kE + lane];
-    int rank = 0;
-#pragma unroll 16
-    for (int j = 0; j < kE; ++j) {
-      const float xj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), j));
-      rank += (xj > x || (xj == x && j < lane)) ? 1 : 0;
-    }
-    const unsigned long long m = __ballot(rank == s);
-    e = __ffsll(m) - 1;
-    if (bx == 0 && s == 0 && wv == 0) {
-      const float mx = wave_max(x);
-      const float ex = expf(x - mx);
-      const float sm = wave_sum(ex);
-      if (rank < kTopK) {
-        a.ids[b * kTopK + rank] = lane;
-        a.wts[b * kTopK + rank] = ex / sm * a.scaling;
+  // x first (it does not depend on the routing), then the logits
+  const uint4 x4 = ldg16(a.xn + (int64_t)b * kH + tid * 8);
+  if (wv == 0) {
+    int e = 0;
+    if (s < kTopK && a.logits) {
+      // one wave per workgroup ranks the logits; the route's first workgroup also
+      // publishes the row's ids and softmax weights
+      const float x = a.logits[(int64_t)b * kE + lane];
+      e = routed_expert(x, s);
+      if (bx == 0 && s == 0) {
+        int rank = 0;
+        for (int j = 0; j < kE; ++j) {
+          const float xj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), j));
+          rank += (xj > x || (xj == x && j < lane)) ? 1 : 0;
+        }
+        const float mx = wave_max(x);
+        const float ex = expf(x - mx);
+        const float sm = wave_sum(ex);
+        if (rank < kTopK) {
+          a.ids[b * kTopK + rank] = lane;
+          a.wts[b * kTopK + rank] = ex / sm * a.scaling;
+        }
       }
+    } else if (s < kTopK) {
+      e = min(max(a.ids[b * kTopK + s], 0), kE - 1);
     }
-  } else if (s < kTopK) {
-    e = min(max(a.ids[b * kTopK + s], 0), kE - 1);
-  }
-  const bool live = i0 < a.inter;  // inter % RPW == 0: a live wave owns RPW whole rows
-  uint4 wg[RPW][4], wu[RPW][4];
-  if (live) {
-    const bf16_t *gp, *up;
-    if (s < kTopK) {
-      gp = a.wgu + (int64_t)e * 2 * a.inter * kH;
-      up = gp + (int64_t)a.inter * kH;
-    } else {
-      const int half = s - kTopK;
-      gp = a.shgu + (int64_t)half * a.inter * kH;
-      up = a.shgu + (int64_t)(2 * a.inter + half * a.inter) * kH;
-    }
-    gp += (int64_t)i0 * kH;
-    up += (int64_t)i0 * kH;
-#pragma unroll
-    for (int r = 0; r < RPW; ++r)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        wg[r][j] = ldg16(gp + (int64_t)r * kH + (lane + 64 * j) * 8);
-        wu[r][j] = ldg16(up + (int64_t)r * kH + (lane + 64 * j) * 8);
-      }
+    if (lane == 0) eid = e;
   }
   {
     float f[8];
-    unpack8(ldg16(a.xn + (int64_t)b * kH + tid * 8), f);
+    unpack8(x4, f);
 #pragma unroll
     for (int i = 0; i < 8; ++i) xs[tid * 8 + i] = f[i];
   }
   __syncthreads();
+  const int e = eid;
+  const bool live = i0 < a.inter;  // inter % RPW == 0: a live wave owns RPW whole rows
   if (!live) return;
+  const bf16_t *gp, *up;
+  if (s < kTopK) {
+    gp = a.wgu + (int64_t)e * 2 * a.inter * kH;
+    up = gp + (int64_t)a.inter * kH;
+  } else {
+    const int half = s - kTopK;
+    gp = a.shgu + (int64_t)half * a.inter * kH;
+    up = a.shgu + (int64_t)(2 * a.inter + half * a.inter) * kH;
+  }
+  gp += (int64_t)i0 * kH;
+  up += (int64_t)i0 * kH;
+  uint4 wg[RPW][4], wu[RPW][4];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      wg[r][j] = ldg16(gp + (int64_t)r * kH + (lane + 64 * j) * 8);
+      wu[r][j] = ldg16(up + (int64_t)r * kH + (lane + 64 * j) * 8);
+    }
   float ag[RPW], au[RPW];
 #pragma unroll
   for (int r = 0; r < RPW; ++r) ag[r] = au[r] = 0.f;

@@ -554,6 +554,36 @@ def test_router_logits_split_and_gateup_topk(rows):
     assert torch.equal(hb, hb2)
 
 
+def test_route_gateup_logits_exact_ties():
+    """Planted exact ties inside the top-6 (rank 0/1 and rank 3/4) and at the rank-5/6 edge:
+    every routed slot must take the lower index first, in the published ids and in the
+    expert each gate_up workgroup streams (compared with the ids-driven entry point)."""
+    rows = 2
+    g = torch.Generator().manual_seed(321)
+    lg = torch.randn(rows, 64, generator=g).float()
+    lg[0, 40] = lg[0, 9] = 9.0          # ranks 0 and 1: 9 before 40
+    lg[0, 50] = lg[0, 2] = 5.0          # ranks 3 and 4 (after 3 larger ones below)
+    lg[0, 33] = 7.0
+    lg[1, 63] = lg[1, 0] = lg[1, 31] = 4.0  # a three-way tie across the rank-5/6 edge
+    lg[1, 1:6] = torch.tensor([8.0, 7.5, 7.0, 6.5, 6.0])
+    lg = lg.to(DEV)
+    xn = rnd(rows, 2048, seed=322)
+    gu, _, sgu, _ = _moe_layer(323)
+    ids = torch.full((rows, 6), -1, dtype=torch.int32, device=DEV)
+    w = torch.empty(rows, 6, dtype=torch.float32, device=DEV)
+    hb = torch.empty(rows, 8, 1408, dtype=BF, device=DEV)
+    call("dsv2_moe_route_gateup_logits", xn.data_ptr(), rows, lg.data_ptr(), 1.0, ids.data_ptr(), w.data_ptr(),
+         gu.data_ptr(), sgu.data_ptr(), 1408, hb.data_ptr(), st())
+    lc = lg.cpu()
+    ref_ids = torch.stack([torch.tensor(sorted(range(64), key=lambda e: (-float(lc[r, e]), e))[:6]) for r in range(rows)])
+    assert ref_ids[0, :2].tolist() == [9, 40] and ref_ids[1, 5].item() == 0
+    assert torch.equal(ids.cpu().long(), ref_ids)
+    hb2 = torch.empty_like(hb)
+    call("dsv2_moe_route_gateup", xn.data_ptr(), rows, ids.data_ptr(), gu.data_ptr(), sgu.data_ptr(), 1408,
+         hb2.data_ptr(), st())
+    assert torch.equal(hb, hb2)
+
+
 @pytest.mark.parametrize("rows", [1, 2, 5])
 def test_lm_head_argmax_matches_gemv_then_argmax(rows):
     x = rnd(rows, 2048, seed=99)
