@@ -10,7 +10,9 @@ whole step replayed as one hipGraph.  Prints ONE JSON line.
 Extra fields:
   roofline      -- dominant kernel of the step: algorithmic bytes per launch /
                    average launch time (HIP events around a graph of repeated
-                   launches on the engine's stream) vs 8 TB/s.
+                   launches on the engine's stream) vs 8 TB/s; traffic = HBM bytes
+                   per launch from the committed PMC summary profiles/traffic_c<N>.json
+                   (see --pmc-traffic), null when absent.
   step_roofline -- algorithmic bytes per step (weights of the experts actually hit,
                    counted from the router output, + compressed KV read) / step time.
   cpu_baseline  -- the CPU oracle (PyTorch eager restatement of the HF math) timed on
@@ -49,7 +51,9 @@ CONFIGS = {
 
 
 def step_bytes(cfg, n_exp_per_layer: list[int], ctx_sum_per_layer: float, batch: int) -> float:
-    """Algorithmic HBM bytes of one decode step (BASELINE.md section 2 byte model)."""
+    """Algorithmic HBM bytes of one decode step: every weight read once (attention,
+    router, the experts actually hit, shared experts, dense layer 0, lm_head, norms), the
+    new cache rows written and the compressed KV rows read (1,152 B per token per layer)."""
     attn_w = 2048 * 3648 + 512 * 4096 + 2048 * 2048  # 13,762,560 elements per layer
     expert = 3 * 2048 * 1408  # 8,650,752
     shared = 3 * 2048 * 2816  # 17,301,504
@@ -71,14 +75,16 @@ def time_dominant_kernel(eng, family: str, reps: int = 4) -> dict:
     moe_layers = [L for L in eng.w.layers if L.moe]
     B = eng.B
     if family == "small":
-        name = "route_gateup_kernel (small-family MoE gate_up+SwiGLU, 6 routed + 2 shared halves)"
+        name = "route_gateup_kernel<2> (small-family MoE gate_up+SwiGLU, 6 routed + 2 shared halves)"
         bytes_per = B * 8 * 2 * c.moe_inter * c.hidden * 2 + B * 8 * c.moe_inter * 2
 
         def launch(L):
             call("dsv2_moe_route_gateup", ptr(b.xn), B, ptr(b.ids32), ptr(L.w_gu), ptr(L.sh_gu), c.moe_inter,
                  ptr(b.hbuf), stream_ptr())
     else:
-        name = "gemm_kernel<swiglu> via dsv2_moe_grouped_gateup (expert-grouped gate_up+SwiGLU on MFMA)"
+        tb = {16: 1, 32: 2, 64: 4}[b.tile_tokens]
+        sym = f"gemm_xlds_kernel<{tb}, true, {2 if tb == 4 else 4}, {'false' if tb == 4 else 'true'}, 2>"
+        name = f"{sym} via dsv2_moe_grouped_gateup (expert-grouped gate_up+SwiGLU on MFMA, {b.tile_tokens}-token tiles)"
         n_exp = int(torch.unique(b.ids32[:B]).numel())
         bytes_per = n_exp * 2 * c.moe_inter * c.hidden * 2 + B * 6 * c.moe_inter * 2
 
@@ -106,6 +112,106 @@ def time_dominant_kernel(eng, family: str, reps: int = 4) -> dict:
     ach = bytes_per / avg_s
     return {"kernel": name, "bound": "hbm", "achieved": ach / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
             "frac": ach / HBM_PEAK, "traffic": None, "bytes_per_launch": bytes_per, "avg_us": avg_s * 1e6}
+
+
+def measured_traffic(config: int, kernel: str):
+    """HBM bytes per launch of the dominant kernel from the committed PMC summary
+    (profiles/traffic_c<config>.json, written by --pmc-traffic), or None when that summary
+    is missing or covers another kernel."""
+    path = os.path.join(ROOT, "profiles", f"traffic_c{config}.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if not kernel.startswith(t.get("kernel_symbol", "\0")):
+        return None
+    return t.get("traffic_bytes_per_dispatch")
+
+
+def _csv_rows(path: str):
+    import csv
+    with open(path, newline="") as f:
+        yield from csv.DictReader(f)
+
+
+def pmc_traffic(fetch_csv: str, write_csv: str, kernel: str, copy_bytes: int, out: str, command: str) -> dict:
+    """Scale the FETCH_SIZE / WRITE_SIZE counters (KiB per dispatch) of the dominant kernel by
+    what the same counters read for a plain device copy of copy_bytes (the --copy-calibration
+    copies of the profiled run): bytes = counter * copy_bytes / counter(copy)."""
+    def per_kernel(path: str):
+        vals, copies = [], []
+        for r in sorted(_csv_rows(path), key=lambda r: int(r["Dispatch_Id"])):
+            name = r["Kernel_Name"].replace("void ", "")
+            v = float(r["Counter_Value"])
+            if name.startswith(kernel):
+                vals.append(v)
+            elif "copy" in name.lower():
+                copies.append(v)
+        copies = sorted(copies[-3:])  # the run ends with the three calibration copies
+        if not vals or len(copies) < 3:
+            raise SystemExit(f"{path}: no dispatches of {kernel!r} or no calibration copies")
+        return sum(vals) / len(vals), len(vals), copies[1]
+    f_kib, n_f, f_copy = per_kernel(fetch_csv)
+    w_kib, n_w, w_copy = per_kernel(write_csv)
+    f_scale, w_scale = copy_bytes / (f_copy * 1024), copy_bytes / (w_copy * 1024)
+    res = {"kernel_symbol": kernel, "command": command, "dispatches": [n_f, n_w],
+           "fetch_kib_per_dispatch": f_kib, "write_kib_per_dispatch": w_kib,
+           "copy_calibration": {"bytes": copy_bytes, "fetch_kib": f_copy, "write_kib": w_copy,
+                                "fetch_scale": f_scale, "write_scale": w_scale},
+           "traffic_bytes_per_dispatch": f_kib * 1024 * f_scale + w_kib * 1024 * w_scale}
+    with open(out, "w") as f:
+        json.dump(res, f, indent=1)
+        f.write("\n")
+    return res
+
+
+def summarize_trace(db: str, out: str, title: str, command: str, marker: str = "embed_gather") -> None:
+    """rocprofv3 rocpd database -> short markdown: per-kernel durations over the whole run and
+    one graph-replayed decode step (from one `marker` kernel to the next)."""
+    import collections
+    import sqlite3
+    c = sqlite3.connect(db)
+    rows = list(c.execute("select name, start, end from kernels order by start"))
+
+    def short(n: str) -> str:
+        return n.split("(")[0].replace("void ", "")[:70]
+    st = collections.defaultdict(list)
+    for n, a, b in rows:
+        st[short(n)].append(b - a)
+    tot = sum(sum(v) for v in st.values())
+    L = [f"# {title}", "", "Command (from the repo root, on one MI355X):", "", "```", command, "```", "",
+         f"Kernel dispatches recorded: {len(rows)}. Durations are rocprofv3 kernel-trace begin/end (ns), averaged "
+         "per kernel symbol over the whole run (prefill and the dominant-kernel timing graph included).", "",
+         "| kernel | calls | avg us | min us | max us | total ms | % |", "|---|---:|---:|---:|---:|---:|---:|"]
+    for n, v in sorted(st.items(), key=lambda kv: -sum(kv[1]))[:25]:
+        L.append(f"| `{n}` | {len(v)} | {sum(v) / len(v) / 1e3:.2f} | {min(v) / 1e3:.2f} | {max(v) / 1e3:.2f} | "
+                 f"{sum(v) / 1e6:.3f} | {100 * sum(v) / tot:.1f} |")
+    idx = [i for i, r in enumerate(rows) if marker in r[0]]
+    if len(idx) >= 3:
+        a, b = idx[-2], idx[-1]
+        seg = rows[a:b]
+        wall = seg[-1][2] - seg[0][1]
+        per = collections.defaultdict(lambda: [0, 0])
+        for r in seg:
+            per[short(r[0])][0] += 1
+            per[short(r[0])][1] += r[2] - r[1]
+        L += ["", f"## One decode step (graph replay {len(idx) - 1} of {len(idx)}, from `{marker}` to the next)", "",
+              f"{len(seg)} kernels, {wall / 1e3:.1f} us from first begin to last end "
+              f"({sum(r[2] - r[1] for r in seg) / 1e3:.1f} us inside kernels).", "",
+              "| kernel | calls/step | us/step |", "|---|---:|---:|"]
+        for n, (k, d) in sorted(per.items(), key=lambda kv: -kv[1][1]):
+            L.append(f"| `{n}` | {k} | {d / 1e3:.1f} |")
+        # one MoE layer in dispatch order (the kernels between the 2nd and 3rd MLA launches)
+        mla = [i for i, r in enumerate(seg) if "mla_" in r[0] and ("fused" in r[0] or "prepare" in r[0])]
+        if len(mla) >= 3:
+            L += ["", "## One MoE layer in dispatch order", "", "| # | kernel | us | gap before us |", "|---:|---|---:|---:|"]
+            for k, i in enumerate(range(mla[1], mla[2])):
+                r = seg[i]
+                gap = (r[1] - seg[i - 1][2]) / 1e3
+                L.append(f"| {k} | `{short(r[0])}` | {(r[2] - r[1]) / 1e3:.2f} | {gap:.2f} |")
+    with open(out, "w") as f:
+        f.write("\n".join(L) + "\n")
 
 
 def cpu_baseline(max_seconds: float = 30.0) -> dict:
@@ -171,7 +277,23 @@ def main() -> None:
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 3 plain 512 MiB device copies (the reference kernel for scaling the "
                          "FETCH_SIZE / WRITE_SIZE counters of a --pmc run)")
+    ap.add_argument("--summarize-trace", nargs=2, metavar=("DB", "OUT_MD"),
+                    help="no GPU: summarise a rocprofv3 rocpd database into markdown (with --title/--command)")
+    ap.add_argument("--pmc-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="no GPU: HBM bytes per dispatch of --kernel from two --pmc runs (FETCH_SIZE, WRITE_SIZE) "
+                         "scaled by the run's calibration copies; written to --out")
+    ap.add_argument("--kernel", default=None)
+    ap.add_argument("--out", default=None)
+    ap.add_argument("--title", default="")
+    ap.add_argument("--command", default="")
     args = ap.parse_args()
+    if args.summarize_trace:
+        summarize_trace(args.summarize_trace[0], args.summarize_trace[1], args.title, args.command)
+        return
+    if args.pmc_traffic:
+        print(json.dumps(pmc_traffic(args.pmc_traffic[0], args.pmc_traffic[1], args.kernel, 512 * 2**20, args.out,
+                                     args.command)))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (every box here has one "
               "GPU); run with --gpus 1", file=sys.stderr)
@@ -228,6 +350,7 @@ def main() -> None:
     sb = step_bytes(cfg, n_exp, ctx_avg, B)
     _log(f"timed {steps} graph replays: {ms:.3f} ms/step, {value:.1f} tok/s")
     roof = time_dominant_kernel(eng, family)
+    roof["traffic"] = measured_traffic(args.config, roof["kernel"])
     out = {
         "metric": METRIC, "value": round(value, 2), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warm,
         "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
