@@ -66,6 +66,17 @@ __device__ __forceinline__ uint4 pack8(const float* f) {
 
 __device__ __forceinline__ uint4 ldg16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 
+// 16-byte load with the non-temporal hint, for the weight streams of the few-row GEMVs:
+// on MI355X a 256-CU stream of such loads reaches ~6.8 TB/s from HBM against ~6.1 TB/s for
+// plain loads, but one CU then streams ~62 GB/s instead of ~130 GB/s -- so kernels whose
+// bytes sit on few CUs, and the MFMA GEMMs (measured slower), keep plain loads.  The hint
+// only changes the cache policy, not coherence.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ldg16_nt(const void* p) {
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // v if ok else 0, component-wise (a `?:` between two uint4 values is lowered through
 // scratch memory; a mask keeps it in registers)
 __device__ __forceinline__ uint4 keep_if(bool ok, const uint4& v) {

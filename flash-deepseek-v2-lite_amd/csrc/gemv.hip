@@ -53,8 +53,8 @@ __global__ __launch_bounds__(256) void gemv_k2048_kernel(const bf16_t* __restric
       const int c = min(lane + 64 * u, nch - 1);
 #pragma unroll
       for (int r = 0; r < RPW; ++r) {
-        wg[u][r] = ldg16(wr + (int64_t)r * K + c * 8);
-        if (SWIGLU) wu[u][r] = ldg16(wr + (int64_t)(N + r) * K + c * 8);
+        wg[u][r] = ldg16_nt(wr + (int64_t)r * K + c * 8);
+        if (SWIGLU) wu[u][r] = ldg16_nt(wr + (int64_t)(N + r) * K + c * 8);
       }
     }
   };
@@ -217,8 +217,8 @@ __global__ __launch_bounds__(256) void gemv_b1_kernel(const bf16_t* __restrict__
   for (int r = 0; r < RPW; ++r)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      wg[r][j] = ldg16(W + (int64_t)(n0 + r) * 2048 + (lane + 64 * j) * 8);
-      if (SW) wu[r][j] = ldg16(W + (int64_t)(N + n0 + r) * 2048 + (lane + 64 * j) * 8);
+      wg[r][j] = ldg16_nt(W + (int64_t)(n0 + r) * 2048 + (lane + 64 * j) * 8);
+      if (SW) wu[r][j] = ldg16_nt(W + (int64_t)(N + n0 + r) * 2048 + (lane + 64 * j) * 8);
     }
 #pragma unroll
   for (int r = 0; r < RPW; ++r) pin(rvb[r]);
@@ -325,7 +325,7 @@ __global__ __launch_bounds__(256) void gemv_klong_kernel(const bf16_t* __restric
 #pragma unroll
       for (int b = 0; b < NB; ++b) xb[u][b] = ldg16(x + (b < B ? b : 0) * xs + c * 8);
 #pragma unroll
-      for (int r = 0; r < RPW; ++r) wg[u][r] = ldg16(wr + (int64_t)r * K + c * 8);
+      for (int r = 0; r < RPW; ++r) wg[u][r] = ldg16_nt(wr + (int64_t)r * K + c * 8);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {

@@ -32,7 +32,7 @@ __global__ __launch_bounds__(1024) void router_kernel(const bf16_t* __restrict__
 #pragma unroll
     for (int r = 0; r < 4; ++r)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) wa[r][j] = ldg16(wr + (int64_t)(wv * 4 + r) * kH + (lane + 64 * j) * 8);
+      for (int j = 0; j < 4; ++j) wa[r][j] = ldg16_nt(wr + (int64_t)(wv * 4 + r) * kH + (lane + 64 * j) * 8);
     // norm: 2 elements per thread
     const uint32_t x2 = reinterpret_cast<const uint32_t*>(h + b * hs)[tid];
     float f0 = __uint_as_float(x2 << 16), f1 = __uint_as_float(x2 & 0xffff0000u);
@@ -124,7 +124,7 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const bf16_t* __rest
   const int e = part * 4 + wv;
   uint4 wa[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) wa[j] = ldg16(wr + (int64_t)e * kH + (lane + 64 * j) * 8);
+  for (int j = 0; j < 4; ++j) wa[j] = ldg16_nt(wr + (int64_t)e * kH + (lane + 64 * j) * 8);
   float f[8], g[8];
   unpack8(ldg16(h + b * hs + tid * 8), f);
   unpack8(ldg16(nw + tid * 8), g);
@@ -265,8 +265,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) voi
   for (int r = 0; r < RPW; ++r)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      wg[r][j] = ldg16(gp + (int64_t)r * kH + (lane + 64 * j) * 8);
-      wu[r][j] = ldg16(up + (int64_t)r * kH + (lane + 64 * j) * 8);
+      wg[r][j] = ldg16_nt(gp + (int64_t)r * kH + (lane + 64 * j) * 8);
+      wu[r][j] = ldg16_nt(up + (int64_t)r * kH + (lane + 64 * j) * 8);
     }
   float ag[RPW], au[RPW];
 #pragma unroll
@@ -403,7 +403,7 @@ __global__ __launch_bounds__(256) void route_down_kernel(const bf16_t* __restric
       for (int q = 0; q < 2; ++q) {
         x[q][k] = ldg16(hbuf + ((int64_t)b * hbuf_routes + 2 * wv + q) * inter + c * 8);
 #pragma unroll
-        for (int r = 0; r < 2; ++r) w[q][r][k] = ldg16(wrow[q] + r * wstride[q] + c * 8);
+        for (int r = 0; r < 2; ++r) w[q][r][k] = ldg16_nt(wrow[q] + r * wstride[q] + c * 8);
       }
     }
     pin(resb);
