@@ -83,7 +83,7 @@ def time_dominant_kernel(eng, family: str, reps: int = 4) -> dict:
                  ptr(b.hbuf), stream_ptr())
     else:
         tb = {16: 1, 32: 2, 64: 4}[b.tile_tokens]
-        sym = f"gemm_xlds_kernel<{tb}, true, {2 if tb == 4 else 4}, {'false' if tb == 4 else 'true'}, 2>"
+        sym = f"gemm_xlds_kernel<{tb}, true, 4, true, 2, {2 if tb == 1 else 4}>"
         name = f"{sym} via dsv2_moe_grouped_gateup (expert-grouped gate_up+SwiGLU on MFMA, {b.tile_tokens}-token tiles)"
         n_exp = int(torch.unique(b.ids32[:B]).numel())
         bytes_per = n_exp * 2 * c.moe_inter * c.hidden * 2 + B * 6 * c.moe_inter * 2

@@ -148,11 +148,11 @@ __global__ __launch_bounds__(NW * 64) void gemm_kernel(const GemmArgs a) {
 // 256 B, four loads a wave's 16 rows x 128 k -- which streams ~35% faster from HBM on
 // MI355X than the MFMA fragment order (16 rows x 64 B per load); the wave then passes
 // them through its own 4 KB LDS tile to form the A fragments.
-template <int TB, bool SWIGLU, int CS, bool AST, int DEPTH>
+template <int TB, bool SWIGLU, int CS, bool AST, int DEPTH, int NRB>
 __global__ __launch_bounds__(512) void gemm_xlds_kernel(const GemmArgs a) {
   static_assert(!AST || CS == 4, "row-contiguous weight staging works on 128-k chunks");
   constexpr int R = SWIGLU ? 2 : 1;    // row blocks per wave (gate, up)
-  constexpr int NRB = SWIGLU ? 2 : 4;  // feature blocks of 16 per workgroup
+  static_assert(NRB == 2 || NRB == 4, "feature blocks of 16 per workgroup");
   constexpr int NKQ = 8 / NRB;         // k ranges
   constexpr int TOK = 16 * TB;
   constexpr int XROW = CS * 32 + 8;  // LDS row in elements (+16 B pad: conflict-free B reads)
@@ -523,22 +523,28 @@ static void launch_os_variant(const GemmArgs& a, const OsShape& sh, hipStream_t 
 // features per workgroup of gemm_xlds_kernel
 static int xlds_features(bool swiglu) { return swiglu ? 32 : 64; }
 
-template <int TB, bool SWIGLU, int CS, bool AST, int DEPTH>
+template <int TB, bool SWIGLU, int CS, bool AST, int DEPTH, int NRB = (SWIGLU ? 2 : 4)>
 static void launch_xlds_variant(const GemmArgs& a, int grid_y, hipStream_t st) {
-  hipLaunchKernelGGL((gemm_xlds_kernel<TB, SWIGLU, CS, AST, DEPTH>), dim3(a.N / xlds_features(SWIGLU), grid_y),
-                     dim3(512), 0, st, a);
+  hipLaunchKernelGGL((gemm_xlds_kernel<TB, SWIGLU, CS, AST, DEPTH, NRB>), dim3(a.N / (16 * NRB), grid_y), dim3(512), 0,
+                     st, a);
 }
 
 static int launch_gemm_xlds(const GemmArgs& a, int tb, bool swiglu, int grid_y, hipStream_t st) {
-  // row-contiguous weight staging wherever its LDS tiles fit next to the token chunks
+  // Variants measured on MI355X for the expert-grouped MoE (64 experts, 16/32/64-token
+  // tiles): row-contiguous weight staging wherever its LDS tiles fit next to the token
+  // chunks; SwiGLU with 2+ token blocks takes 64 features (4 blocks x 2 k ranges) so each
+  // token chunk in LDS serves twice the weight rows (bsz=256 gate_up 178 -> 140 us).
+  const bool wide = a.N % 64 == 0;
   if (swiglu) {
     if (tb == 1) launch_xlds_variant<1, true, 4, true, 2>(a, grid_y, st);
+    else if (tb == 2 && wide) launch_xlds_variant<2, true, 4, true, 2, 4>(a, grid_y, st);
     else if (tb == 2) launch_xlds_variant<2, true, 4, true, 2>(a, grid_y, st);
+    else if (wide) launch_xlds_variant<4, true, 4, true, 2, 4>(a, grid_y, st);
     else launch_xlds_variant<4, true, 2, false, 2>(a, grid_y, st);
   } else {
     if (tb == 1) launch_xlds_variant<1, false, 4, true, 2>(a, grid_y, st);
     else if (tb == 2) launch_xlds_variant<2, false, 4, true, 2>(a, grid_y, st);
-    else if (tb == 4) launch_xlds_variant<4, false, 4, true, 2>(a, grid_y, st);
+    else if (tb == 4) launch_xlds_variant<4, false, 4, false, 2>(a, grid_y, st);
     else launch_xlds_variant<8, false, 2, false, 2>(a, grid_y, st);
   }
   return dsv2_launch_status("gemm");
