@@ -134,6 +134,7 @@ __global__ __launch_bounds__(256, 2) void mla_decode_kernel(const bf16_t* __rest
                                                             int max_splits, float scale_log2,
                                                             float* __restrict__ part_o, float* __restrict__ part_ml) {
   __shared__ __attribute__((aligned(16))) bf16_t lds[2][kTile * kLdsRow];
+  __shared__ floatx4_t spart[4][64];  // per-wave partial S^T (one 16-token block, half of K)
   const int s = blockIdx.x, b = blockIdx.y;
   const int len = pos[b] + 1;
   const int t_begin = s * split_tokens;
@@ -143,12 +144,15 @@ __global__ __launch_bounds__(256, 2) void mla_decode_kernel(const bf16_t* __rest
   const bf16_t* crow = cache + base[b] * kRow;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, li = lane & 15, kg = lane >> 4;
 
-  // Q^T fragments (B operand): head li, dims kk*32 + kg*8 .. +8
-  bf16x8_t qf[18];
+  // S^T = K Q^T is split over the waves: wave w scores 16-token block w >> 1 of every tile
+  // over k steps [9*(w & 1), 9*(w & 1) + 9) of the 18; the pair's partials meet in LDS.
+  // Q^T fragments (B operand) of those steps: head li, dims kk*32 + kg*8 .. +8
+  const int sblk = wv >> 1, k0 = (wv & 1) * 9;
+  bf16x8_t qf[9];
   {
-    const bf16_t* qh = q + ((int64_t)b * kHeads + li) * kRow + kg * 8;
+    const bf16_t* qh = q + ((int64_t)b * kHeads + li) * kRow + kg * 8 + k0 * 32;
 #pragma unroll
-    for (int kk = 0; kk < 18; ++kk) qf[kk] = as_bf16x8(ldg16(qh + kk * 32));
+    for (int kk = 0; kk < 9; ++kk) qf[kk] = as_bf16x8(ldg16(qh + kk * 32));
   }
 
   uint4 stage[9];
@@ -185,16 +189,18 @@ __global__ __launch_bounds__(256, 2) void mla_decode_kernel(const bf16_t* __rest
     if (it + 1 < ntiles) load_tile(t0 + kTile);
     const bf16_t* L = lds[buf];
 
-    // S^T = K Q^T for two 16-token blocks: sc[blk][e] = score(token blk*16 + 4kg + e, head li)
+    // S^T for two 16-token blocks: sc[blk][e] = score(token blk*16 + 4kg + e, head li)
+    {
+      floatx4_t sp = floatx4_t{0.f, 0.f, 0.f, 0.f};
+      const bf16_t* kr = L + (sblk * 16 + li) * kLdsRow + kg * 8 + k0 * 32;
+#pragma unroll
+      for (int kk = 0; kk < 9; ++kk) sp = mfma16x16x32(*reinterpret_cast<const bf16x8_t*>(kr + kk * 32), qf[kk], sp);
+      spart[wv][lane] = sp;
+    }
+    __syncthreads();
     floatx4_t sc[2];
 #pragma unroll
-    for (int blk = 0; blk < 2; ++blk) {
-      sc[blk] = floatx4_t{0.f, 0.f, 0.f, 0.f};
-      const bf16_t* kr = L + (blk * 16 + li) * kLdsRow + kg * 8;
-#pragma unroll
-      for (int kk = 0; kk < 18; ++kk)
-        sc[blk] = mfma16x16x32(*reinterpret_cast<const bf16x8_t*>(kr + kk * 32), qf[kk], sc[blk]);
-    }
+    for (int blk = 0; blk < 2; ++blk) sc[blk] = spart[2 * blk][lane] + spart[2 * blk + 1][lane];
     float p[8];
     float mx = -INFINITY;
 #pragma unroll
@@ -293,6 +299,12 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(const float* __restric
 #pragma unroll
     for (int r = 0; r < 8; ++r) wr[r] = ldg16(wp + (int64_t)r * kLat);
   }
+  // the first 8 splits' partial outputs are requested before the (m, l) merge; further
+  // splits come 8 loads at a time (split indices clamped, masked where used)
+  const float* po = part_o + ((int64_t)b * max_splits * kHeads + h) * kLat + 2 * tid;
+  float2 pv[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) pv[j] = *reinterpret_cast<const float2*>(po + (int64_t)min(j, ns - 1) * kHeads * kLat);
   if (wv == 0) {
     const float* pm = part_ml + ((int64_t)b * max_splits * kHeads + h) * 2;
     const float m = lane < ns ? pm[(int64_t)lane * kHeads * 2] : -INFINITY;
@@ -304,11 +316,19 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(const float* __restric
   }
   __syncthreads();
   float o0 = 0.f, o1 = 0.f;
-  const float* po = part_o + ((int64_t)b * max_splits * kHeads + h) * kLat + 2 * tid;
-  for (int s = 0; s < ns; ++s) {
-    const float2 v = *reinterpret_cast<const float2*>(po + (int64_t)s * kHeads * kLat);
-    o0 = __builtin_fmaf(wsp[s], v.x, o0);
-    o1 = __builtin_fmaf(wsp[s], v.y, o1);
+  for (int s0 = 0; s0 < ns; s0 += 8) {
+    if (s0 > 0) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        pv[j] = *reinterpret_cast<const float2*>(po + (int64_t)min(s0 + j, ns - 1) * kHeads * kLat);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (s0 + j < ns) {
+        o0 = __builtin_fmaf(wsp[s0 + j], pv[j].x, o0);
+        o1 = __builtin_fmaf(wsp[s0 + j], pv[j].y, o1);
+      }
+    }
   }
   if (!UV) {
     if (part == 0) *reinterpret_cast<uint32_t*>(out + b * os + h * kLat + 2 * tid) = pack2(o0, o1);
