@@ -11,10 +11,35 @@ constexpr int kTopK = 6;
 constexpr int kGateRPW = 2;
 }  // namespace
 
+// Softmax over the 64 router logits of one row (lane e holds logit e) and its top-6,
+// published as ids / weights: the probabilities v = exp(x - max) / sum are ranked directly
+// -- rank = number of lanes with a larger v, or an equal v at a lower index -- which is the
+// order six rounds of argmax with ties to the lower index would produce, in one pass.
+__device__ __forceinline__ void topk6_publish(float x, int64_t b, float scaling, int32_t* __restrict__ ids32,
+                                              int64_t* __restrict__ ids64, float* __restrict__ wts) {
+  const int lane = threadIdx.x & 63;
+  const float mx = wave_max(x);
+  const float ex = expf(x - mx);
+  const float sm = wave_sum(ex);
+  const float v = ex / sm;
+  int rank = 0;
+#pragma unroll 16
+  for (int j = 0; j < kE; ++j) {
+    const float vj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
+    rank += (vj > v || (vj == v && j < lane)) ? 1 : 0;
+  }
+  if (rank < kTopK) {
+    if (ids32) ids32[b * kTopK + rank] = lane;
+    if (ids64) ids64[b * kTopK + rank] = lane;
+    wts[b * kTopK + rank] = v * scaling;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // router: one workgroup per token.  xn = RMSNorm(h); logits = fp32(xn).fp32(W_r)
-// (bf16 x bf16 products are exact in fp32); softmax; top-6 by repeated max with
-// ties to the lower index.
+// (bf16 x bf16 products are exact in fp32); softmax; top-6 with ties to the lower index.
+// (A 16-token MFMA tile variant that reads W_r once per tile measured slower on MI355X at
+// 64 and 256 rows -- 18.3 vs 11.0 us -- so every row count takes this kernel.)
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(1024) void router_kernel(const bf16_t* __restrict__ h, int64_t hs,
                                                       const bf16_t* __restrict__ nw, float eps,
@@ -64,24 +89,7 @@ __global__ __launch_bounds__(1024) void router_kernel(const bf16_t* __restrict__
     if (tid < kE) lg[tid] = logits_in[(int64_t)b * kE + tid];
     __syncthreads();
   }
-  if (wv == 0) {
-    const float x = lg[lane];
-    const float mx = wave_max(x);
-    const float ex = expf(x - mx);
-    const float sm = wave_sum(ex);
-    float v = ex / sm;
-    for (int s = 0; s < kTopK; ++s) {
-      float bv = v;
-      int bi = lane;
-      wave_argmax(bv, bi);
-      if (lane == 0) {
-        if (ids32) ids32[b * kTopK + s] = bi;
-        if (ids64) ids64[b * kTopK + s] = bi;
-        wts[b * kTopK + s] = bv * scaling;
-      }
-      if (lane == bi) v = -INFINITY;
-    }
-  }
+  if (wv == 0) topk6_publish(lg[lane], b, scaling, ids32, ids64, wts);
 }
 
 extern "C" int dsv2_router_topk6(const void* h, int64_t h_stride, const void* norm_w, float eps, const void* w_router,
@@ -499,13 +507,17 @@ __global__ __launch_bounds__(1024) void bucket_kernel(const int32_t* __restrict_
   __syncthreads();
   for (int c = wv; c < nchunks; c += 16) {
     const int r = c * 64 + lane;
-    const int e = r < R ? min(max(ids[r], 0), kE - 1) : -1;
-    int before = 0, after = 0;
-    for (int j = 0; j < 64; ++j) {
-      const int ej = __shfl(e, j, 64);
-      before += (j < lane && ej == e) ? 1 : 0;
-      after += (j > lane && ej == e) ? 1 : 0;
+    const int e = r < R ? min(max(ids[r], 0), kE - 1) : kE;  // kE: no route (matches no expert)
+    // lanes holding the same expert: intersect, over the 7 bits of e, the ballots that agree
+    unsigned long long same = ~0ull;
+#pragma unroll
+    for (int bit = 0; bit < 7; ++bit) {
+      const unsigned long long bl = __ballot((e >> bit) & 1);
+      same &= ((e >> bit) & 1) ? bl : ~bl;
     }
+    const unsigned long long below = (1ull << lane) - 1ull;
+    const int before = __popcll(same & below);
+    const int after = __popcll(same & ~below) - 1;
     if (r < R) {
       rank[r] = (uint8_t)before;
       expert[r] = (uint8_t)e;

@@ -197,16 +197,17 @@ def test_gemm_grouped_heads_absorption(rows):
     assert rel_err(attn.float(), ref) < 1e-2
 
 
-def _router_case(rows, seed):
+def _router_case(rows, seed, unit_norm=True):
     h = rnd(rows, 2048, seed=seed)
-    nw = torch.ones(2048, dtype=BF, device=DEV)
+    nw = torch.ones(2048, dtype=BF, device=DEV) if unit_norm else (1 + rnd(2048, std=0.1, seed=seed + 2)).to(BF)
     wr = rnd(64, 2048, std=0.02, seed=seed + 1)
     return h, nw, wr
 
 
-@pytest.mark.parametrize("rows", [1, 64, 300])
-def test_router_topk6(rows):
-    h, nw, wr = _router_case(rows, 20)
+@pytest.mark.parametrize("rows,unit_norm", [(1, True), (64, True), (300, True), (37, False)])
+def test_router_topk6(rows, unit_norm):
+    """One workgroup per token; 37 rows with a non-trivial norm weight."""
+    h, nw, wr = _router_case(rows, 20, unit_norm)
     xn = torch.empty_like(h)
     ids = torch.empty(rows, 6, dtype=torch.int32, device=DEV)
     ids64 = torch.empty(rows, 6, dtype=torch.int64, device=DEV)
