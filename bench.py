@@ -1,11 +1,14 @@
 """Decode-throughput benchmark of the HIP DeepSeek-V2-Lite decode step on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1|2|3] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1|2|3|r64|r256] [--no-cpu-baseline]
 
 Default workload: full 27-layer random-init DeepSeek-V2-Lite
 bf16 (N(0,0.02), seed 0), bsz=1, a 128-token prompt of uniform random ids (seed
 1), eager prefill, then K greedy decode steps with the small kernel family, the
-whole step replayed as one hipGraph.  Prints ONE JSON line.
+whole step replayed as one hipGraph.  Prints ONE JSON line.  --config 2|3 are the
+bsz=64/256 random-prompt workloads; r64|r256 the reference's own published workload (one
+24-token prompt replicated over the batch), whose vs_baseline is value / the published A100
+batch-family TPS for it.
 
 Extra fields:
   roofline      -- dominant kernel of the step: algorithmic bytes per launch /
@@ -47,6 +50,16 @@ CONFIGS = {
             workload="C2: bsz=64, prompt lengths U[256,1024], batch family, hipGraph"),
     3: dict(batch=256, family="batch", prompt=lambda g: [2048] * 256, seed=2,
             workload="C3: bsz=256, prompt 2048, batch family, hipGraph"),
+    # The reference's own published workload (src/run.py:733-741): ONE 24-token prompt
+    # replicated over the batch, so every row routes to the same 6 experts per layer; the
+    # published A100 batch-family decode TPS for it (docs/third_party_baselines.md:90-100)
+    # is the baseline of these lines.
+    "r64": dict(batch=64, family="batch", prompt=lambda g: [24] * 64, seed=4, replicate=True, published=6237.99,
+                workload="reference workload: bsz=64, one 24-token random prompt replicated, batch family, "
+                         "hipGraph"),
+    "r256": dict(batch=256, family="batch", prompt=lambda g: [24] * 256, seed=4, replicate=True, published=11428.26,
+                 workload="reference workload: bsz=256, one 24-token random prompt replicated, batch family, "
+                          "hipGraph"),
 }
 
 
@@ -269,7 +282,7 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=99)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", type=int, default=1, choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="1", choices=[str(k) for k in CONFIGS])
     ap.add_argument("--family", choices=("small", "batch"), default=None)
     ap.add_argument("--mla-path", choices=("fused", "split"), default="fused",
                     help="small family: one fused MLA kernel per layer, or prepare + split-KV decode + combine")
@@ -301,6 +314,7 @@ def main() -> None:
 
     import dsv2lite
 
+    args.config = int(args.config) if args.config.isdigit() else args.config
     spec = CONFIGS[args.config]
     family = args.family or spec["family"]
     cfg = dsv2lite.DSV2Config()
@@ -313,7 +327,10 @@ def main() -> None:
     _log(f"weights ready ({w.nbytes() / 1e9:.1f} GB, {t_init:.1f}s)")
     g = torch.Generator().manual_seed(spec["seed"])
     lens = spec["prompt"](g)
-    prompts = [torch.randint(0, cfg.vocab, (n,), generator=g) for n in lens]
+    if spec.get("replicate"):
+        prompts = [torch.randint(0, cfg.vocab, (lens[0],), generator=g)] * len(lens)
+    else:
+        prompts = [torch.randint(0, cfg.vocab, (n,), generator=g) for n in lens]
     steps, warm = args.steps, args.warmup
     caps = [n + steps + warm + 8 for n in lens]
     eng = dsv2lite.DecodeEngine(w, caps, family=family, mla_path=args.mla_path)
@@ -353,8 +370,10 @@ def main() -> None:
     roof["traffic"] = measured_traffic(args.config, roof["kernel"])
     out = {
         "metric": METRIC, "value": round(value, 2), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warm,
-        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "bf16", "data": "synthetic: random-init weights N(0,0.02) seed 0, uniform random prompt ids",
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": round(value / spec["published"], 3) if spec.get("published") else None,
+        "dtype": "bf16", "data": "synthetic: random-init weights N(0,0.02) seed 0, uniform random prompt ids"
+                                 + (" (one prompt replicated over the batch)" if spec.get("replicate") else ""),
         "config": {"workload": spec["workload"], "global_batch": B, "seq_len": max(lens), "kernel_family": family,
                    "mla_path": args.mla_path if family == "small" else "split",
                    "prompt_tokens": sum(lens), "parallelism": "none (1 GPU)"},

@@ -72,6 +72,14 @@ __device__ __forceinline__ uint4 ldg16(const void* p) { return *reinterpret_cast
 // bytes sit on few CUs, and the MFMA GEMMs (measured slower), keep plain loads.  The hint
 // only changes the cache policy, not coherence.
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+// ds_read_b64_tr_b16 (gfx950): in each 16-lane group, lane i receives element i % 4 of the
+// four 16-bit elements that lane 4e + i / 4 addressed, for e = 0..3 (measured with a probe
+// kernel on MI355X: LDS element values = their index).  p must point into LDS, 8-byte aligned.
+__device__ __forceinline__ uint2 lds_read_tr16(const bf16_t* p) {
+  typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+  const bf16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4_t*)p);
+  return __builtin_bit_cast(uint2, v);
+}
 __device__ __forceinline__ uint4 ldg16_nt(const void* p) {
   const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
   return make_uint4(v.x, v.y, v.z, v.w);

@@ -4,8 +4,9 @@
 //
 //   prepare : kv-norm + RoPE(k_pe) -> cache row; RoPE(q_pe); q_lat = W_UK^T q_nope
 //   decode  : split-KV flash decoding; per workgroup one (row, split); 32-token
-//             tiles double-buffered in LDS; S^T = K Q^T and O^T += V^T P^T on
-//             v_mfma_f32_16x16x32_bf16 (16 heads = one MFMA dimension)
+//             tiles double-buffered in LDS, two more in flight in registers; S^T = K Q^T
+//             and O^T += V^T P^T on v_mfma_f32_16x16x32_bf16 (16 heads = one MFMA
+//             dimension), V^T fragments by transposed LDS reads
 //   combine : log-sum-exp merge of the splits, then W_UV (fused GEMV) or bf16 o_lat
 #include "common.h"
 
@@ -155,27 +156,34 @@ __global__ __launch_bounds__(256, 2) void mla_decode_kernel(const bf16_t* __rest
     for (int kk = 0; kk < 9; ++kk) qf[kk] = as_bf16x8(ldg16(qh + kk * 32));
   }
 
-  uint4 stage[9];
-  auto load_tile = [&](int t0) {
+  // Two register stages: tile it + 2 is requested while tile it + 1 is still in flight
+  // (cache rows are read once per step: non-temporal loads, which stream ~15% faster here).
+  // Requests past the last tile repeat it (L2 hits, never stored), so every load is
+  // unconditional and the waits count the newer stage's 9 loads exactly.
+  uint4 stage[2][9];
+  const int last = t_begin + (ntiles - 1) * kTile;
+  auto load_tile = [&](int st, int t0) {
+    t0 = min(t0, last);
 #pragma unroll
     for (int i = 0; i < 9; ++i) {
       const int c = tid + 256 * i;
       const int tok = c / 72, off = (c % 72) * 8;
       const int tt = min(t0 + tok, t_end - 1);
-      stage[i] = ldg16(crow + (int64_t)tt * kRow + off);
+      stage[st][i] = ldg16_nt(crow + (int64_t)tt * kRow + off);
     }
   };
-  auto store_tile = [&](int buf) {
+  auto store_tile = [&](int st, int buf) {
 #pragma unroll
     for (int i = 0; i < 9; ++i) {
       const int c = tid + 256 * i;
       const int tok = c / 72, off = (c % 72) * 8;
-      *reinterpret_cast<uint4*>(&lds[buf][tok * kLdsRow + off]) = stage[i];
+      *reinterpret_cast<uint4*>(&lds[buf][tok * kLdsRow + off]) = stage[st][i];
     }
   };
 
-  load_tile(t_begin);
-  store_tile(0);
+  load_tile(0, t_begin);
+  load_tile(1, t_begin + kTile);
+  store_tile(0, 0);
   __syncthreads();
 
   float m_run = -INFINITY, l_run = 0.f;
@@ -183,11 +191,11 @@ __global__ __launch_bounds__(256, 2) void mla_decode_kernel(const bf16_t* __rest
 #pragma unroll
   for (int mb = 0; mb < 8; ++mb) acc[mb] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 
-  for (int it = 0; it < ntiles; ++it) {
-    const int buf = it & 1;
+  // one tile: register stage u (= tile parity) and LDS buffer u
+  auto tile_step = [&](const int u, const int it) {
     const int t0 = t_begin + it * kTile;
-    if (it + 1 < ntiles) load_tile(t0 + kTile);
-    const bf16_t* L = lds[buf];
+    load_tile(u, t0 + 2 * kTile);
+    const bf16_t* L = lds[u];
 
     // S^T for two 16-token blocks: sc[blk][e] = score(token blk*16 + 4kg + e, head li)
     {
@@ -229,25 +237,31 @@ __global__ __launch_bounds__(256, 2) void mla_decode_kernel(const bf16_t* __rest
 #pragma unroll
     for (int mb = 0; mb < 8; ++mb) acc[mb] *= alpha;
 
-    // P^T (B operand): head li, tokens {4kg+e} then {16+4kg+e}; V^T (A operand) uses the same token order
+    // P^T (B operand): head li, tokens {4kg+e} then {16+4kg+e}; the V^T A operand takes the
+    // same tokens of dim d0 + li through two transposed LDS reads (ds_read_b64_tr_b16): in
+    // each 16-lane group, lane i receives element i % 4 of the 8 bytes that lane 4e + i / 4
+    // addressed (e = 0..3), so lane (li, kg) addresses token 4kg + li/4 (then 16 + 4kg + li/4),
+    // dims d0 + 4(li % 4) .. +3, and receives V[4kg + e][d0 + li] (then V[16 + 4kg + e][..]).
     const bf16x8_t pb = as_bf16x8(pack8(p));
+    const bf16_t* vp = L + (4 * kg + (li >> 2)) * kLdsRow + wv * 128 + 4 * (li & 3);
 #pragma unroll
     for (int mb = 0; mb < 8; ++mb) {
-      const int d = wv * 128 + mb * 16 + li;
-      const bf16_t* vc = L + d;
-      uint4 av;
-      av.x = (uint32_t)vc[(4 * kg + 0) * kLdsRow] | ((uint32_t)vc[(4 * kg + 1) * kLdsRow] << 16);
-      av.y = (uint32_t)vc[(4 * kg + 2) * kLdsRow] | ((uint32_t)vc[(4 * kg + 3) * kLdsRow] << 16);
-      av.z = (uint32_t)vc[(16 + 4 * kg + 0) * kLdsRow] | ((uint32_t)vc[(16 + 4 * kg + 1) * kLdsRow] << 16);
-      av.w = (uint32_t)vc[(16 + 4 * kg + 2) * kLdsRow] | ((uint32_t)vc[(16 + 4 * kg + 3) * kLdsRow] << 16);
-      acc[mb] = mfma16x16x32(as_bf16x8(av), pb, acc[mb]);
+      const uint2 lo = lds_read_tr16(vp + mb * 16), hi = lds_read_tr16(vp + mb * 16 + 16 * kLdsRow);
+      acc[mb] = mfma16x16x32(as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y)), pb, acc[mb]);
     }
     if (it + 1 < ntiles) {
-      // buf^1 was last read in iteration it-1, which every wave finished before the
-      // barrier that ended it; one barrier after the store publishes tile it+1.
-      store_tile(buf ^ 1);
+      // buffer u ^ 1 was last read in tile it - 1, which every wave finished before the
+      // barrier that ended it; one barrier after the store publishes tile it + 1.
+      store_tile(u ^ 1, u ^ 1);
       __syncthreads();
     }
+  };
+  // two tiles per pass, so each register stage stays in its own registers across the back edge
+  for (int it = 0;; it += 2) {
+    tile_step(0, it);
+    if (it + 1 >= ntiles) break;
+    tile_step(1, it + 1);
+    if (it + 2 >= ntiles) break;
   }
   // O^T layout: lane holds head li, dims wv*128 + mb*16 + 4kg + e
   float* po = part_o + (((int64_t)b * max_splits + s) * kHeads + li) * kLat + wv * 128 + 4 * kg;

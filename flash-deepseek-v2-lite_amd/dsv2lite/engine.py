@@ -26,6 +26,7 @@ import torch
 
 from triton_kernels import _hip
 from triton_kernels._hip import LINEAR_OUT_F32, LINEAR_SWIGLU, call, ptr
+from triton_kernels.attention_decode_batch import plan_splits
 
 from .cache import CompressedKVCache
 from .config import DSV2Config
@@ -35,15 +36,6 @@ from .weights import ModelWeights
 BF16 = torch.bfloat16
 FAMILIES = ("small", "batch")
 FUSED_MLA_MAX_CTX = 2048
-
-
-def plan_splits(rows: int, max_ctx: int, target_wgs: int = 1024) -> tuple[int, int]:
-    """(split_tokens, max_splits) for the split-KV decode: about target_wgs workgroups,
-    split_tokens a multiple of 32, at most 64 splits per row."""
-    per_row = max(1, min(64, math.ceil(target_wgs / max(rows, 1))))
-    split = max(32, math.ceil(math.ceil(max_ctx / per_row) / 32) * 32)
-    split = max(split, math.ceil(max_ctx / 64 / 32) * 32)
-    return split, math.ceil(max_ctx / split)
 
 
 def moe_tile_tokens(rows: int, n_experts: int = 64, top_k: int = 6) -> int:

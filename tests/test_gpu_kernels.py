@@ -364,8 +364,13 @@ def _mla_reference(q, cache_rows, lens, scale):
     return torch.stack(outs)
 
 
-@pytest.mark.parametrize("B,lo,hi,seed", [(1, 1, 40, 50), (3, 1, 300, 51), (16, 256, 8192, 3)])
-def test_mla_decode_combine_vs_fp32(B, lo, hi, seed):
+@pytest.mark.parametrize("B,lo,hi,seed,split", [(1, 1, 40, 50, None), (3, 1, 300, 51, None), (16, 256, 8192, 3, None),
+                                                (2, 500, 1300, 52, 1056), (3, 40, 200, 53, 128), (4, 1, 97, 54, 96)])
+def test_mla_decode_combine_vs_fp32(B, lo, hi, seed, split):
+    """Split plan of the engine, or a fixed one: 33 tiles (odd) / 4 tiles (even, last one
+    partial) / 3 tiles per split, so both register stages and the loop exits are covered."""
+    from triton_kernels.attention_decode_batch import plan_splits
+
     g = torch.Generator().manual_seed(seed)
     lens = torch.randint(lo, hi + 1, (B,), generator=g).tolist()
     cap = [L + 7 for L in lens]
@@ -374,10 +379,11 @@ def test_mla_decode_combine_vs_fp32(B, lo, hi, seed):
     q = torch.randn(B, 16, 576, generator=g).to(BF).to(DEV)
     pos = torch.tensor([L - 1 for L in lens], dtype=torch.int32, device=DEV)
     scale = O.softmax_scale(O.Dims())
-    per_row = max(1, min(64, math.ceil(1024 / B)))
     maxL = max(cap)
-    split = max(32, math.ceil(math.ceil(maxL / per_row) / 32) * 32, math.ceil(maxL / 64 / 32) * 32)
-    ns = math.ceil(maxL / split)
+    if split is None:
+        split, ns = plan_splits(B, maxL)
+    else:
+        ns = math.ceil(maxL / split)
     po = torch.empty(B, ns, 16, 512, device=DEV)
     pm = torch.empty(B, ns, 16, 2, device=DEV)
     base_d = base.to(DEV)  # keep device copies alive until the kernels have run
