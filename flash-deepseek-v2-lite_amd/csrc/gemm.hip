@@ -148,9 +148,10 @@ __global__ __launch_bounds__(NW * 64) void gemm_kernel(const GemmArgs a) {
 // 256 B, four loads a wave's 16 rows x 128 k -- which streams ~35% faster from HBM on
 // MI355X than the MFMA fragment order (16 rows x 64 B per load); the wave then passes
 // them through its own 4 KB LDS tile to form the A fragments.
-template <int TB, bool SWIGLU, int CS, bool AST, int DEPTH, int NRB>
+template <int TB, bool SWIGLU, int CS, bool AST, int DEPTH, int NRB, int XD = 1>
 __global__ __launch_bounds__(512) void gemm_xlds_kernel(const GemmArgs a) {
   static_assert(!AST || CS == 4, "row-contiguous weight staging works on 128-k chunks");
+  static_assert(XD >= 1 && DEPTH % XD == 0, "token-chunk stages must divide the unroll");
   constexpr int R = SWIGLU ? 2 : 1;    // row blocks per wave (gate, up)
   static_assert(NRB == 2 || NRB == 4, "feature blocks of 16 per workgroup");
   constexpr int NKQ = 8 / NRB;         // k ranges
@@ -216,15 +217,15 @@ __global__ __launch_bounds__(512) void gemm_xlds_kernel(const GemmArgs a) {
   // needed.  Steps past K read step S-1 and are zeroed in the X tile only: the weight
   // fragments there are real (finite) weights multiplied by zero.  Token rows past the
   // tile hold row 0's values; their output columns are never stored.
-#define XL_LOAD_X(c)                                                             \
+#define XL_LOAD_X(c, xs)                                                         \
   _Pragma("unroll") for (int j = 0; j < UPT; ++j) {                              \
     const int step_ = xkq[j] * SP + (c) * CS + (xpart[j] >> 2);                  \
-    xr[j] = ldg16(xsrc[j] + (int64_t)min(step_, S - 1) * 32);                    \
+    xs[j] = ldg16(xsrc[j] + (int64_t)min(step_, S - 1) * 32);                    \
   }
-#define XL_STORE_X(c, buf)                                                       \
+#define XL_STORE_X(c, xs, buf)                                                   \
   _Pragma("unroll") for (int j = 0; j < UPT; ++j) {                              \
     const int step_ = xkq[j] * SP + (c) * CS + (xpart[j] >> 2);                  \
-    *reinterpret_cast<uint4*>(xbuf + (buf) * XBUF + xdst[j]) = keep_if(step_ < S, xr[j]); \
+    *reinterpret_cast<uint4*>(xbuf + (buf) * XBUF + xdst[j]) = keep_if(step_ < S, xs[j]); \
   }
 // AST: av[q][r] = rows 4q + (lane >> 4) of block r, k = chunk + (lane & 15) * 8
 #define XL_LOAD_A(c, av)                                                                         \
@@ -241,22 +242,24 @@ __global__ __launch_bounds__(512) void gemm_xlds_kernel(const GemmArgs a) {
     for (int tb = 0; tb < TB; ++tb) acc[r][tb] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 
   // Weight chunks are requested DEPTH - 1 chunks ahead of the one being multiplied, token
-  // chunks one ahead and before the weight loads (loads complete in issue order, so the wait
-  // for a token chunk before its LDS store leaves the later weight loads in flight).  The
-  // chunk loop is unrolled by DEPTH (nch is a multiple of it) so every register buffer index
-  // is a constant, and no load sits behind a branch: requests past the last chunk repeat it
-  // (L2 hits), so the compiler's wait counts stay exact.
-  uint4 ab[DEPTH][CS][R], xr[UPT];
-  XL_LOAD_X(0)
+  // chunks XD ahead (a ring of XD register stages; chunk c + 1 goes to LDS at the end of
+  // chunk c) and before the weight loads (loads complete in issue order, so the wait for a
+  // token chunk before its LDS store leaves the later weight loads in flight).  The chunk
+  // loop is unrolled by DEPTH (nch is a multiple of it) so every register buffer index is a
+  // constant, and no load sits behind a branch: requests past the last chunk repeat it (L2
+  // hits), so the compiler's wait counts stay exact.
+  uint4 ab[DEPTH][CS][R], xr[XD][UPT];
 #pragma unroll
-  for (int p = 0; p + 1 < DEPTH; ++p) XL_LOAD_A(p, ab[p])
-  XL_STORE_X(0, 0)
+  for (int x = 0; x < XD; ++x) XL_LOAD_X(min(x, nch - 1), xr[x])
+#pragma unroll
+  for (int p = 0; p + 1 < DEPTH; ++p) XL_LOAD_A(min(p, nch - 1), ab[p])
+  XL_STORE_X(0, xr[0], 0)
   __syncthreads();
   for (int c0 = 0; c0 < nch; c0 += DEPTH) {
 #pragma unroll
     for (int i = 0; i < DEPTH; ++i) {
       const int c = c0 + i;
-      XL_LOAD_X(min(c + 1, nch - 1))
+      XL_LOAD_X(min(c + XD, nch - 1), xr[i % XD])  // stage i % XD held chunk c, now in LDS
       XL_LOAD_A(min(c + DEPTH - 1, nch - 1), ab[(i + DEPTH - 1) % DEPTH])
       const bf16_t* xb = xbuf + (c & 1) * XBUF + (kq * TOK + li) * XROW + kg * 8;
       bf16x8_t afr[CS][R];
@@ -288,7 +291,7 @@ __global__ __launch_bounds__(512) void gemm_xlds_kernel(const GemmArgs a) {
           for (int r = 0; r < R; ++r) acc[r][tb] = mfma16x16x32(afr[si][r], bfr, acc[r][tb]);
         }
       // the last chunk's store fills the idle buffer with a repeat (never read)
-      XL_STORE_X(c + 1, (c + 1) & 1)
+      XL_STORE_X(c + 1, xr[(i + 1) % XD], (c + 1) & 1)
       __syncthreads();
     }
   }
@@ -523,10 +526,10 @@ static void launch_os_variant(const GemmArgs& a, const OsShape& sh, hipStream_t 
 // features per workgroup of gemm_xlds_kernel
 static int xlds_features(bool swiglu) { return swiglu ? 32 : 64; }
 
-template <int TB, bool SWIGLU, int CS, bool AST, int DEPTH, int NRB = (SWIGLU ? 2 : 4)>
+template <int TB, bool SWIGLU, int CS, bool AST, int DEPTH, int NRB = (SWIGLU ? 2 : 4), int XD = 1>
 static void launch_xlds_variant(const GemmArgs& a, int grid_y, hipStream_t st) {
-  hipLaunchKernelGGL((gemm_xlds_kernel<TB, SWIGLU, CS, AST, DEPTH, NRB>), dim3(a.N / (16 * NRB), grid_y), dim3(512), 0,
-                     st, a);
+  hipLaunchKernelGGL((gemm_xlds_kernel<TB, SWIGLU, CS, AST, DEPTH, NRB, XD>), dim3(a.N / (16 * NRB), grid_y), dim3(512),
+                     0, st, a);
 }
 
 static int launch_gemm_xlds(const GemmArgs& a, int tb, bool swiglu, int grid_y, hipStream_t st) {
@@ -581,13 +584,22 @@ static int launch_gemm(const GemmArgs& a, int tb, bool swiglu, int grid_y, hipSt
 static int pick_tb(int rows) { return rows <= 16 ? 1 : (rows <= 32 ? 2 : (rows <= 64 ? 4 : 8)); }
 
 // Dense (implicit-tile) shapes whose row blocks alone cannot fill the chip, measured on
-// MI355X at 16..256 tokens: the one-shot kernel for short K, SwiGLU and up to 64 tokens;
-// the token-rows-in-LDS kernel (64-row workgroups sharing token chunks) for more tokens,
-// with the largest token tile that still gives ~200 workgroups.  Returns false (nothing
+// MI355X at 16..256 tokens: the one-shot kernel for short K and up to 64 tokens; the
+// token-rows-in-LDS kernel (64-row workgroups sharing token chunks) for more tokens, with
+// the largest token tile that still gives ~200 workgroups (SwiGLU: 64-token tiles).  Returns false (nothing
 // launched) for shapes left to launch_gemm: long K, huge N, or N not a multiple of 16*rbw.
 static bool launch_dense_os(GemmArgs a, int groups, bool swiglu, hipStream_t st) {
   const int rows = a.rows, K = a.K;
   if (K > 4096 || (int64_t)a.N * groups >= 16384) return false;
+  if (swiglu && K > 512 && rows > 64 && a.N % 64 == 0) {
+    // 64-token tiles, 64 features (gate + up rows) per workgroup, two token chunks in flight
+    // (shared experts at 256 tokens: 22.4 us vs 28.8 us for the one-shot shape)
+    a.tiles_per_group = (rows + 63) / 64;
+    const int64_t gy = (int64_t)a.tiles_per_group * groups;
+    if (gy > 65535) return false;
+    launch_xlds_variant<4, true, 4, true, 2, 4, 2>(a, (int)gy, st);
+    return true;
+  }
   if (!swiglu && K > 512 && rows > 64 && a.N % 64 == 0) {
     int tb = 1;
     for (int t : {2, 4}) {
@@ -599,7 +611,7 @@ static bool launch_dense_os(GemmArgs a, int groups, bool swiglu, hipStream_t st)
     if (gy > 65535) return false;
     if (tb == 1) launch_xlds_variant<1, false, 4, true, 2>(a, (int)gy, st);
     else if (tb == 2) launch_xlds_variant<2, false, 4, true, 2>(a, (int)gy, st);
-    else launch_xlds_variant<4, false, 4, true, 2>(a, (int)gy, st);
+    else launch_xlds_variant<4, false, 4, true, 2, 4, 2>(a, (int)gy, st);  // two token chunks in flight
     return true;
   }
   const int tb = K <= 512 ? (rows <= 64 ? 1 : 2) : (swiglu ? (rows <= 16 ? 1 : (rows <= 32 ? 2 : 4)) : (rows <= 16 ? 1 : 2));
