@@ -586,10 +586,22 @@ static int pick_tb(int rows) { return rows <= 16 ? 1 : (rows <= 32 ? 2 : (rows <
 // Dense (implicit-tile) shapes whose row blocks alone cannot fill the chip, measured on
 // MI355X at 16..256 tokens: the one-shot kernel for short K and up to 64 tokens; the
 // token-rows-in-LDS kernel (64-row workgroups sharing token chunks) for more tokens, with
-// the largest token tile that still gives ~200 workgroups (SwiGLU: 64-token tiles).  Returns false (nothing
-// launched) for shapes left to launch_gemm: long K, huge N, or N not a multiple of 16*rbw.
+// the largest token tile that still gives ~200 workgroups (SwiGLU: 64-token tiles); long K
+// with few features on 16/32-token tiles.  Returns false (nothing launched) for shapes left
+// to launch_gemm: huge N, long K with SwiGLU or groups, or N not a multiple of 16*rbw.
 static bool launch_dense_os(GemmArgs a, int groups, bool swiglu, hipStream_t st) {
   const int rows = a.rows, K = a.K;
+  if (K > 4096 && !swiglu && groups == 1 && a.N % 64 == 0 && a.N < 16384) {
+    // long K, few features (dense layer-0 down, K = 10944): token-rows-in-LDS tiles of 16 /
+    // 32 tokens with row-contiguous weight staging (bsz=256: 51 us vs 97 us for the k-split
+    // kernel's MFMA-fragment-order loads; bsz=64: 41 vs 62 us)
+    const int tb = rows <= 64 ? 1 : 2;
+    a.tiles_per_group = (rows + 16 * tb - 1) / (16 * tb);
+    if (a.tiles_per_group > 65535) return false;
+    if (tb == 1) launch_xlds_variant<1, false, 4, true, 2>(a, a.tiles_per_group, st);
+    else launch_xlds_variant<2, false, 4, true, 2>(a, a.tiles_per_group, st);
+    return true;
+  }
   if (K > 4096 || (int64_t)a.N * groups >= 16384) return false;
   if (swiglu && K > 512 && rows > 64 && a.N % 64 == 0) {
     // 64-token tiles, 64 features (gate + up rows) per workgroup, two token chunks in flight

@@ -153,11 +153,12 @@ def test_gemm_k_split_shapes(rows, K, N, swiglu):
 
 @pytest.mark.parametrize("rows", [16, 64, 130, 256])
 @pytest.mark.parametrize("K,N,mode", [(2048, 3648, "plain"), (2048, 2048, "residual"), (2048, 2816, "swiglu"),
-                                      (2816, 2048, "plain"), (2048, 10944, "swiglu"), (2048, 2048, "f32")])
+                                      (2816, 2048, "plain"), (2048, 10944, "swiglu"), (10944, 2048, "residual"),
+                                      (2048, 2048, "f32")])
 def test_gemm_dense_model_shapes(rows, K, N, mode):
     """The batch family's dense projections (qkv_a, o_proj + residual, shared-expert
-    gate_up / down, layer-0 MLP gate_up) at the token counts where the one-shot and the
-    token-rows-in-LDS shapes take over from the k-split kernel."""
+    gate_up / down, layer-0 MLP gate_up / down + residual) at the token counts where the
+    one-shot and the token-rows-in-LDS shapes take over from the k-split kernel."""
     x = rnd(rows, K, seed=K + N + rows)
     W = rnd(2 * N if mode == "swiglu" else N, K, std=0.02, seed=K + N)
     res = rnd(rows, N, seed=3 * rows) if mode == "residual" else None
