@@ -96,7 +96,8 @@ def time_dominant_kernel(eng, family: str, reps: int = 4) -> dict:
                  ptr(b.hbuf), stream_ptr())
     else:
         tb = {16: 1, 32: 2, 64: 4}[b.tile_tokens]
-        sym = f"gemm_xlds_kernel<{tb}, true, 4, true, 2, {2 if tb == 1 else 4}>"
+        sym = {1: "gemm_xlds_kernel<1, true, 4, true, 2, 2, 1, false>", 2: "gemm_xlds_kernel<2, true, 4, true, 2, 4, 2, true>",
+               4: "gemm_xlds_kernel<4, true, 4, true, 2, 4, 1, false>"}[tb]
         name = f"{sym} via dsv2_moe_grouped_gateup (expert-grouped gate_up+SwiGLU on MFMA, {b.tile_tokens}-token tiles)"
         n_exp = int(torch.unique(b.ids32[:B]).numel())
         bytes_per = n_exp * 2 * c.moe_inter * c.hidden * 2 + B * 6 * c.moe_inter * 2

@@ -148,7 +148,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_kernel(const GemmArgs a) {
 // 256 B, four loads a wave's 16 rows x 128 k -- which streams ~35% faster from HBM on
 // MI355X than the MFMA fragment order (16 rows x 64 B per load); the wave then passes
 // them through its own 4 KB LDS tile to form the A fragments.
-template <int TB, bool SWIGLU, int CS, bool AST, int DEPTH, int NRB, int XD = 1>
+template <int TB, bool SWIGLU, int CS, bool AST, int DEPTH, int NRB, int XD = 1, bool NTA = false>
 __global__ __launch_bounds__(512) void gemm_xlds_kernel(const GemmArgs a) {
   static_assert(!AST || CS == 4, "row-contiguous weight staging works on 128-k chunks");
   static_assert(XD >= 1 && DEPTH % XD == 0, "token-chunk stages must divide the unroll");
@@ -232,7 +232,8 @@ __global__ __launch_bounds__(512) void gemm_xlds_kernel(const GemmArgs a) {
   _Pragma("unroll") for (int si = 0; si < CS; ++si) {                                            \
     const int step_ = kq * SP + (c) * CS + (AST ? ((lane & 15) >> 2) : si);                      \
     _Pragma("unroll") for (int r = 0; r < R; ++r)                                                \
-      av[si][r] = ldg16(wrow[r] + (AST ? (int64_t)si * 4 * K : 0) + (int64_t)min(step_, S - 1) * 32); \
+      av[si][r] = NTA ? ldg16_nt(wrow[r] + (AST ? (int64_t)si * 4 * K : 0) + (int64_t)min(step_, S - 1) * 32) \
+                      : ldg16(wrow[r] + (AST ? (int64_t)si * 4 * K : 0) + (int64_t)min(step_, S - 1) * 32); \
   }
 
   floatx4_t acc[R][TB];
@@ -526,21 +527,23 @@ static void launch_os_variant(const GemmArgs& a, const OsShape& sh, hipStream_t 
 // features per workgroup of gemm_xlds_kernel
 static int xlds_features(bool swiglu) { return swiglu ? 32 : 64; }
 
-template <int TB, bool SWIGLU, int CS, bool AST, int DEPTH, int NRB = (SWIGLU ? 2 : 4), int XD = 1>
+template <int TB, bool SWIGLU, int CS, bool AST, int DEPTH, int NRB = (SWIGLU ? 2 : 4), int XD = 1, bool NTA = false>
 static void launch_xlds_variant(const GemmArgs& a, int grid_y, hipStream_t st) {
-  hipLaunchKernelGGL((gemm_xlds_kernel<TB, SWIGLU, CS, AST, DEPTH, NRB, XD>), dim3(a.N / (16 * NRB), grid_y), dim3(512),
-                     0, st, a);
+  hipLaunchKernelGGL((gemm_xlds_kernel<TB, SWIGLU, CS, AST, DEPTH, NRB, XD, NTA>), dim3(a.N / (16 * NRB), grid_y),
+                     dim3(512), 0, st, a);
 }
 
 static int launch_gemm_xlds(const GemmArgs& a, int tb, bool swiglu, int grid_y, hipStream_t st) {
   // Variants measured on MI355X for the expert-grouped MoE (64 experts, 16/32/64-token
   // tiles): row-contiguous weight staging wherever its LDS tiles fit next to the token
   // chunks; SwiGLU with 2+ token blocks takes 64 features (4 blocks x 2 k ranges) so each
-  // token chunk in LDS serves twice the weight rows (bsz=256 gate_up 178 -> 140 us).
+  // token chunk in LDS serves twice the weight rows (bsz=256 gate_up 178 -> 140 us); with
+  // 32-token tiles also non-temporal weight loads and two token chunks in flight (140 ->
+  // 130 us; the same loads measured slower for 16-token tiles and for the down projection).
   const bool wide = a.N % 64 == 0;
   if (swiglu) {
     if (tb == 1) launch_xlds_variant<1, true, 4, true, 2>(a, grid_y, st);
-    else if (tb == 2 && wide) launch_xlds_variant<2, true, 4, true, 2, 4>(a, grid_y, st);
+    else if (tb == 2 && wide) launch_xlds_variant<2, true, 4, true, 2, 4, 2, true>(a, grid_y, st);
     else if (tb == 2) launch_xlds_variant<2, true, 4, true, 2>(a, grid_y, st);
     else if (wide) launch_xlds_variant<4, true, 4, true, 2, 4>(a, grid_y, st);
     else launch_xlds_variant<4, true, 2, false, 2>(a, grid_y, st);
