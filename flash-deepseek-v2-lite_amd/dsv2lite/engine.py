@@ -36,6 +36,10 @@ from .weights import ModelWeights
 BF16 = torch.bfloat16
 FAMILIES = ("small", "batch")
 FUSED_MLA_MAX_CTX = 2048
+# batch family: up to this many rows the router runs as logits over 16 workgroups per token
+# plus a one-wave top-6 per row (64 rows: 8.3 us vs 11.1 us for one workgroup per token on
+# MI355X); above it one workgroup per token (256 rows: 11.4 us vs 14.7 us)
+SPLIT_ROUTER_MAX_ROWS = 64
 
 
 def moe_tile_tokens(rows: int, n_experts: int = 64, top_k: int = 6) -> int:
@@ -65,9 +69,9 @@ class RowBuffers:
         self.ids32 = e(rows, cfg.top_k, dt=torch.int32)
         self.wts = e(rows, cfg.top_k, dt=torch.float32)
         self.mid = e(rows, cfg.dense_inter)
+        self.router_logits = e(rows, cfg.n_experts, dt=torch.float32)
         if family == "small":
             self.hbuf = e(rows, cfg.top_k + 2, cfg.moe_inter)
-            self.router_logits = e(rows, cfg.n_experts, dt=torch.float32)
         else:
             R = rows * cfg.top_k
             self.olat = e(rows, cfg.n_heads, cfg.kv_rank)
@@ -174,8 +178,14 @@ class DecodeEngine:
                      ptr(b.h), H, ptr(b.h), H, 0, st)
             return
         if L.moe:
-            call("dsv2_router_topk6", ptr(b.h), H, ptr(L.ln_post), c.eps, ptr(L.w_router), c.routed_scaling, R,
-                 ptr(b.xn), ptr(b.ids32), None, ptr(b.wts), st)
+            if R <= SPLIT_ROUTER_MAX_ROWS:
+                call("dsv2_router_logits", ptr(b.h), H, ptr(L.ln_post), c.eps, ptr(L.w_router), R, ptr(b.xn),
+                     ptr(b.router_logits), st)
+                call("dsv2_router_topk6_from_logits", ptr(b.router_logits), R, c.routed_scaling, ptr(b.ids32), None,
+                     ptr(b.wts), st)
+            else:
+                call("dsv2_router_topk6", ptr(b.h), H, ptr(L.ln_post), c.eps, ptr(L.w_router), c.routed_scaling, R,
+                     ptr(b.xn), ptr(b.ids32), None, ptr(b.wts), st)
             call("dsv2_moe_bucket", ptr(b.ids32), R, b.tile_tokens, ptr(b.sorted), ptr(b.route_pos), ptr(b.tiles),
                  ptr(b.ntiles), st)
             call("dsv2_moe_grouped_gateup", ptr(b.xn), ptr(b.sorted), ptr(b.tiles), ptr(b.ntiles), b.max_tiles,
