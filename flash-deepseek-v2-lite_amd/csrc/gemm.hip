@@ -363,6 +363,113 @@ __device__ __forceinline__ void gemm_store4(const GemmArgs& a, int g, int slot, 
   }
 }
 
+// Direct-to-LDS ring shape for dense weights and 128+ tokens: a 4-wave workgroup owns 64
+// features x 64 tokens (each wave 32 x 32, 2 x 2 MFMA blocks).  K streams in 64-wide chunks
+// through a ring of kDmaStages 16 KB LDS stages filled by global_load_lds (16 bytes per
+// lane straight into LDS, no register round trip): every load covers 8 rows x 128 B, and
+// the lanes pick the 16-byte pieces so that the LDS copy is swizzled (piece c of row r at
+// slot c ^ (r & 7)) and the MFMA fragment reads are conflict-free.  One barrier per chunk;
+// the wait before it counts only this wave's newer ring loads (the workgroup fence of
+// __syncthreads would drain the whole ring).  XCD-aware 1-D grid: the token tiles of one
+// feature block are consecutive work items on one XCD, so their weight reads after the
+// first hit that XCD's L2 (qkv_a at 256 tokens: 12.2 us vs 17.9 us for the token-rows-in-LDS
+// shape; without the XCD grouping 18.3 us).
+constexpr int kDmaStages = 4;
+// s_waitcnt immediate (gfx9 encoding): wait until at most n vector-memory operations are
+// outstanding, leaving the LDS/scalar (15) and export (7) counters unconstrained
+constexpr int vmcnt_only(int n) { return (n & 0xf) | (0x7 << 4) | (0xf << 8) | (((n >> 4) & 3) << 14); }
+
+struct DmaShape {
+  int tiles, nwg;
+};
+
+__global__ __launch_bounds__(256) void gemm_dma_kernel(const GemmArgs a, const DmaShape sh) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // kDmaStages * 16 KB
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, li = lane & 15, kg = lane >> 4;
+  const int per = sh.nwg / 8;
+  const int w = (blockIdx.x % 8) * per + blockIdx.x / 8;
+  if (w >= (a.N / 64) * sh.tiles) return;
+  const int tile = w % sh.tiles, fb = w / sh.tiles;
+  const int f0 = fb * 64, t0 = tile * 64, count = min(64, a.rows - t0);
+  const int K = a.K, nch = K / 64;
+  // this wave's 4 ring loads per chunk: weight rows 16wv .. 16wv+15 (j = 0, 1) and token rows
+  // 16wv .. 16wv+15 (j = 2, 3), 8 rows per load; lane -> (row r, slot lane & 7), which holds
+  // piece (lane & 7) ^ (r & 7)
+  const bf16_t* src[4];
+  int dst[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = 16 * wv + 8 * (j & 1) + (lane >> 3);
+    const int pc = (lane & 7) ^ (r & 7);
+    if (j >= 2) src[j] = a.X + (int64_t)(t0 + (r < count ? r : 0)) * a.xs + pc * 8;  // rows past the tile: row t0
+    else src[j] = a.W + (int64_t)(f0 + r) * K + pc * 8;
+    dst[j] = (j >= 2 ? 8192 : 0) + (16 * wv + 8 * (j & 1)) * 128;
+  }
+  auto issue = [&](int chunk, int buf) {
+    const int cc = min(chunk, nch - 1);  // past the last chunk: repeat it (never multiplied)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      __builtin_amdgcn_global_load_lds(src[j] + cc * 64,
+                                       (__attribute__((address_space(3))) void*)(lds + buf * 16384 + dst[j]), 16, 0, 0);
+  };
+  floatx4_t acc[2][2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y) acc[x][y] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+  const int wa = (wv & 1) * 32, wt = (wv >> 1) * 32;  // this wave's 32 features x 32 tokens
+#pragma unroll
+  for (int s = 0; s + 1 < kDmaStages; ++s) issue(s, s);
+  for (int c0 = 0; c0 < nch; c0 += kDmaStages) {
+#pragma unroll
+    for (int i = 0; i < kDmaStages; ++i) {
+      const int c = c0 + i;
+      if (c >= nch) break;
+      // this wave's loads of chunk c have landed (the 4 of each newer chunk may not), then
+      // every wave's: chunk c is complete in LDS and chunk c - 1's stage is free
+      __builtin_amdgcn_s_waitcnt(vmcnt_only((kDmaStages - 2) * 4));
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      issue(c + kDmaStages - 1, (i + kDmaStages - 1) % kDmaStages);
+      const uint8_t* st = lds + i * 16384;
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        bf16x8_t af[2], bfr[2];
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+          const int r = wa + 16 * x + li, t = wt + 16 * x + li, pc = 4 * s + kg;
+          af[x] = *reinterpret_cast<const bf16x8_t*>(st + r * 128 + ((pc ^ (r & 7)) * 16));
+          bfr[x] = *reinterpret_cast<const bf16x8_t*>(st + 8192 + t * 128 + ((pc ^ (t & 7)) * 16));
+        }
+#pragma unroll
+        for (int x = 0; x < 2; ++x)
+#pragma unroll
+          for (int y = 0; y < 2; ++y) acc[x][y] = mfma16x16x32(af[x], bfr[y], acc[x][y]);
+      }
+    }
+  }
+  // the repeats past the last chunk must land before the workgroup's LDS is released
+  __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y) {
+      if (wt + 16 * y + li >= count) continue;
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = rbf(acc[x][y][e]);
+      gemm_store4(a, 0, t0 + wt + 16 * y + li, f0 + wa + 16 * x + 4 * kg, v);
+    }
+}
+
+static void launch_dma(const GemmArgs& a, hipStream_t st) {
+  DmaShape sh;
+  sh.tiles = (a.rows + 63) / 64;
+  sh.nwg = ((a.N / 64) * sh.tiles + 7) / 8 * 8;
+  hipLaunchKernelGGL(gemm_dma_kernel, dim3(sh.nwg), dim3(256), kDmaStages * 16384, st, a, sh);
+}
+
 // One-shot shape for dense weights and few tokens (the row blocks alone cannot fill the
 // chip): a workgroup owns RBW blocks of 16 features for one tile of 16*TB tokens, and
 // KW waves per block split K into 128-wide chunks (wave kw takes chunks kw, kw + KW, ...,
@@ -606,6 +713,14 @@ static bool launch_dense_os(GemmArgs a, int groups, bool swiglu, hipStream_t st)
     return true;
   }
   if (K > 4096 || (int64_t)a.N * groups >= 16384) return false;
+  if (!swiglu && groups == 1 && rows > 128 && K <= 4096 && a.N % 64 == 0 && a.N < 16384 &&
+      (a.N / 64) * ((rows + 63) / 64) >= 192) {
+    // 128+ tokens and enough 64 x 64 tiles to fill the chip (qkv_a at 256 tokens, 228
+    // workgroups: 12.9 vs 16.1 us in the decode step); N = 2048 gives only 128 and stays on
+    // the token-rows-in-LDS shape's 32-token tiles (o_proj 12.9 vs 14.0 us)
+    launch_dma(a, st);
+    return true;
+  }
   if (swiglu && K > 512 && rows > 64 && a.N % 64 == 0) {
     // 64-token tiles, 64 features (gate + up rows) per workgroup, two token chunks in flight
     // (shared experts at 256 tokens: 22.4 us vs 28.8 us for the one-shot shape)

@@ -176,6 +176,24 @@ def test_gemm_dense_model_shapes(rows, K, N, mode):
     assert rel_err(y.float(), ref) < 1e-2
 
 
+@pytest.mark.parametrize("rows", [200, 256])
+@pytest.mark.parametrize("mode", ["plain", "residual", "f32"])
+def test_gemm_wide_dense_epilogues(rows, mode):
+    """Wide dense outputs at 128+ tokens (the direct-to-LDS ring shape: N = 3648, 64 x 64
+    tiles, XCD-aware grid), every epilogue, a partial last token tile at 200 rows."""
+    K, N = 2048, 3648
+    x = rnd(rows, K, seed=rows + 7)
+    W = rnd(N, K, std=0.02, seed=8)
+    res = rnd(rows, N, seed=9) if mode == "residual" else None
+    flags = LINEAR_OUT_F32 if mode == "f32" else 0
+    y = torch.empty(rows, N, dtype=torch.float32 if mode == "f32" else BF, device=DEV)
+    call("dsv2_gemm_bf16", x.data_ptr(), K, 0, rows, K, W.data_ptr(), 0, N, 1, _hip.ptr(res), N, y.data_ptr(), N, 0,
+         flags, st())
+    acc = x.float() @ W.float().t()
+    ref = rb(res.float() + rb(acc)) if mode == "residual" else rb(acc)
+    assert rel_err(y.float(), ref) < 1e-2
+
+
 @pytest.mark.parametrize("rows", [1, 5, 64, 200, 256])
 def test_gemm_grouped_heads_absorption(rows):
     # q_lat[r, h, :512] = W_UK_h^T q_nope[r, h]   and   attn[r, h*128+i] = W_UV_h o_lat[r, h]
