@@ -43,11 +43,25 @@ SPLIT_ROUTER_MAX_ROWS = 64
 
 
 def moe_tile_tokens(rows: int, n_experts: int = 64, top_k: int = 6) -> int:
-    """Token tile of the expert-grouped MoE GEMMs from the mean routes per expert.  Measured
-    on MI355X (gate_up + down per layer): 16-token tiles at 6 routes/expert (bsz=64), 32-token
-    tiles at 24 (bsz=256: 250 us vs 289 us with 16 and 313 us with 64)."""
-    avg = rows * top_k / n_experts
-    return 16 if avg <= 10 else (32 if avg <= 40 else 64)
+    """Token tile of the expert-grouped MoE GEMMs before any routing has been seen, from the
+    mean routes per expert under uniform routing (see tile_tokens_for_load)."""
+    return tile_tokens_for_load(rows * top_k / n_experts)
+
+
+def tile_tokens_for_load(load: float) -> int:
+    """Token tile for a mean of `load` routes per routed expert.  Measured on MI355X (gate_up +
+    down per layer): 16-token tiles at 6 routes/expert (bsz=64, random prompts), 32-token
+    tiles at 24 (bsz=256: 250 us vs 289 us with 16 and 313 us with 64), 64-token tiles when
+    every row takes the same 6 experts (bsz=64: 34.8 us vs 48.2 us with 16)."""
+    return 16 if load <= 10 else (32 if load <= 40 else 64)
+
+
+def routing_load(ids: torch.Tensor, n_experts: int = 64) -> float:
+    """Mean number of routes in the expert a route goes to (sum c_e^2 / sum c_e over the
+    per-expert route counts c_e of one layer's top-k ids): the tile occupancy the grouped
+    GEMMs see, ~rows*k/E + 1 for uniform routing, rows for identical rows."""
+    c = torch.bincount(ids.reshape(-1).to(torch.int64).cpu(), minlength=n_experts).double()
+    return float((c * c).sum() / c.sum().clamp(min=1))
 
 
 class RowBuffers:
@@ -75,16 +89,26 @@ class RowBuffers:
         else:
             R = rows * cfg.top_k
             self.olat = e(rows, cfg.n_heads, cfg.kv_rank)
+            self._routes, self._n_experts = R, cfg.n_experts
             self.tile_tokens = moe_tile_tokens(rows, cfg.n_experts, cfg.top_k)
             self.max_tiles = math.ceil(R / self.tile_tokens) + cfg.n_experts
             self.sorted = e(R, dt=torch.int32)
             self.route_pos = e(R, dt=torch.int32)
-            self.tiles = e(self.max_tiles, 4, dt=torch.int32)
+            self.tiles = e(math.ceil(R / 16) + cfg.n_experts, 4, dt=torch.int32)  # room for any tile size
             self.ntiles = e(1, dt=torch.int32)
             self.hs = e(R, cfg.moe_inter)
             self.ys = e(R, H)
             self.shmid = e(rows, cfg.shared_inter)
             self.shout = e(rows, H)
+
+
+    def set_tile_tokens(self, tile_tokens: int) -> None:
+        """Token tile of the grouped MoE launches (16, 32 or 64); the tile table was sized
+        for the smallest."""
+        if tile_tokens not in (16, 32, 64):
+            raise ValueError(f"tile_tokens must be 16, 32 or 64, got {tile_tokens}")
+        self.tile_tokens = tile_tokens
+        self.max_tiles = math.ceil(self._routes / tile_tokens) + self._n_experts
 
 
 class DecodeEngine:
@@ -308,8 +332,28 @@ class DecodeEngine:
         self.ids.copy_(ids)
         self._host_pos = list(host)
 
+    def tune_moe_tiles(self) -> int:
+        """Batch family: pick the grouped MoE token tile from the routing of one eager step
+        (state restored afterwards), like the reference's tile selection before capture
+        (moe_batch.py:596-657) but without timing runs: the median over MoE layers of
+        routing_load, mapped by tile_tokens_for_load.  Returns the tile."""
+        if self.family != "batch":
+            return 0
+        snap = self.snapshot()
+        rec: list = []
+        self.step(record=rec)
+        self.restore(snap)
+        loads = sorted(routing_load(r[2], self.cfg.n_experts) for r in rec if r[0] == "router")
+        tile = tile_tokens_for_load(loads[len(loads) // 2]) if loads else self.buf.tile_tokens
+        self.buf.set_tile_tokens(tile)
+        self._moe_tiles_tuned = True
+        return tile
+
     def capture(self) -> torch.cuda.CUDAGraph:
-        """Record one step() into a graph (positions/ids advance on every replay)."""
+        """Record one step() into a graph (positions/ids advance on every replay).  The batch
+        family first picks its MoE token tile from one eager step (tune_moe_tiles)."""
+        if self.family == "batch" and not getattr(self, "_moe_tiles_tuned", False):
+            self.tune_moe_tiles()
         saved = list(self._host_pos)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):

@@ -92,6 +92,14 @@ def test_moe_tile_choice_and_cache_layout():
 
     assert moe_tile_tokens(1) == 16 and moe_tile_tokens(64) == 16 and moe_tile_tokens(256) == 32
     assert moe_tile_tokens(512) == 64
+    from dsv2lite.engine import routing_load, tile_tokens_for_load
+
+    g = torch.Generator().manual_seed(0)
+    uniform = torch.stack([torch.randperm(64, generator=g)[:6] for _ in range(64)])
+    same = torch.tensor([7, 16, 25, 34, 43, 52]).repeat(64, 1)
+    assert 6 < routing_load(uniform) < 10 and tile_tokens_for_load(routing_load(uniform)) == 16
+    assert routing_load(same) == 64 and tile_tokens_for_load(routing_load(same)) == 64
+    assert tile_tokens_for_load(24.5) == 32
     c = CompressedKVCache(2, [5, 7, 3], device="cpu")
     assert c.base.tolist() == [0, 5, 12] and c.total == 15 and c.data.shape == (2, 15, 576)
     c.pos.copy_(torch.tensor([1, 2, 3], dtype=torch.int32))
