@@ -712,15 +712,16 @@ static bool launch_dense_os(GemmArgs a, int groups, bool swiglu, hipStream_t st)
     else launch_xlds_variant<2, false, 4, true, 2>(a, a.tiles_per_group, st);
     return true;
   }
-  if (K > 4096 || (int64_t)a.N * groups >= 16384) return false;
-  if (!swiglu && groups == 1 && rows > 128 && K <= 4096 && a.N % 64 == 0 && a.N < 16384 &&
-      (a.N / 64) * ((rows + 63) / 64) >= 192) {
-    // 128+ tokens and enough 64 x 64 tiles to fill the chip (qkv_a at 256 tokens, 228
-    // workgroups: 12.9 vs 16.1 us in the decode step); N = 2048 gives only 128 and stays on
-    // the token-rows-in-LDS shape's 32-token tiles (o_proj 12.9 vs 14.0 us)
+  if (!swiglu && groups == 1 && K <= 4096 && a.N % 64 == 0 &&
+      ((rows > 128 && (a.N / 64) * ((rows + 63) / 64) >= 192) || (rows > 32 && a.N >= 16384))) {
+    // direct-to-LDS ring: 128+ tokens with enough 64 x 64 tiles to fill the chip (qkv_a at
+    // 256 tokens, 228 workgroups: 12.9 vs 16.1 us in the decode step; N = 2048 gives only 128
+    // and stays on the token-rows-in-LDS shape's 32-token tiles, o_proj 12.9 vs 14.0 us), and
+    // the lm_head (N = 102400) from 33 tokens (64: 104 vs 121 us; 256: 251 vs 301 us)
     launch_dma(a, st);
     return true;
   }
+  if (K > 4096 || (int64_t)a.N * groups >= 16384) return false;
   if (swiglu && K > 512 && rows > 64 && a.N % 64 == 0) {
     // 64-token tiles, 64 features (gate + up rows) per workgroup, two token chunks in flight
     // (shared experts at 256 tokens: 22.4 us vs 28.8 us for the one-shot shape)
