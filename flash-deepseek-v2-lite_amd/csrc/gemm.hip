@@ -383,14 +383,19 @@ struct DmaShape {
   int tiles, nwg;
 };
 
+// SWIGLU: the 64 weight rows of a workgroup are, per 16 features, 16 gate rows then the 16
+// matching up rows (32 features per workgroup); a wave's two row blocks are then one
+// feature block's gate and up tiles, combined in its epilogue.
+template <bool SWIGLU>
 __global__ __launch_bounds__(256) void gemm_dma_kernel(const GemmArgs a, const DmaShape sh) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // kDmaStages * 16 KB
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, li = lane & 15, kg = lane >> 4;
   const int per = sh.nwg / 8;
   const int w = (blockIdx.x % 8) * per + blockIdx.x / 8;
-  if (w >= (a.N / 64) * sh.tiles) return;
+  constexpr int FPW = SWIGLU ? 32 : 64;  // output features per workgroup
+  if (w >= (a.N / FPW) * sh.tiles) return;
   const int tile = w % sh.tiles, fb = w / sh.tiles;
-  const int f0 = fb * 64, t0 = tile * 64, count = min(64, a.rows - t0);
+  const int f0 = fb * FPW, t0 = tile * 64, count = min(64, a.rows - t0);
   const int K = a.K, nch = K / 64;
   // this wave's 4 ring loads per chunk: weight rows 16wv .. 16wv+15 (j = 0, 1) and token rows
   // 16wv .. 16wv+15 (j = 2, 3), 8 rows per load; lane -> (row r, slot lane & 7), which holds
@@ -402,6 +407,7 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const GemmArgs a, const D
     const int r = 16 * wv + 8 * (j & 1) + (lane >> 3);
     const int pc = (lane & 7) ^ (r & 7);
     if (j >= 2) src[j] = a.X + (int64_t)(t0 + (r < count ? r : 0)) * a.xs + pc * 8;  // rows past the tile: row t0
+    else if (SWIGLU) src[j] = a.W + (int64_t)(f0 + (r >> 5) * 16 + ((r >> 4) & 1) * a.N + (r & 15)) * K + pc * 8;
     else src[j] = a.W + (int64_t)(f0 + r) * K + pc * 8;
     dst[j] = (j >= 2 ? 8192 : 0) + (16 * wv + 8 * (j & 1)) * 128;
   }
@@ -451,6 +457,17 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const GemmArgs a, const D
   }
   // the repeats past the last chunk must land before the workgroup's LDS is released
   __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+  if (SWIGLU) {
+#pragma unroll
+    for (int y = 0; y < 2; ++y) {
+      if (wt + 16 * y + li >= count) continue;
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = swiglu_bf(acc[0][y][e], acc[1][y][e]);
+      gemm_store4(a, 0, t0 + wt + 16 * y + li, f0 + (wa >> 1) + 4 * kg, v);
+    }
+    return;
+  }
 #pragma unroll
   for (int x = 0; x < 2; ++x)
 #pragma unroll
@@ -463,11 +480,12 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const GemmArgs a, const D
     }
 }
 
-static void launch_dma(const GemmArgs& a, hipStream_t st) {
+static void launch_dma(const GemmArgs& a, bool swiglu, hipStream_t st) {
   DmaShape sh;
   sh.tiles = (a.rows + 63) / 64;
-  sh.nwg = ((a.N / 64) * sh.tiles + 7) / 8 * 8;
-  hipLaunchKernelGGL(gemm_dma_kernel, dim3(sh.nwg), dim3(256), kDmaStages * 16384, st, a, sh);
+  sh.nwg = ((a.N / (swiglu ? 32 : 64)) * sh.tiles + 7) / 8 * 8;
+  if (swiglu) hipLaunchKernelGGL(gemm_dma_kernel<true>, dim3(sh.nwg), dim3(256), kDmaStages * 16384, st, a, sh);
+  else hipLaunchKernelGGL(gemm_dma_kernel<false>, dim3(sh.nwg), dim3(256), kDmaStages * 16384, st, a, sh);
 }
 
 // One-shot shape for dense weights and few tokens (the row blocks alone cannot fill the
@@ -718,7 +736,13 @@ static bool launch_dense_os(GemmArgs a, int groups, bool swiglu, hipStream_t st)
     // 256 tokens, 228 workgroups: 12.9 vs 16.1 us in the decode step; N = 2048 gives only 128
     // and stays on the token-rows-in-LDS shape's 32-token tiles, o_proj 12.9 vs 14.0 us), and
     // the lm_head (N = 102400) from 33 tokens (64: 104 vs 121 us; 256: 251 vs 301 us)
-    launch_dma(a, st);
+    launch_dma(a, false, st);
+    return true;
+  }
+  if (swiglu && groups == 1 && K <= 4096 && a.N % 32 == 0 && rows > 128) {
+    // SwiGLU on the ring (32 features x 64 tokens per workgroup): shared experts and the dense
+    // layer-0 gate_up above 128 tokens (reference workload at 256 rows 39.3k -> 39.4k tok/s)
+    launch_dma(a, true, st);
     return true;
   }
   if (K > 4096 || (int64_t)a.N * groups >= 16384) return false;
