@@ -51,8 +51,9 @@ def moe_tile_tokens(rows: int, n_experts: int = 64, top_k: int = 6) -> int:
 def tile_tokens_for_load(load: float) -> int:
     """Token tile for a mean of `load` routes per routed expert.  Measured on MI355X (gate_up +
     down per layer): 16-token tiles at 6 routes/expert (bsz=64, random prompts), 32-token
-    tiles at 24 (bsz=256: 250 us vs 289 us with 16 and 313 us with 64), 64-token tiles when
-    every row takes the same 6 experts (bsz=64: 34.8 us vs 48.2 us with 16)."""
+    tiles at 24 (bsz=256: 250 us vs 289 us with 16; 64-token tiles, on the direct-to-LDS ring
+    GEMM, tie with 32 there: 21.73k vs 21.77k tok/s), 64-token tiles when every row takes
+    the same 6 experts (bsz=64: 19.1k tok/s vs 17.0k with 32)."""
     return 16 if load <= 10 else (32 if load <= 40 else 64)
 
 

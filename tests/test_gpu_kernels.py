@@ -372,6 +372,48 @@ def test_moe_batch_family_grouped(rows):
     assert torch.equal(out, out2)
 
 
+@pytest.mark.parametrize("rows,replicated", [(64, True), (200, True), (150, False)])
+def test_moe_grouped_tile_sizes(rows, replicated):
+    """Bucketing + grouped gate_up / down + combine with 16-, 32- and 64-token expert tiles
+    (64: the direct-to-LDS ring GEMM; replicated rows give full and partial 64-token tiles,
+    random routing mostly near-empty ones) against the oracle on a subset of rows."""
+    gu, dn, sgu, sdn = _moe_layer(60)
+    xn = rnd(rows, 2048, seed=61)
+    g = torch.Generator().manual_seed(62)
+    if replicated:
+        ids = torch.randperm(64, generator=g)[:6].repeat(rows, 1)
+    else:
+        ids = torch.stack([torch.randperm(64, generator=g)[:6] for _ in range(rows)])
+    w = torch.rand(rows, 6, generator=g) * 0.3
+    ids32, wd = ids.to(torch.int32).to(DEV), w.to(DEV)
+    R = rows * 6
+    outs = {}
+    for tt in (16, 32, 64):
+        max_tiles = math.ceil(R / tt) + 64
+        srt = torch.empty(R, dtype=torch.int32, device=DEV)
+        rpos = torch.empty(R, dtype=torch.int32, device=DEV)
+        tiles = torch.empty(max_tiles, 4, dtype=torch.int32, device=DEV)
+        nt = torch.empty(1, dtype=torch.int32, device=DEV)
+        hs = torch.empty(R, 1408, dtype=BF, device=DEV)
+        ys = torch.empty(R, 2048, dtype=BF, device=DEV)
+        out = torch.empty(rows, 2048, dtype=BF, device=DEV)
+        call("dsv2_moe_bucket", ids32.data_ptr(), rows, tt, srt.data_ptr(), rpos.data_ptr(), tiles.data_ptr(),
+             nt.data_ptr(), st())
+        call("dsv2_moe_grouped_gateup", xn.data_ptr(), srt.data_ptr(), tiles.data_ptr(), nt.data_ptr(), max_tiles, tt,
+             gu.data_ptr(), 1408, hs.data_ptr(), st())
+        call("dsv2_moe_grouped_down", hs.data_ptr(), tiles.data_ptr(), nt.data_ptr(), max_tiles, tt, dn.data_ptr(),
+             1408, ys.data_ptr(), st())
+        call("dsv2_moe_combine", ys.data_ptr(), rpos.data_ptr(), wd.data_ptr(), rows, None, None, out.data_ptr(), None,
+             0.0, None, st())
+        outs[tt] = out.float().cpu()
+    c = lambda t: t.float().cpu()  # noqa: E731
+    sel = list(range(0, rows, max(1, rows // 20)))
+    routed, _ = _oracle_moe_parts(c(xn)[sel], ids[sel], w[sel], c(gu), c(dn), c(sgu), c(sdn))
+    for tt, out in outs.items():
+        assert rel_err(out[sel], routed) < 1e-2, tt
+        assert rel_err(out, outs[16]) < 1e-2, tt
+
+
 def _mla_reference(q, cache_rows, lens, scale):
     """fp32 softmax(q . c^T * scale) . c[:, :512] per row (o_lat [B, 16, 512])."""
     outs = []
