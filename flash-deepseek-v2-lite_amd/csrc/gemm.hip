@@ -28,6 +28,14 @@ struct GemmArgs {
   void* Y;
   int64_t ys, yg;
   bool out_f32;
+  // grouped ring GEMM: the shared-expert halves (one 64-token tile per `rows` chunk and half,
+  // after the table's tiles): half h's gate rows at W2 + h*w2g, row stride w2ld, up row =
+  // gate row + w2up; token t of half h -> Y2[t * y2s + h * y2g + n] (bf16, no residual)
+  const bf16_t* W2;
+  int64_t w2g;
+  int w2ld, w2up, s_tiles;
+  bf16_t* Y2;
+  int64_t y2s, y2g;
 };
 
 template <int TB, bool SWIGLU, int NW, int U>
@@ -395,14 +403,23 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const GemmArgs a, const D
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, li = lane & 15, kg = lane >> 4;
   constexpr int FPW = SWIGLU ? 32 : 64;  // output features per workgroup
   int fb, g = 0, t0, count;
+  bool shared = false;
   if (a.tiles) {
     const int tile = blockIdx.x / sh.nfb;
     fb = blockIdx.x % sh.nfb;
-    if (tile >= a.ntiles[0]) return;
-    const int4 tt = reinterpret_cast<const int4*>(a.tiles)[tile];
-    g = tt.x;
-    t0 = tt.y;
-    count = tt.z;
+    if (tile >= sh.tiles) {  // a shared-expert half's tile of tokens
+      const int s = tile - sh.tiles;
+      shared = true;
+      g = s / a.s_tiles;
+      t0 = (s % a.s_tiles) * 64;
+      count = min(64, a.rows - t0);
+    } else {
+      if (tile >= a.ntiles[0]) return;
+      const int4 tt = reinterpret_cast<const int4*>(a.tiles)[tile];
+      g = tt.x;
+      t0 = tt.y;
+      count = tt.z;
+    }
   } else {
     const int per = sh.nwg / 8;
     const int w = (blockIdx.x % 8) * per + blockIdx.x / 8;
@@ -417,6 +434,9 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const GemmArgs a, const D
   // this wave's 4 ring loads per chunk: weight rows 16wv .. 16wv+15 (j = 0, 1) and token rows
   // 16wv .. 16wv+15 (j = 2, 3), 8 rows per load; lane -> (row r, slot lane & 7), which holds
   // piece (lane & 7) ^ (r & 7)
+  const bf16_t* const wbase = shared ? a.W2 + g * a.w2g : a.W + g * a.wg;
+  const int64_t wld = shared ? a.w2ld : K;
+  const int upoff = shared ? a.w2up : a.N;
   const bf16_t* src[4];
   int dst[4];
 #pragma unroll
@@ -425,12 +445,12 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const GemmArgs a, const D
     const int pc = (lane & 7) ^ (r & 7);
     if (j >= 2) {
       const int slot = t0 + (r < count ? r : 0);  // rows past the tile: the tile's first row
-      const int row = a.slot_row ? a.slot_row[slot] / a.slot_div : slot;
-      src[j] = a.X + g * a.xg + (int64_t)row * a.xs + pc * 8;
+      const int row = a.slot_row && !shared ? a.slot_row[slot] / a.slot_div : slot;
+      src[j] = a.X + (shared ? 0 : g * a.xg) + (int64_t)row * a.xs + pc * 8;
     } else if (SWIGLU) {
-      src[j] = a.W + g * a.wg + (int64_t)(f0 + (r >> 5) * 16 + ((r >> 4) & 1) * a.N + (r & 15)) * K + pc * 8;
+      src[j] = wbase + (f0 + (r >> 5) * 16 + ((r >> 4) & 1) * upoff + (r & 15)) * wld + pc * 8;
     } else {
-      src[j] = a.W + g * a.wg + (int64_t)(f0 + r) * K + pc * 8;
+      src[j] = wbase + (f0 + r) * wld + pc * 8;
     }
     dst[j] = (j >= 2 ? 8192 : 0) + (16 * wv + 8 * (j & 1)) * 128;
   }
@@ -487,7 +507,15 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const GemmArgs a, const D
       float v[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] = swiglu_bf(acc[0][y][e], acc[1][y][e]);
-      gemm_store4(a, g, t0 + wt + 16 * y + li, f0 + (wa >> 1) + 4 * kg, v);
+      if (shared) {
+        uint2 o;
+        o.x = pack2(v[0], v[1]);
+        o.y = pack2(v[2], v[3]);
+        *reinterpret_cast<uint2*>(a.Y2 + (int64_t)(t0 + wt + 16 * y + li) * a.y2s + g * a.y2g + f0 + (wa >> 1) +
+                                  4 * kg) = o;
+      } else {
+        gemm_store4(a, g, t0 + wt + 16 * y + li, f0 + (wa >> 1) + 4 * kg, v);
+      }
     }
     return;
   }
@@ -508,7 +536,7 @@ static void launch_dma(const GemmArgs& a, bool swiglu, hipStream_t st, int max_t
   DmaShape sh;
   sh.nfb = a.N / (swiglu ? 32 : 64);
   sh.tiles = a.tiles ? max_tiles : (a.rows + 63) / 64;
-  sh.nwg = a.tiles ? sh.nfb * sh.tiles : (sh.nfb * sh.tiles + 7) / 8 * 8;
+  sh.nwg = a.tiles ? sh.nfb * (sh.tiles + (a.W2 ? 2 * a.s_tiles : 0)) : (sh.nfb * sh.tiles + 7) / 8 * 8;
   if (swiglu) hipLaunchKernelGGL(gemm_dma_kernel<true>, dim3(sh.nwg), dim3(256), kDmaStages * 16384, st, a, sh);
   else hipLaunchKernelGGL(gemm_dma_kernel<false>, dim3(sh.nwg), dim3(256), kDmaStages * 16384, st, a, sh);
 }
@@ -886,6 +914,45 @@ extern "C" int dsv2_moe_grouped_gateup(const void* xn, const int32_t* sorted_rou
     return dsv2_launch_status("moe_grouped_gateup");
   }
   return launch_gemm(a, tile_tb(tile_tokens), true, max_tiles, (hipStream_t)stream);
+}
+
+extern "C" int dsv2_moe_grouped_gateup_shared(const void* xn, int rows, const int32_t* sorted_routes,
+                                              const int32_t* tiles, const int32_t* num_tiles, int max_tiles,
+                                              const void* w_gate_up, const void* sh_gate_up, int inter, void* hsorted,
+                                              void* shared_out, void* stream) {
+  DSV2_REQUIRE(xn && sorted_routes && tiles && num_tiles && w_gate_up && sh_gate_up && hsorted && shared_out,
+               DSV2_E_NULL, "moe_grouped_gateup_shared: null pointer");
+  DSV2_REQUIRE(rows >= 0 && max_tiles >= 0 && inter > 0 && inter % 32 == 0 &&
+                   ((int64_t)max_tiles + 2 * ((rows + 63) / 64)) * (inter / 32) <= 0x7fffffff,
+               DSV2_E_SHAPE, "moe_grouped_gateup_shared: bad shape (inter %% 32)");
+  DSV2_REQUIRE(dsv2_aligned16(xn) && dsv2_aligned16(w_gate_up) && dsv2_aligned16(sh_gate_up) &&
+                   dsv2_aligned16(tiles) && dsv2_aligned16(shared_out),
+               DSV2_E_ALIGN, "moe_grouped_gateup_shared: alignment");
+  if (rows == 0) return DSV2_OK;
+  GemmArgs a{};
+  a.X = (const bf16_t*)xn;
+  a.xs = 2048;
+  a.slot_row = sorted_routes;
+  a.slot_div = 6;
+  a.tiles = tiles;
+  a.ntiles = num_tiles;
+  a.rows = rows;
+  a.W = (const bf16_t*)w_gate_up;
+  a.wg = (int64_t)2 * inter * 2048;
+  a.N = inter;
+  a.K = 2048;
+  a.Y = hsorted;
+  a.ys = inter;
+  a.W2 = (const bf16_t*)sh_gate_up;
+  a.w2g = (int64_t)inter * 2048;
+  a.w2ld = 2048;
+  a.w2up = 2 * inter;
+  a.s_tiles = (rows + 63) / 64;
+  a.Y2 = (bf16_t*)shared_out;
+  a.y2s = 2 * inter;
+  a.y2g = inter;
+  launch_dma(a, true, (hipStream_t)stream, max_tiles);
+  return dsv2_launch_status("moe_grouped_gateup_shared");
 }
 
 extern "C" int dsv2_moe_grouped_down(const void* hsorted, const int32_t* tiles, const int32_t* num_tiles,

@@ -213,12 +213,18 @@ class DecodeEngine:
                      ptr(b.xn), ptr(b.ids32), None, ptr(b.wts), st)
             call("dsv2_moe_bucket", ptr(b.ids32), R, b.tile_tokens, ptr(b.sorted), ptr(b.route_pos), ptr(b.tiles),
                  ptr(b.ntiles), st)
-            call("dsv2_moe_grouped_gateup", ptr(b.xn), ptr(b.sorted), ptr(b.tiles), ptr(b.ntiles), b.max_tiles,
-                 b.tile_tokens, ptr(L.w_gu), c.moe_inter, ptr(b.hs), st)
+            if b.tile_tokens == 64:
+                # 64-token tiles: the shared experts' gate_up rides in the grouped launch
+                call("dsv2_moe_grouped_gateup_shared", ptr(b.xn), R, ptr(b.sorted), ptr(b.tiles), ptr(b.ntiles),
+                     b.max_tiles, ptr(L.w_gu), ptr(L.sh_gu), c.moe_inter, ptr(b.hs), ptr(b.shmid), st)
+            else:
+                call("dsv2_moe_grouped_gateup", ptr(b.xn), ptr(b.sorted), ptr(b.tiles), ptr(b.ntiles), b.max_tiles,
+                     b.tile_tokens, ptr(L.w_gu), c.moe_inter, ptr(b.hs), st)
             call("dsv2_moe_grouped_down", ptr(b.hs), ptr(b.tiles), ptr(b.ntiles), b.max_tiles, b.tile_tokens,
                  ptr(L.w_down), c.moe_inter, ptr(b.ys), st)
-            call("dsv2_gemm_bf16", ptr(b.xn), H, 0, R, H, ptr(L.sh_gu), 0, c.shared_inter, 1, None, 0, ptr(b.shmid),
-                 c.shared_inter, 0, LINEAR_SWIGLU, st)
+            if b.tile_tokens != 64:
+                call("dsv2_gemm_bf16", ptr(b.xn), H, 0, R, H, ptr(L.sh_gu), 0, c.shared_inter, 1, None, 0,
+                     ptr(b.shmid), c.shared_inter, 0, LINEAR_SWIGLU, st)
             call("dsv2_gemm_bf16", ptr(b.shmid), c.shared_inter, 0, R, c.shared_inter, ptr(L.sh_down), 0, H, 1,
                  None, 0, ptr(b.shout), H, 0, 0, st)
             call("dsv2_moe_combine", ptr(b.ys), ptr(b.route_pos), ptr(b.wts), R, ptr(b.shout), ptr(b.h), ptr(b.h),

@@ -230,6 +230,16 @@ int dsv2_moe_grouped_gateup(const void* xn, const int32_t* sorted_routes, const 
                             const int32_t* num_tiles, int max_tiles, int tile_tokens, const void* w_gate_up,
                             int inter, void* hsorted, void* stream);
 
+/* dsv2_moe_grouped_gateup with 64-token tiles, plus the two shared-expert halves in the same
+ * launch: shared_out[t, h*inter + i] = SwiGLU(xn[t] . gate/up rows h*inter + i of sh_gate_up)
+ * for t < rows, h = 0, 1 (sh_gate_up [2*2*inter, 2048]: gate rows, then up rows), i.e. the
+ * dense shared gate_up of dsv2_gemm_bf16 with DSV2_LINEAR_SWIGLU.  The tile table must come
+ * from dsv2_moe_bucket with tile_tokens = 64.  Replaces _grouped_gate_up_swiglu_kernel
+ * (moe_batch.py:152-234) and the shared MLP's gate_proj / up_proj + SiLU-mul (src/run.py:341-351). */
+int dsv2_moe_grouped_gateup_shared(const void* xn, int rows, const int32_t* sorted_routes, const int32_t* tiles,
+                                   const int32_t* num_tiles, int max_tiles, const void* w_gate_up,
+                                   const void* sh_gate_up, int inter, void* hsorted, void* shared_out, void* stream);
+
 /* Expert-grouped down projection: ysorted[p, :] = bf16(hsorted[p, :] . Wd_e^T).
  * Replaces _grouped_down_partial_kernel (moe_batch.py:238-307) with a bf16 result
  * (the expert output's own rounding point) instead of an fp32 partial. */

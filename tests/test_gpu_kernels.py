@@ -414,6 +414,44 @@ def test_moe_grouped_tile_sizes(rows, replicated):
         assert rel_err(out, outs[16]) < 1e-2, tt
 
 
+@pytest.mark.parametrize("rows,replicated", [(64, True), (130, False)])
+def test_moe_grouped_gateup_with_shared(rows, replicated):
+    """The 64-token grouped gate_up with the shared halves in the same launch: routed rows
+    equal dsv2_moe_grouped_gateup's bit for bit, the shared output matches the fp32 SwiGLU
+    reference and the dense shared gate_up."""
+    gu, dn, sgu, sdn = _moe_layer(70)
+    xn = rnd(rows, 2048, seed=71)
+    g = torch.Generator().manual_seed(72)
+    if replicated:
+        ids = torch.randperm(64, generator=g)[:6].repeat(rows, 1)
+    else:
+        ids = torch.stack([torch.randperm(64, generator=g)[:6] for _ in range(rows)])
+    ids32 = ids.to(torch.int32).to(DEV)
+    R = rows * 6
+    max_tiles = math.ceil(R / 64) + 64
+    srt = torch.empty(R, dtype=torch.int32, device=DEV)
+    rpos = torch.empty(R, dtype=torch.int32, device=DEV)
+    tiles = torch.empty(max_tiles, 4, dtype=torch.int32, device=DEV)
+    nt = torch.empty(1, dtype=torch.int32, device=DEV)
+    call("dsv2_moe_bucket", ids32.data_ptr(), rows, 64, srt.data_ptr(), rpos.data_ptr(), tiles.data_ptr(),
+         nt.data_ptr(), st())
+    hs_ref = torch.empty(R, 1408, dtype=BF, device=DEV)
+    call("dsv2_moe_grouped_gateup", xn.data_ptr(), srt.data_ptr(), tiles.data_ptr(), nt.data_ptr(), max_tiles, 64,
+         gu.data_ptr(), 1408, hs_ref.data_ptr(), st())
+    hs = torch.empty_like(hs_ref)
+    sh = torch.empty(rows, 2816, dtype=BF, device=DEV)
+    call("dsv2_moe_grouped_gateup_shared", xn.data_ptr(), rows, srt.data_ptr(), tiles.data_ptr(), nt.data_ptr(),
+         max_tiles, gu.data_ptr(), sgu.data_ptr(), 1408, hs.data_ptr(), sh.data_ptr(), st())
+    assert torch.equal(hs, hs_ref)
+    acc = xn.float() @ sgu.float().t()
+    ref = rb(rb(torch.nn.functional.silu(rb(acc[:, :2816]))) * rb(acc[:, 2816:]))
+    assert rel_err(sh.float(), ref) < 1e-2
+    dense = torch.empty_like(sh)
+    call("dsv2_gemm_bf16", xn.data_ptr(), 2048, 0, rows, 2048, sgu.data_ptr(), 0, 2816, 1, None, 0, dense.data_ptr(),
+         2816, 0, LINEAR_SWIGLU, st())
+    assert rel_err(sh.float(), dense.float()) < 1e-2
+
+
 def _mla_reference(q, cache_rows, lens, scale):
     """fp32 softmax(q . c^T * scale) . c[:, :512] per row (o_lat [B, 16, 512])."""
     outs = []
