@@ -29,12 +29,15 @@ struct GemmArgs {
   int64_t ys, yg;
   bool out_f32;
   // grouped ring GEMM: the shared-expert halves (one 64-token tile per `rows` chunk and half,
-  // after the table's tiles): half h's gate rows at W2 + h*w2g, row stride w2ld, up row =
-  // gate row + w2up; token t of half h -> Y2[t * y2s + h * y2g + n] (bf16, no residual)
+  // after the table's tiles): half h reads token t at X2 + h*x2g + t*x2s, its (gate) weight
+  // rows at W2 + h*w2g with row stride w2ld (SwiGLU: up row = gate row + w2up), and writes
+  // Y2[h * y2g + t * y2s + n] (SwiGLU: bf16; plain: the fp32 partial sum; no residual)
+  const bf16_t* X2;
+  int64_t x2s, x2g;
   const bf16_t* W2;
   int64_t w2g;
   int w2ld, w2up, s_tiles;
-  bf16_t* Y2;
+  void* Y2;
   int64_t y2s, y2g;
 };
 
@@ -383,152 +386,170 @@ __device__ __forceinline__ void gemm_store4(const GemmArgs& a, int g, int slot, 
 // first hit that XCD's L2 (qkv_a at 256 tokens: 12.2 us vs 17.9 us for the token-rows-in-LDS
 // shape; without the XCD grouping 18.3 us).
 constexpr int kDmaStages = 4;
+constexpr int kDmaGroupedWgs = 512;  // 256 CUs x 2 (64 KB of LDS each)
 // s_waitcnt immediate (gfx9 encoding): wait until at most n vector-memory operations are
 // outstanding, leaving the LDS/scalar (15) and export (7) counters unconstrained
 constexpr int vmcnt_only(int n) { return (n & 0xf) | (0x7 << 4) | (0xf << 8) | (((n >> 4) & 3) << 14); }
 
 struct DmaShape {
-  int tiles, nwg, nfb;
+  int tiles, nwg, nfb, items;
 };
 
 // SWIGLU: the 64 weight rows of a workgroup are, per 16 features, 16 gate rows then the 16
 // matching up rows (32 features per workgroup); a wave's two row blocks are then one
 // feature block's gate and up tiles, combined in its epilogue.
-// Grouped (a.tiles, 64-token expert tiles): work item w = blockIdx.x = tile * nfb + fb, so
-// the live tiles' workgroups come first and go round-robin over the XCDs; token rows are
-// gathered through slot_row and the tile's expert selects the weights.
+// Grouped (a.tiles, 64-token expert tiles): a grid of at most kDmaGroupedWgs workgroups
+// loops over the items tile * nfb + fb (consecutive items go round-robin over the XCDs), so
+// the table's dead tiles cost no workgroup launches; token rows are gathered through
+// slot_row and the tile's expert selects the weights.
 template <bool SWIGLU>
 __global__ __launch_bounds__(256) void gemm_dma_kernel(const GemmArgs a, const DmaShape sh) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // kDmaStages * 16 KB
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, li = lane & 15, kg = lane >> 4;
   constexpr int FPW = SWIGLU ? 32 : 64;  // output features per workgroup
-  int fb, g = 0, t0, count;
-  bool shared = false;
-  if (a.tiles) {
-    const int tile = blockIdx.x / sh.nfb;
-    fb = blockIdx.x % sh.nfb;
-    if (tile >= sh.tiles) {  // a shared-expert half's tile of tokens
-      const int s = tile - sh.tiles;
-      shared = true;
-      g = s / a.s_tiles;
-      t0 = (s % a.s_tiles) * 64;
-      count = min(64, a.rows - t0);
-    } else {
-      if (tile >= a.ntiles[0]) return;
-      const int4 tt = reinterpret_cast<const int4*>(a.tiles)[tile];
-      g = tt.x;
-      t0 = tt.y;
-      count = tt.z;
-    }
-  } else {
-    const int per = sh.nwg / 8;
-    const int w = (blockIdx.x % 8) * per + blockIdx.x / 8;
-    if (w >= sh.nfb * sh.tiles) return;
-    const int tile = w % sh.tiles;
-    fb = w / sh.tiles;
-    t0 = tile * 64;
-    count = min(64, a.rows - t0);
-  }
-  const int f0 = fb * FPW;
-  const int K = a.K, nch = K / 64;
-  // this wave's 4 ring loads per chunk: weight rows 16wv .. 16wv+15 (j = 0, 1) and token rows
-  // 16wv .. 16wv+15 (j = 2, 3), 8 rows per load; lane -> (row r, slot lane & 7), which holds
-  // piece (lane & 7) ^ (r & 7)
-  const bf16_t* const wbase = shared ? a.W2 + g * a.w2g : a.W + g * a.wg;
-  const int64_t wld = shared ? a.w2ld : K;
-  const int upoff = shared ? a.w2up : a.N;
-  const bf16_t* src[4];
-  int dst[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r = 16 * wv + 8 * (j & 1) + (lane >> 3);
-    const int pc = (lane & 7) ^ (r & 7);
-    if (j >= 2) {
-      const int slot = t0 + (r < count ? r : 0);  // rows past the tile: the tile's first row
-      const int row = a.slot_row && !shared ? a.slot_row[slot] / a.slot_div : slot;
-      src[j] = a.X + (shared ? 0 : g * a.xg) + (int64_t)row * a.xs + pc * 8;
-    } else if (SWIGLU) {
-      src[j] = wbase + (f0 + (r >> 5) * 16 + ((r >> 4) & 1) * upoff + (r & 15)) * wld + pc * 8;
-    } else {
-      src[j] = wbase + (f0 + r) * wld + pc * 8;
-    }
-    dst[j] = (j >= 2 ? 8192 : 0) + (16 * wv + 8 * (j & 1)) * 128;
-  }
-  auto issue = [&](int chunk, int buf) {
-    const int cc = min(chunk, nch - 1);  // past the last chunk: repeat it (never multiplied)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      __builtin_amdgcn_global_load_lds(src[j] + cc * 64,
-                                       (__attribute__((address_space(3))) void*)(lds + buf * 16384 + dst[j]), 16, 0, 0);
-  };
-  floatx4_t acc[2][2];
-#pragma unroll
-  for (int x = 0; x < 2; ++x)
-#pragma unroll
-    for (int y = 0; y < 2; ++y) acc[x][y] = floatx4_t{0.f, 0.f, 0.f, 0.f};
-  const int wa = (wv & 1) * 32, wt = (wv >> 1) * 32;  // this wave's 32 features x 32 tokens
-#pragma unroll
-  for (int s = 0; s + 1 < kDmaStages; ++s) issue(s, s);
-  for (int c0 = 0; c0 < nch; c0 += kDmaStages) {
-#pragma unroll
-    for (int i = 0; i < kDmaStages; ++i) {
-      const int c = c0 + i;
-      if (c >= nch) break;
-      // this wave's loads of chunk c have landed (the 4 of each newer chunk may not), then
-      // every wave's: chunk c is complete in LDS and chunk c - 1's stage is free
-      __builtin_amdgcn_s_waitcnt(vmcnt_only((kDmaStages - 2) * 4));
-      asm volatile("" ::: "memory");
-      __builtin_amdgcn_s_barrier();
-      asm volatile("" ::: "memory");
-      issue(c + kDmaStages - 1, (i + kDmaStages - 1) % kDmaStages);
-      const uint8_t* st = lds + i * 16384;
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        bf16x8_t af[2], bfr[2];
-#pragma unroll
-        for (int x = 0; x < 2; ++x) {
-          const int r = wa + 16 * x + li, t = wt + 16 * x + li, pc = 4 * s + kg;
-          af[x] = *reinterpret_cast<const bf16x8_t*>(st + r * 128 + ((pc ^ (r & 7)) * 16));
-          bfr[x] = *reinterpret_cast<const bf16x8_t*>(st + 8192 + t * 128 + ((pc ^ (t & 7)) * 16));
-        }
-#pragma unroll
-        for (int x = 0; x < 2; ++x)
-#pragma unroll
-          for (int y = 0; y < 2; ++y) acc[x][y] = mfma16x16x32(af[x], bfr[y], acc[x][y]);
-      }
-    }
-  }
-  // the repeats past the last chunk must land before the workgroup's LDS is released
-  __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
-  if (SWIGLU) {
-#pragma unroll
-    for (int y = 0; y < 2; ++y) {
-      if (wt + 16 * y + li >= count) continue;
-      float v[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = swiglu_bf(acc[0][y][e], acc[1][y][e]);
-      if (shared) {
-        uint2 o;
-        o.x = pack2(v[0], v[1]);
-        o.y = pack2(v[2], v[3]);
-        *reinterpret_cast<uint2*>(a.Y2 + (int64_t)(t0 + wt + 16 * y + li) * a.y2s + g * a.y2g + f0 + (wa >> 1) +
-                                  4 * kg) = o;
+  for (int item = blockIdx.x;; item += gridDim.x) {
+    int fb, g = 0, t0, count;
+    bool shared = false;
+    if (a.tiles) {
+      // grouped: items tile * nfb + fb over the shared halves' tiles, then the table's; the
+      // table's live tiles come first, so the first dead one ends the workgroup's loop
+      if (item >= sh.items) break;
+      const int tile = item / sh.nfb, ns = a.W2 ? 2 * a.s_tiles : 0;
+      fb = item % sh.nfb;
+      if (tile < ns) {  // a shared-expert half's tile of tokens
+        shared = true;
+        g = tile / a.s_tiles;
+        t0 = (tile % a.s_tiles) * 64;
+        count = min(64, a.rows - t0);
       } else {
-        gemm_store4(a, g, t0 + wt + 16 * y + li, f0 + (wa >> 1) + 4 * kg, v);
+        if (tile - ns >= a.ntiles[0]) break;
+        const int4 tt = reinterpret_cast<const int4*>(a.tiles)[tile - ns];
+        g = tt.x;
+        t0 = tt.y;
+        count = tt.z;
+      }
+    } else {
+      if (item != (int)blockIdx.x) break;  // dense: one item per workgroup
+      const int per = sh.nwg / 8;
+      const int w = (blockIdx.x % 8) * per + blockIdx.x / 8;
+      if (w >= sh.nfb * sh.tiles) break;
+      const int tile = w % sh.tiles;
+      fb = w / sh.tiles;
+      t0 = tile * 64;
+      count = min(64, a.rows - t0);
+    }
+    const int f0 = fb * FPW;
+    const int K = a.K, nch = K / 64;
+    // this wave's 4 ring loads per chunk: weight rows 16wv .. 16wv+15 (j = 0, 1) and token rows
+    // 16wv .. 16wv+15 (j = 2, 3), 8 rows per load; lane -> (row r, slot lane & 7), which holds
+    // piece (lane & 7) ^ (r & 7)
+    const bf16_t* const wbase = shared ? a.W2 + g * a.w2g : a.W + g * a.wg;
+    const int64_t wld = shared ? a.w2ld : K;
+    const int upoff = shared ? a.w2up : a.N;
+    const bf16_t* src[4];
+    int dst[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = 16 * wv + 8 * (j & 1) + (lane >> 3);
+      const int pc = (lane & 7) ^ (r & 7);
+      if (j >= 2) {
+        const int slot = t0 + (r < count ? r : 0);  // rows past the tile: the tile's first row
+        if (shared) {
+          src[j] = a.X2 + g * a.x2g + (int64_t)slot * a.x2s + pc * 8;
+        } else {
+          const int row = a.slot_row ? a.slot_row[slot] / a.slot_div : slot;
+          src[j] = a.X + g * a.xg + (int64_t)row * a.xs + pc * 8;
+        }
+      } else if (SWIGLU) {
+        src[j] = wbase + (f0 + (r >> 5) * 16 + ((r >> 4) & 1) * upoff + (r & 15)) * wld + pc * 8;
+      } else {
+        src[j] = wbase + (f0 + r) * wld + pc * 8;
+      }
+      dst[j] = (j >= 2 ? 8192 : 0) + (16 * wv + 8 * (j & 1)) * 128;
+    }
+    auto issue = [&](int chunk, int buf) {
+      const int cc = min(chunk, nch - 1);  // past the last chunk: repeat it (never multiplied)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        __builtin_amdgcn_global_load_lds(src[j] + cc * 64,
+                                         (__attribute__((address_space(3))) void*)(lds + buf * 16384 + dst[j]), 16, 0, 0);
+    };
+    floatx4_t acc[2][2];
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int y = 0; y < 2; ++y) acc[x][y] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+    const int wa = (wv & 1) * 32, wt = (wv >> 1) * 32;  // this wave's 32 features x 32 tokens
+#pragma unroll
+    for (int s = 0; s + 1 < kDmaStages; ++s) issue(s, s);
+    for (int c0 = 0; c0 < nch; c0 += kDmaStages) {
+#pragma unroll
+      for (int i = 0; i < kDmaStages; ++i) {
+        const int c = c0 + i;
+        if (c >= nch) break;
+        // this wave's loads of chunk c have landed (the 4 of each newer chunk may not), then
+        // every wave's: chunk c is complete in LDS and chunk c - 1's stage is free
+        __builtin_amdgcn_s_waitcnt(vmcnt_only((kDmaStages - 2) * 4));
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        issue(c + kDmaStages - 1, (i + kDmaStages - 1) % kDmaStages);
+        const uint8_t* st = lds + i * 16384;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          bf16x8_t af[2], bfr[2];
+#pragma unroll
+          for (int x = 0; x < 2; ++x) {
+            const int r = wa + 16 * x + li, t = wt + 16 * x + li, pc = 4 * s + kg;
+            af[x] = *reinterpret_cast<const bf16x8_t*>(st + r * 128 + ((pc ^ (r & 7)) * 16));
+            bfr[x] = *reinterpret_cast<const bf16x8_t*>(st + 8192 + t * 128 + ((pc ^ (t & 7)) * 16));
+          }
+#pragma unroll
+          for (int x = 0; x < 2; ++x)
+#pragma unroll
+            for (int y = 0; y < 2; ++y) acc[x][y] = mfma16x16x32(af[x], bfr[y], acc[x][y]);
+        }
       }
     }
-    return;
-  }
+    // the repeats past the last chunk must land before the workgroup's LDS is released
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+    if (SWIGLU) {
 #pragma unroll
-  for (int x = 0; x < 2; ++x)
+      for (int y = 0; y < 2; ++y) {
+        if (wt + 16 * y + li >= count) continue;
+        float v[4];
 #pragma unroll
-    for (int y = 0; y < 2; ++y) {
-      if (wt + 16 * y + li >= count) continue;
-      float v[4];
+        for (int e = 0; e < 4; ++e) v[e] = swiglu_bf(acc[0][y][e], acc[1][y][e]);
+        if (shared) {
+          uint2 o;
+          o.x = pack2(v[0], v[1]);
+          o.y = pack2(v[2], v[3]);
+          *reinterpret_cast<uint2*>(reinterpret_cast<bf16_t*>(a.Y2) + g * a.y2g +
+                                    (int64_t)(t0 + wt + 16 * y + li) * a.y2s + f0 + (wa >> 1) + 4 * kg) = o;
+        } else {
+          gemm_store4(a, g, t0 + wt + 16 * y + li, f0 + (wa >> 1) + 4 * kg, v);
+        }
+      }
+    } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = rbf(acc[x][y][e]);
-      gemm_store4(a, g, t0 + wt + 16 * y + li, f0 + wa + 16 * x + 4 * kg, v);
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int y = 0; y < 2; ++y) {
+          if (wt + 16 * y + li >= count) continue;
+          if (shared) {  // fp32 partial of one half (the halves are summed by the consumer)
+            float* yp = reinterpret_cast<float*>(a.Y2) + g * a.y2g + (int64_t)(t0 + wt + 16 * y + li) * a.y2s + f0 +
+                        wa + 16 * x + 4 * kg;
+            *reinterpret_cast<float4*>(yp) = make_float4(acc[x][y][0], acc[x][y][1], acc[x][y][2], acc[x][y][3]);
+            continue;
+          }
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = rbf(acc[x][y][e]);
+          gemm_store4(a, g, t0 + wt + 16 * y + li, f0 + wa + 16 * x + 4 * kg, v);
+        }
     }
+    __syncthreads();  // every wave is done with the ring before the next item refills it
+  }
 }
 
 // grouped: max_tiles entries of a 64-token tile table; dense: a.rows tokens
@@ -536,7 +557,9 @@ static void launch_dma(const GemmArgs& a, bool swiglu, hipStream_t st, int max_t
   DmaShape sh;
   sh.nfb = a.N / (swiglu ? 32 : 64);
   sh.tiles = a.tiles ? max_tiles : (a.rows + 63) / 64;
-  sh.nwg = a.tiles ? sh.nfb * (sh.tiles + (a.W2 ? 2 * a.s_tiles : 0)) : (sh.nfb * sh.tiles + 7) / 8 * 8;
+  // grouped: at most two resident workgroups per CU, looping over the items
+  sh.items = a.tiles ? sh.nfb * (sh.tiles + (a.W2 ? 2 * a.s_tiles : 0)) : 0;
+  sh.nwg = a.tiles ? (sh.items < kDmaGroupedWgs ? sh.items : kDmaGroupedWgs) : (sh.nfb * sh.tiles + 7) / 8 * 8;
   if (swiglu) hipLaunchKernelGGL(gemm_dma_kernel<true>, dim3(sh.nwg), dim3(256), kDmaStages * 16384, st, a, sh);
   else hipLaunchKernelGGL(gemm_dma_kernel<false>, dim3(sh.nwg), dim3(256), kDmaStages * 16384, st, a, sh);
 }
@@ -943,16 +966,59 @@ extern "C" int dsv2_moe_grouped_gateup_shared(const void* xn, int rows, const in
   a.K = 2048;
   a.Y = hsorted;
   a.ys = inter;
+  a.X2 = (const bf16_t*)xn;
+  a.x2s = 2048;
   a.W2 = (const bf16_t*)sh_gate_up;
   a.w2g = (int64_t)inter * 2048;
   a.w2ld = 2048;
   a.w2up = 2 * inter;
   a.s_tiles = (rows + 63) / 64;
-  a.Y2 = (bf16_t*)shared_out;
+  a.Y2 = shared_out;
   a.y2s = 2 * inter;
   a.y2g = inter;
   launch_dma(a, true, (hipStream_t)stream, max_tiles);
   return dsv2_launch_status("moe_grouped_gateup_shared");
+}
+
+extern "C" int dsv2_moe_grouped_down_shared(const void* hsorted, int rows, const int32_t* tiles,
+                                            const int32_t* num_tiles, int max_tiles, const void* w_down,
+                                            const void* shared_mid, const void* sh_down, int inter, void* ysorted,
+                                            float* shared_parts, void* stream) {
+  DSV2_REQUIRE(hsorted && tiles && num_tiles && w_down && shared_mid && sh_down && ysorted && shared_parts,
+               DSV2_E_NULL, "moe_grouped_down_shared: null pointer");
+  DSV2_REQUIRE(rows >= 0 && max_tiles >= 0 && inter > 0 && inter % 64 == 0 &&
+                   ((int64_t)max_tiles + 2 * ((rows + 63) / 64)) * 32 <= 0x7fffffff,
+               DSV2_E_SHAPE, "moe_grouped_down_shared: bad shape (inter %% 64)");
+  DSV2_REQUIRE(dsv2_aligned16(hsorted) && dsv2_aligned16(w_down) && dsv2_aligned16(shared_mid) &&
+                   dsv2_aligned16(sh_down) && dsv2_aligned16(tiles) && dsv2_aligned16(ysorted) &&
+                   dsv2_aligned16(shared_parts),
+               DSV2_E_ALIGN, "moe_grouped_down_shared: alignment");
+  if (rows == 0) return DSV2_OK;
+  GemmArgs a{};
+  a.X = (const bf16_t*)hsorted;
+  a.xs = inter;
+  a.slot_div = 1;
+  a.tiles = tiles;
+  a.ntiles = num_tiles;
+  a.rows = rows;
+  a.W = (const bf16_t*)w_down;
+  a.wg = (int64_t)2048 * inter;
+  a.N = 2048;
+  a.K = inter;
+  a.Y = ysorted;
+  a.ys = 2048;
+  a.X2 = (const bf16_t*)shared_mid;
+  a.x2s = 2 * inter;
+  a.x2g = inter;
+  a.W2 = (const bf16_t*)sh_down;
+  a.w2g = inter;
+  a.w2ld = 2 * inter;
+  a.s_tiles = (rows + 63) / 64;
+  a.Y2 = shared_parts;
+  a.y2s = 2048;
+  a.y2g = (int64_t)rows * 2048;
+  launch_dma(a, false, (hipStream_t)stream, max_tiles);
+  return dsv2_launch_status("moe_grouped_down_shared");
 }
 
 extern "C" int dsv2_moe_grouped_down(const void* hsorted, const int32_t* tiles, const int32_t* num_tiles,

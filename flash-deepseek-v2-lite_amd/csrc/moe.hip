@@ -590,6 +590,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const bf16_t* __restri
                                                           const int32_t* __restrict__ route_pos,
                                                           const float* __restrict__ wts,
                                                           const bf16_t* __restrict__ shared,
+                                                          const float* __restrict__ shared_parts,
                                                           const bf16_t* __restrict__ res, bf16_t* __restrict__ out,
                                                           const bf16_t* __restrict__ nw, float eps,
                                                           bf16_t* __restrict__ xn) {
@@ -615,6 +616,14 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const bf16_t* __restri
     unpack8(ldg16(shared + (int64_t)b * kH + tid * 8), f);
 #pragma unroll
     for (int i = 0; i < 8; ++i) y[i] = rbf(y[i] + f[i]);
+  } else if (shared_parts) {  // shared = bf16(half 0 + half 1), the fp32 partials of its down GEMM
+    const float4* p0 = reinterpret_cast<const float4*>(shared_parts + (int64_t)b * kH + tid * 8);
+    const float4* p1 = reinterpret_cast<const float4*>(shared_parts + ((int64_t)gridDim.x + b) * kH + tid * 8);
+    const float4 a0 = p0[0], a1 = p0[1], b0 = p1[0], b1 = p1[1];
+    const float sh[8] = {a0.x + b0.x, a0.y + b0.y, a0.z + b0.z, a0.w + b0.w,
+                         a1.x + b1.x, a1.y + b1.y, a1.z + b1.z, a1.w + b1.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = rbf(y[i] + rbf(sh[i]));
   }
   if (res) {
     float f[8];
@@ -648,7 +657,23 @@ extern "C" int dsv2_moe_combine(const void* ysorted, const int32_t* route_pos, c
                DSV2_E_ALIGN, "moe_combine: alignment");
   if (rows == 0) return DSV2_OK;
   hipLaunchKernelGGL(moe_combine_kernel, dim3(rows), dim3(256), 0, (hipStream_t)stream, (const bf16_t*)ysorted,
-                     route_pos, weights, (const bf16_t*)shared, (const bf16_t*)residual, (bf16_t*)out,
+                     route_pos, weights, (const bf16_t*)shared, nullptr, (const bf16_t*)residual, (bf16_t*)out,
                      (const bf16_t*)next_norm_w, eps, (bf16_t*)xn_out);
   return dsv2_launch_status("moe_combine");
+}
+
+extern "C" int dsv2_moe_combine_parts(const void* ysorted, const int32_t* route_pos, const float* weights, int rows,
+                                      const float* shared_parts, const void* residual, void* out,
+                                      const void* next_norm_w, float eps, void* xn_out, void* stream) {
+  DSV2_REQUIRE(ysorted && route_pos && weights && shared_parts && out && (!next_norm_w || xn_out), DSV2_E_NULL,
+               "moe_combine_parts: null pointer");
+  DSV2_REQUIRE(rows >= 0, DSV2_E_SHAPE, "moe_combine_parts: bad rows");
+  DSV2_REQUIRE(dsv2_aligned16(ysorted) && dsv2_aligned16(out) && dsv2_aligned16(shared_parts) &&
+                   (!residual || dsv2_aligned16(residual)) && (!xn_out || dsv2_aligned16(xn_out)),
+               DSV2_E_ALIGN, "moe_combine_parts: alignment");
+  if (rows == 0) return DSV2_OK;
+  hipLaunchKernelGGL(moe_combine_kernel, dim3(rows), dim3(256), 0, (hipStream_t)stream, (const bf16_t*)ysorted,
+                     route_pos, weights, nullptr, shared_parts, (const bf16_t*)residual, (bf16_t*)out,
+                     (const bf16_t*)next_norm_w, eps, (bf16_t*)xn_out);
+  return dsv2_launch_status("moe_combine_parts");
 }

@@ -101,6 +101,7 @@ class RowBuffers:
             self.ys = e(R, H)
             self.shmid = e(rows, cfg.shared_inter)
             self.shout = e(rows, H)
+            self.shparts = e(2, rows, H, dt=torch.float32)  # shared down halves (64-token tiles)
 
 
     def set_tile_tokens(self, tile_tokens: int) -> None:
@@ -214,21 +215,24 @@ class DecodeEngine:
             call("dsv2_moe_bucket", ptr(b.ids32), R, b.tile_tokens, ptr(b.sorted), ptr(b.route_pos), ptr(b.tiles),
                  ptr(b.ntiles), st)
             if b.tile_tokens == 64:
-                # 64-token tiles: the shared experts' gate_up rides in the grouped launch
+                # 64-token tiles: the shared experts' two halves ride in the grouped launches
                 call("dsv2_moe_grouped_gateup_shared", ptr(b.xn), R, ptr(b.sorted), ptr(b.tiles), ptr(b.ntiles),
                      b.max_tiles, ptr(L.w_gu), ptr(L.sh_gu), c.moe_inter, ptr(b.hs), ptr(b.shmid), st)
+                call("dsv2_moe_grouped_down_shared", ptr(b.hs), R, ptr(b.tiles), ptr(b.ntiles), b.max_tiles,
+                     ptr(L.w_down), ptr(b.shmid), ptr(L.sh_down), c.moe_inter, ptr(b.ys), ptr(b.shparts), st)
+                call("dsv2_moe_combine_parts", ptr(b.ys), ptr(b.route_pos), ptr(b.wts), R, ptr(b.shparts), ptr(b.h),
+                     ptr(b.h), ptr(next_norm), c.eps, ptr(b.xn), st)
             else:
                 call("dsv2_moe_grouped_gateup", ptr(b.xn), ptr(b.sorted), ptr(b.tiles), ptr(b.ntiles), b.max_tiles,
                      b.tile_tokens, ptr(L.w_gu), c.moe_inter, ptr(b.hs), st)
-            call("dsv2_moe_grouped_down", ptr(b.hs), ptr(b.tiles), ptr(b.ntiles), b.max_tiles, b.tile_tokens,
-                 ptr(L.w_down), c.moe_inter, ptr(b.ys), st)
-            if b.tile_tokens != 64:
+                call("dsv2_moe_grouped_down", ptr(b.hs), ptr(b.tiles), ptr(b.ntiles), b.max_tiles, b.tile_tokens,
+                     ptr(L.w_down), c.moe_inter, ptr(b.ys), st)
                 call("dsv2_gemm_bf16", ptr(b.xn), H, 0, R, H, ptr(L.sh_gu), 0, c.shared_inter, 1, None, 0,
                      ptr(b.shmid), c.shared_inter, 0, LINEAR_SWIGLU, st)
-            call("dsv2_gemm_bf16", ptr(b.shmid), c.shared_inter, 0, R, c.shared_inter, ptr(L.sh_down), 0, H, 1,
-                 None, 0, ptr(b.shout), H, 0, 0, st)
-            call("dsv2_moe_combine", ptr(b.ys), ptr(b.route_pos), ptr(b.wts), R, ptr(b.shout), ptr(b.h), ptr(b.h),
-                 ptr(next_norm), c.eps, ptr(b.xn), st)
+                call("dsv2_gemm_bf16", ptr(b.shmid), c.shared_inter, 0, R, c.shared_inter, ptr(L.sh_down), 0, H, 1,
+                     None, 0, ptr(b.shout), H, 0, 0, st)
+                call("dsv2_moe_combine", ptr(b.ys), ptr(b.route_pos), ptr(b.wts), R, ptr(b.shout), ptr(b.h),
+                     ptr(b.h), ptr(next_norm), c.eps, ptr(b.xn), st)
         else:
             call("dsv2_rmsnorm_bf16", ptr(b.h), H, ptr(L.ln_post), ptr(b.xn), H, R, H, c.eps, st)
             call("dsv2_gemm_bf16", ptr(b.xn), H, 0, R, H, ptr(L.w_gu), 0, c.dense_inter, 1, None, 0, ptr(b.mid),

@@ -55,6 +55,8 @@ _SIGS = {
     "dsv2_moe_grouped_gateup_shared": ([_p, _i32, _p, _p, _p, _i32, _p, _p, _i32, _p, _p, _p], _i32),
     "dsv2_moe_grouped_down": ([_p, _p, _p, _i32, _i32, _p, _i32, _p, _p], _i32),
     "dsv2_moe_combine": ([_p, _p, _p, _i32, _p, _p, _p, _p, _f32, _p, _p], _i32),
+    "dsv2_moe_grouped_down_shared": ([_p, _i32, _p, _p, _i32, _p, _p, _p, _i32, _p, _p, _p], _i32),
+    "dsv2_moe_combine_parts": ([_p, _p, _p, _i32, _p, _p, _p, _p, _f32, _p, _p], _i32),
 }
 
 EXPORTS = tuple(_SIGS)

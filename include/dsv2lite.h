@@ -246,6 +246,16 @@ int dsv2_moe_grouped_gateup_shared(const void* xn, int rows, const int32_t* sort
 int dsv2_moe_grouped_down(const void* hsorted, const int32_t* tiles, const int32_t* num_tiles, int max_tiles,
                           int tile_tokens, const void* w_down, int inter, void* ysorted, void* stream);
 
+/* dsv2_moe_grouped_down with 64-token tiles, plus the two shared-expert halves in the same
+ * launch: shared_parts[h, t, :] = fp32 shared_mid[t, h*inter : (h+1)*inter] . sh_down[:, same]^T
+ * for t < rows, h = 0, 1 (shared_mid [rows, 2*inter] from dsv2_moe_grouped_gateup_shared,
+ * sh_down [2048, 2*inter]); dsv2_moe_combine_parts adds bf16(half 0 + half 1), the shared
+ * MLP's down_proj output (src/run.py:351).  Replaces _grouped_down_partial_kernel
+ * (moe_batch.py:238-307) and the shared experts' down projection. */
+int dsv2_moe_grouped_down_shared(const void* hsorted, int rows, const int32_t* tiles, const int32_t* num_tiles,
+                                 int max_tiles, const void* w_down, const void* shared_mid, const void* sh_down,
+                                 int inter, void* ysorted, float* shared_parts, void* stream);
+
 /* Combine: routed = bf16(sum_s w[r,s] ysorted[route_pos[r*6+s]]) (fp32, slot order);
  * y = shared ? bf16(routed + shared[r]) : routed;  out[r] = residual ? bf16(residual[r] + y) : y.
  * If next_norm_w != NULL also xn_out[r] = RMSNorm(out[r]; next_norm_w).
@@ -254,6 +264,12 @@ int dsv2_moe_grouped_down(const void* hsorted, const int32_t* tiles, const int32
 int dsv2_moe_combine(const void* ysorted, const int32_t* route_pos, const float* weights, int rows,
                      const void* shared, const void* residual, void* out, const void* next_norm_w, float eps,
                      void* xn_out, void* stream);
+
+/* dsv2_moe_combine with the shared output given as the two fp32 halves of
+ * dsv2_moe_grouped_down_shared (shared_parts [2, rows, 2048]): shared = bf16(half 0 + half 1). */
+int dsv2_moe_combine_parts(const void* ysorted, const int32_t* route_pos, const float* weights, int rows,
+                           const float* shared_parts, const void* residual, void* out, const void* next_norm_w,
+                           float eps, void* xn_out, void* stream);
 
 #ifdef __cplusplus
 }

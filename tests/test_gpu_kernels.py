@@ -450,6 +450,28 @@ def test_moe_grouped_gateup_with_shared(rows, replicated):
     call("dsv2_gemm_bf16", xn.data_ptr(), 2048, 0, rows, 2048, sgu.data_ptr(), 0, 2816, 1, None, 0, dense.data_ptr(),
          2816, 0, LINEAR_SWIGLU, st())
     assert rel_err(sh.float(), dense.float()) < 1e-2
+    # down: routed rows equal dsv2_moe_grouped_down's; the shared halves' fp32 partials sum to
+    # the shared down projection; the combine of both paths agrees with the oracle
+    ys_ref = torch.empty(R, 2048, dtype=BF, device=DEV)
+    call("dsv2_moe_grouped_down", hs.data_ptr(), tiles.data_ptr(), nt.data_ptr(), max_tiles, 64, dn.data_ptr(), 1408,
+         ys_ref.data_ptr(), st())
+    ys = torch.empty_like(ys_ref)
+    parts = torch.empty(2, rows, 2048, dtype=torch.float32, device=DEV)
+    call("dsv2_moe_grouped_down_shared", hs.data_ptr(), rows, tiles.data_ptr(), nt.data_ptr(), max_tiles,
+         dn.data_ptr(), sh.data_ptr(), sdn.data_ptr(), 1408, ys.data_ptr(), parts.data_ptr(), st())
+    assert torch.equal(ys, ys_ref)
+    sh_ref = sh.float() @ sdn.float().t()
+    assert rel_err(parts[0] + parts[1], sh_ref) < 1e-3
+    assert rel_err(parts[1], sh.float()[:, 1408:] @ sdn.float()[:, 1408:].t()) < 1e-3
+    w = (torch.rand(rows, 6, generator=g) * 0.3).to(DEV)
+    res = rnd(rows, 2048, seed=73)
+    out = torch.empty(rows, 2048, dtype=BF, device=DEV)
+    call("dsv2_moe_combine_parts", ys.data_ptr(), rpos.data_ptr(), w.data_ptr(), rows, parts.data_ptr(),
+         res.data_ptr(), out.data_ptr(), None, 0.0, None, st())
+    c = lambda t: t.float().cpu()  # noqa: E731
+    sel = list(range(0, rows, max(1, rows // 12)))
+    routed, shared = _oracle_moe_parts(c(xn)[sel], ids[sel], c(w)[sel], c(gu), c(dn), c(sgu), c(sdn))
+    assert rel_err(c(out)[sel], rb(c(res)[sel] + rb(routed + shared))) < 1e-2
 
 
 def _mla_reference(q, cache_rows, lens, scale):
