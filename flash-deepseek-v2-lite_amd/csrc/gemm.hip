@@ -392,44 +392,47 @@ constexpr int kDmaGroupedWgs = 512;  // 256 CUs x 2 (64 KB of LDS each)
 constexpr int vmcnt_only(int n) { return (n & 0xf) | (0x7 << 4) | (0xf << 8) | (((n >> 4) & 3) << 14); }
 
 struct DmaShape {
-  int tiles, nwg, nfb, items;
+  int tiles, nwg, nfb;
 };
 
 // SWIGLU: the 64 weight rows of a workgroup are, per 16 features, 16 gate rows then the 16
 // matching up rows (32 features per workgroup); a wave's two row blocks are then one
 // feature block's gate and up tiles, combined in its epilogue.
-// Grouped (a.tiles, 64-token expert tiles): a grid of at most kDmaGroupedWgs workgroups
-// loops over the items tile * nfb + fb (consecutive items go round-robin over the XCDs), so
-// the table's dead tiles cost no workgroup launches; token rows are gathered through
-// slot_row and the tile's expert selects the weights.
+// Grouped (a.tiles, 64-token expert tiles): a grid of kDmaGroupedWgs workgroups loops over
+// the live (tile, feature block) items only, so the table's dead tiles cost no workgroup
+// launches; token rows are gathered through slot_row and the tile's expert selects the
+// weights.
 template <bool SWIGLU>
 __global__ __launch_bounds__(256) void gemm_dma_kernel(const GemmArgs a, const DmaShape sh) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // kDmaStages * 16 KB
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, li = lane & 15, kg = lane >> 4;
   constexpr int FPW = SWIGLU ? 32 : 64;  // output features per workgroup
-  for (int item = blockIdx.x;; item += gridDim.x) {
+  // grouped: items j = tile * nfb + fb over the live tiles (the shared halves' tiles, then the
+  // table's), consecutive items round-robin over the XCDs (keeping all token tiles of a
+  // feature block on one XCD measured slower: fewer feature blocks than XCD slots balance)
+  const int ns = a.W2 ? 2 * a.s_tiles : 0;
+  const int live = a.tiles ? ns + min(a.ntiles[0], sh.tiles) : 0;  // sh.tiles: the table's size
+  for (int it = 0;; ++it) {
     int fb, g = 0, t0, count;
     bool shared = false;
     if (a.tiles) {
-      // grouped: items tile * nfb + fb over the shared halves' tiles, then the table's; the
-      // table's live tiles come first, so the first dead one ends the workgroup's loop
-      if (item >= sh.items) break;
-      const int tile = item / sh.nfb, ns = a.W2 ? 2 * a.s_tiles : 0;
-      fb = item % sh.nfb;
+      const int j = blockIdx.x + it * gridDim.x;
+      if (j >= live * sh.nfb) break;
+      const int tile = j / sh.nfb;
+      fb = j % sh.nfb;
       if (tile < ns) {  // a shared-expert half's tile of tokens
         shared = true;
         g = tile / a.s_tiles;
         t0 = (tile % a.s_tiles) * 64;
         count = min(64, a.rows - t0);
       } else {
-        if (tile - ns >= a.ntiles[0]) break;
         const int4 tt = reinterpret_cast<const int4*>(a.tiles)[tile - ns];
         g = tt.x;
         t0 = tt.y;
         count = tt.z;
       }
     } else {
-      if (item != (int)blockIdx.x) break;  // dense: one item per workgroup
+      if (it > 0) break;  // dense: one item per workgroup
       const int per = sh.nwg / 8;
       const int w = (blockIdx.x % 8) * per + blockIdx.x / 8;
       if (w >= sh.nfb * sh.tiles) break;
@@ -557,9 +560,8 @@ static void launch_dma(const GemmArgs& a, bool swiglu, hipStream_t st, int max_t
   DmaShape sh;
   sh.nfb = a.N / (swiglu ? 32 : 64);
   sh.tiles = a.tiles ? max_tiles : (a.rows + 63) / 64;
-  // grouped: at most two resident workgroups per CU, looping over the items
-  sh.items = a.tiles ? sh.nfb * (sh.tiles + (a.W2 ? 2 * a.s_tiles : 0)) : 0;
-  sh.nwg = a.tiles ? (sh.items < kDmaGroupedWgs ? sh.items : kDmaGroupedWgs) : (sh.nfb * sh.tiles + 7) / 8 * 8;
+  // grouped: two resident workgroups per CU, looping over the live items
+  sh.nwg = a.tiles ? kDmaGroupedWgs : (sh.nfb * sh.tiles + 7) / 8 * 8;
   if (swiglu) hipLaunchKernelGGL(gemm_dma_kernel<true>, dim3(sh.nwg), dim3(256), kDmaStages * 16384, st, a, sh);
   else hipLaunchKernelGGL(gemm_dma_kernel<false>, dim3(sh.nwg), dim3(256), kDmaStages * 16384, st, a, sh);
 }
