@@ -104,7 +104,7 @@ def time_dominant_kernel(eng, family: str, reps: int = 4) -> dict:
 
         def launch(L):
             call("dsv2_moe_grouped_gateup_shared", ptr(b.xn), B, ptr(b.sorted), ptr(b.tiles), ptr(b.ntiles),
-                 b.max_tiles, ptr(L.w_gu), ptr(L.sh_gu), c.moe_inter, ptr(b.hs), ptr(b.shmid), stream_ptr())
+                 b.max_tiles, 64, ptr(L.w_gu), ptr(L.sh_gu), c.moe_inter, ptr(b.hs), ptr(b.shmid), stream_ptr())
     else:
         sym = {16: "gemm_xlds_kernel<1, true, 4, true, 2, 2, 1, false>",
                32: "gemm_xlds_kernel<2, true, 4, true, 2, 4, 2, true>"}[b.tile_tokens]

@@ -186,12 +186,21 @@ __global__ __launch_bounds__(512) void gemm_xlds_kernel(const GemmArgs a) {
   const int rb = wv % NRB, kq = wv / NRB;
   const int li = lane & 15, kg = lane >> 4;
   int g, start, count;
+  bool shared = false;  // a tile of one of the shared-expert halves (a.W2), grid rows 0 .. ns-1
   if (a.tiles) {
-    if ((int)blockIdx.y >= a.ntiles[0]) return;
-    const int4 t = reinterpret_cast<const int4*>(a.tiles)[blockIdx.y];
-    g = t.x;
-    start = t.y;
-    count = t.z;
+    const int ns = a.W2 ? 2 * a.s_tiles : 0;
+    if ((int)blockIdx.y < ns) {
+      shared = true;
+      g = blockIdx.y / a.s_tiles;
+      start = (blockIdx.y % a.s_tiles) * TOK;
+      count = min(TOK, a.rows - start);
+    } else {
+      if ((int)blockIdx.y - ns >= a.ntiles[0]) return;
+      const int4 t = reinterpret_cast<const int4*>(a.tiles)[blockIdx.y - ns];
+      g = t.x;
+      start = t.y;
+      count = t.z;
+    }
   } else {
     g = blockIdx.y / a.tiles_per_group;
     start = (blockIdx.y % a.tiles_per_group) * TOK;
@@ -202,11 +211,14 @@ __global__ __launch_bounds__(512) void gemm_xlds_kernel(const GemmArgs a) {
   const int SP = ((S + NKQ - 1) / NKQ + CS * DEPTH - 1) / (CS * DEPTH) * (CS * DEPTH);
   const int nch = SP / CS;
   const int f0 = blockIdx.x * 16 * NRB + rb * 16;
+  const bf16_t* const wbase = shared ? a.W2 + g * a.w2g : a.W + g * a.wg;
+  const int64_t wld = shared ? a.w2ld : K;  // weight row stride
+  const int upoff = shared ? a.w2up : a.N;  // SwiGLU: gate row -> up row
   const bf16_t* wrow[R];
 #pragma unroll
   for (int r = 0; r < R; ++r)
-    wrow[r] = AST ? a.W + g * a.wg + (int64_t)(f0 + r * a.N + (lane >> 4)) * K + (lane & 3) * 8
-                  : a.W + g * a.wg + (int64_t)(f0 + r * a.N + li) * K + kg * 8;
+    wrow[r] = AST ? wbase + (f0 + r * upoff + (lane >> 4)) * wld + (lane & 3) * 8
+                  : wbase + (f0 + r * upoff + li) * wld + kg * 8;
 
   // this thread's X units: fixed (range, token, 16-byte part) for every chunk
   const bf16_t* xsrc[UPT];
@@ -217,8 +229,12 @@ __global__ __launch_bounds__(512) void gemm_xlds_kernel(const GemmArgs a) {
     const int uk = u / (TOK * CS * 4), rem = u % (TOK * CS * 4);
     const int tok = rem / (CS * 4), part = rem % (CS * 4);
     const int tk = tok < count ? tok : 0;
-    const int row = a.slot_row ? a.slot_row[start + tk] / a.slot_div : start + tk;
-    xsrc[j] = a.X + g * a.xg + (int64_t)row * a.xs + (part & 3) * 8;
+    if (shared) {
+      xsrc[j] = a.X2 + g * a.x2g + (int64_t)(start + tk) * a.x2s + (part & 3) * 8;
+    } else {
+      const int row = a.slot_row ? a.slot_row[start + tk] / a.slot_div : start + tk;
+      xsrc[j] = a.X + g * a.xg + (int64_t)row * a.xs + (part & 3) * 8;
+    }
     xkq[j] = uk;
     xpart[j] = part;
     xdst[j] = (uk * TOK + tok) * XROW + (part >> 2) * 32 + (part & 3) * 8;
@@ -243,8 +259,8 @@ __global__ __launch_bounds__(512) void gemm_xlds_kernel(const GemmArgs a) {
   _Pragma("unroll") for (int si = 0; si < CS; ++si) {                                            \
     const int step_ = kq * SP + (c) * CS + (AST ? ((lane & 15) >> 2) : si);                      \
     _Pragma("unroll") for (int r = 0; r < R; ++r)                                                \
-      av[si][r] = NTA ? ldg16_nt(wrow[r] + (AST ? (int64_t)si * 4 * K : 0) + (int64_t)min(step_, S - 1) * 32) \
-                      : ldg16(wrow[r] + (AST ? (int64_t)si * 4 * K : 0) + (int64_t)min(step_, S - 1) * 32); \
+      av[si][r] = NTA ? ldg16_nt(wrow[r] + (AST ? si * 4 * wld : 0) + (int64_t)min(step_, S - 1) * 32) \
+                      : ldg16(wrow[r] + (AST ? si * 4 * wld : 0) + (int64_t)min(step_, S - 1) * 32); \
   }
 
   floatx4_t acc[R][TB];
@@ -334,6 +350,18 @@ __global__ __launch_bounds__(512) void gemm_xlds_kernel(const GemmArgs a) {
     float v[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) v[e] = SWIGLU ? swiglu_bf(acc[0][tb][e], acc[R - 1][tb][e]) : rbf(acc[0][tb][e]);
+    if (shared) {  // SwiGLU: bf16 row of the half's output; plain: the fp32 partial sum
+      if (SWIGLU) {
+        uint2 o;
+        o.x = pack2(v[0], v[1]);
+        o.y = pack2(v[2], v[3]);
+        *reinterpret_cast<uint2*>(reinterpret_cast<bf16_t*>(a.Y2) + g * a.y2g + (int64_t)slot * a.y2s + n) = o;
+      } else {
+        *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.Y2) + g * a.y2g + (int64_t)slot * a.y2s + n) =
+            make_float4(acc[0][tb][0], acc[0][tb][1], acc[0][tb][2], acc[0][tb][3]);
+      }
+      continue;
+    }
     if (a.res) {
       const uint2 r2 = *reinterpret_cast<const uint2*>(a.res + slot * a.rs + n);
       v[0] = rbf(__uint_as_float(r2.x << 16) + v[0]);
@@ -943,13 +971,14 @@ extern "C" int dsv2_moe_grouped_gateup(const void* xn, const int32_t* sorted_rou
 
 extern "C" int dsv2_moe_grouped_gateup_shared(const void* xn, int rows, const int32_t* sorted_routes,
                                               const int32_t* tiles, const int32_t* num_tiles, int max_tiles,
-                                              const void* w_gate_up, const void* sh_gate_up, int inter, void* hsorted,
-                                              void* shared_out, void* stream) {
+                                              int tile_tokens, const void* w_gate_up, const void* sh_gate_up,
+                                              int inter, void* hsorted, void* shared_out, void* stream) {
   DSV2_REQUIRE(xn && sorted_routes && tiles && num_tiles && w_gate_up && sh_gate_up && hsorted && shared_out,
                DSV2_E_NULL, "moe_grouped_gateup_shared: null pointer");
-  DSV2_REQUIRE(rows >= 0 && max_tiles >= 0 && inter > 0 && inter % 32 == 0 &&
-                   ((int64_t)max_tiles + 2 * ((rows + 63) / 64)) * (inter / 32) <= 0x7fffffff,
-               DSV2_E_SHAPE, "moe_grouped_gateup_shared: bad shape (inter %% 32)");
+  DSV2_REQUIRE(rows >= 0 && max_tiles >= 0 && max_tiles <= 65535 && inter > 0 && inter % 64 == 0 &&
+                   (tile_tokens == 16 || tile_tokens == 32 || tile_tokens == 64) &&
+                   (tile_tokens == 64 || (int64_t)max_tiles + 2 * ((rows + tile_tokens - 1) / tile_tokens) <= 65535),
+               DSV2_E_SHAPE, "moe_grouped_gateup_shared: bad shape (inter %% 64, tile_tokens in {16,32,64})");
   DSV2_REQUIRE(dsv2_aligned16(xn) && dsv2_aligned16(w_gate_up) && dsv2_aligned16(sh_gate_up) &&
                    dsv2_aligned16(tiles) && dsv2_aligned16(shared_out),
                DSV2_E_ALIGN, "moe_grouped_gateup_shared: alignment");
@@ -974,23 +1003,27 @@ extern "C" int dsv2_moe_grouped_gateup_shared(const void* xn, int rows, const in
   a.w2g = (int64_t)inter * 2048;
   a.w2ld = 2048;
   a.w2up = 2 * inter;
-  a.s_tiles = (rows + 63) / 64;
+  a.s_tiles = (rows + tile_tokens - 1) / tile_tokens;
   a.Y2 = shared_out;
   a.y2s = 2 * inter;
   a.y2g = inter;
-  launch_dma(a, true, (hipStream_t)stream, max_tiles);
-  return dsv2_launch_status("moe_grouped_gateup_shared");
+  if (tile_tokens == 64) {
+    launch_dma(a, true, (hipStream_t)stream, max_tiles);
+    return dsv2_launch_status("moe_grouped_gateup_shared");
+  }
+  return launch_gemm(a, tile_tb(tile_tokens), true, 2 * a.s_tiles + max_tiles, (hipStream_t)stream);
 }
 
 extern "C" int dsv2_moe_grouped_down_shared(const void* hsorted, int rows, const int32_t* tiles,
-                                            const int32_t* num_tiles, int max_tiles, const void* w_down,
-                                            const void* shared_mid, const void* sh_down, int inter, void* ysorted,
-                                            float* shared_parts, void* stream) {
+                                            const int32_t* num_tiles, int max_tiles, int tile_tokens,
+                                            const void* w_down, const void* shared_mid, const void* sh_down, int inter,
+                                            void* ysorted, float* shared_parts, void* stream) {
   DSV2_REQUIRE(hsorted && tiles && num_tiles && w_down && shared_mid && sh_down && ysorted && shared_parts,
                DSV2_E_NULL, "moe_grouped_down_shared: null pointer");
-  DSV2_REQUIRE(rows >= 0 && max_tiles >= 0 && inter > 0 && inter % 64 == 0 &&
-                   ((int64_t)max_tiles + 2 * ((rows + 63) / 64)) * 32 <= 0x7fffffff,
-               DSV2_E_SHAPE, "moe_grouped_down_shared: bad shape (inter %% 64)");
+  DSV2_REQUIRE(rows >= 0 && max_tiles >= 0 && max_tiles <= 65535 && inter > 0 && inter % 64 == 0 &&
+                   (tile_tokens == 16 || tile_tokens == 32 || tile_tokens == 64) &&
+                   (tile_tokens == 64 || (int64_t)max_tiles + 2 * ((rows + tile_tokens - 1) / tile_tokens) <= 65535),
+               DSV2_E_SHAPE, "moe_grouped_down_shared: bad shape (inter %% 64, tile_tokens in {16,32,64})");
   DSV2_REQUIRE(dsv2_aligned16(hsorted) && dsv2_aligned16(w_down) && dsv2_aligned16(shared_mid) &&
                    dsv2_aligned16(sh_down) && dsv2_aligned16(tiles) && dsv2_aligned16(ysorted) &&
                    dsv2_aligned16(shared_parts),
@@ -1015,12 +1048,15 @@ extern "C" int dsv2_moe_grouped_down_shared(const void* hsorted, int rows, const
   a.W2 = (const bf16_t*)sh_down;
   a.w2g = inter;
   a.w2ld = 2 * inter;
-  a.s_tiles = (rows + 63) / 64;
+  a.s_tiles = (rows + tile_tokens - 1) / tile_tokens;
   a.Y2 = shared_parts;
   a.y2s = 2048;
   a.y2g = (int64_t)rows * 2048;
-  launch_dma(a, false, (hipStream_t)stream, max_tiles);
-  return dsv2_launch_status("moe_grouped_down_shared");
+  if (tile_tokens == 64) {
+    launch_dma(a, false, (hipStream_t)stream, max_tiles);
+    return dsv2_launch_status("moe_grouped_down_shared");
+  }
+  return launch_gemm(a, tile_tb(tile_tokens), false, 2 * a.s_tiles + max_tiles, (hipStream_t)stream);
 }
 
 extern "C" int dsv2_moe_grouped_down(const void* hsorted, const int32_t* tiles, const int32_t* num_tiles,

@@ -52,10 +52,10 @@ _SIGS = {
     "dsv2_moe_route_down": ([_p, _i32, _p, _p, _p, _p, _i32, _i32, _p, _p, _p, _p], _i32),
     "dsv2_moe_bucket": ([_p, _i32, _i32, _p, _p, _p, _p, _p], _i32),
     "dsv2_moe_grouped_gateup": ([_p, _p, _p, _p, _i32, _i32, _p, _i32, _p, _p], _i32),
-    "dsv2_moe_grouped_gateup_shared": ([_p, _i32, _p, _p, _p, _i32, _p, _p, _i32, _p, _p, _p], _i32),
+    "dsv2_moe_grouped_gateup_shared": ([_p, _i32, _p, _p, _p, _i32, _i32, _p, _p, _i32, _p, _p, _p], _i32),
     "dsv2_moe_grouped_down": ([_p, _p, _p, _i32, _i32, _p, _i32, _p, _p], _i32),
     "dsv2_moe_combine": ([_p, _p, _p, _i32, _p, _p, _p, _p, _f32, _p, _p], _i32),
-    "dsv2_moe_grouped_down_shared": ([_p, _i32, _p, _p, _i32, _p, _p, _p, _i32, _p, _p, _p], _i32),
+    "dsv2_moe_grouped_down_shared": ([_p, _i32, _p, _p, _i32, _i32, _p, _p, _p, _i32, _p, _p, _p], _i32),
     "dsv2_moe_combine_parts": ([_p, _p, _p, _i32, _p, _p, _p, _p, _f32, _p, _p], _i32),
 }
 

@@ -230,14 +230,14 @@ int dsv2_moe_grouped_gateup(const void* xn, const int32_t* sorted_routes, const 
                             const int32_t* num_tiles, int max_tiles, int tile_tokens, const void* w_gate_up,
                             int inter, void* hsorted, void* stream);
 
-/* dsv2_moe_grouped_gateup with 64-token tiles, plus the two shared-expert halves in the same
- * launch: shared_out[t, h*inter + i] = SwiGLU(xn[t] . gate/up rows h*inter + i of sh_gate_up)
+/* dsv2_moe_grouped_gateup plus the two shared-expert halves in the same launch:
+ * shared_out[t, h*inter + i] = SwiGLU(xn[t] . gate/up rows h*inter + i of sh_gate_up)
  * for t < rows, h = 0, 1 (sh_gate_up [2*2*inter, 2048]: gate rows, then up rows), i.e. the
  * dense shared gate_up of dsv2_gemm_bf16 with DSV2_LINEAR_SWIGLU.  The tile table must come
- * from dsv2_moe_bucket with tile_tokens = 64.  Replaces _grouped_gate_up_swiglu_kernel
+ * from dsv2_moe_bucket with the same tile_tokens (16, 32 or 64).  Replaces _grouped_gate_up_swiglu_kernel
  * (moe_batch.py:152-234) and the shared MLP's gate_proj / up_proj + SiLU-mul (src/run.py:341-351). */
 int dsv2_moe_grouped_gateup_shared(const void* xn, int rows, const int32_t* sorted_routes, const int32_t* tiles,
-                                   const int32_t* num_tiles, int max_tiles, const void* w_gate_up,
+                                   const int32_t* num_tiles, int max_tiles, int tile_tokens, const void* w_gate_up,
                                    const void* sh_gate_up, int inter, void* hsorted, void* shared_out, void* stream);
 
 /* Expert-grouped down projection: ysorted[p, :] = bf16(hsorted[p, :] . Wd_e^T).
@@ -246,15 +246,14 @@ int dsv2_moe_grouped_gateup_shared(const void* xn, int rows, const int32_t* sort
 int dsv2_moe_grouped_down(const void* hsorted, const int32_t* tiles, const int32_t* num_tiles, int max_tiles,
                           int tile_tokens, const void* w_down, int inter, void* ysorted, void* stream);
 
-/* dsv2_moe_grouped_down with 64-token tiles, plus the two shared-expert halves in the same
- * launch: shared_parts[h, t, :] = fp32 shared_mid[t, h*inter : (h+1)*inter] . sh_down[:, same]^T
+/* dsv2_moe_grouped_down plus the two shared-expert halves in the same launch: shared_parts[h, t, :] = fp32 shared_mid[t, h*inter : (h+1)*inter] . sh_down[:, same]^T
  * for t < rows, h = 0, 1 (shared_mid [rows, 2*inter] from dsv2_moe_grouped_gateup_shared,
  * sh_down [2048, 2*inter]); dsv2_moe_combine_parts adds bf16(half 0 + half 1), the shared
  * MLP's down_proj output (src/run.py:351).  Replaces _grouped_down_partial_kernel
  * (moe_batch.py:238-307) and the shared experts' down projection. */
 int dsv2_moe_grouped_down_shared(const void* hsorted, int rows, const int32_t* tiles, const int32_t* num_tiles,
-                                 int max_tiles, const void* w_down, const void* shared_mid, const void* sh_down,
-                                 int inter, void* ysorted, float* shared_parts, void* stream);
+                                 int max_tiles, int tile_tokens, const void* w_down, const void* shared_mid,
+                                 const void* sh_down, int inter, void* ysorted, float* shared_parts, void* stream);
 
 /* Combine: routed = bf16(sum_s w[r,s] ysorted[route_pos[r*6+s]]) (fp32, slot order);
  * y = shared ? bf16(routed + shared[r]) : routed;  out[r] = residual ? bf16(residual[r] + y) : y.

@@ -100,6 +100,10 @@ def test_moe_tile_choice_and_cache_layout():
     assert 6 < routing_load(uniform) < 10 and tile_tokens_for_load(routing_load(uniform)) == 16
     assert routing_load(same) == 64 and tile_tokens_for_load(routing_load(same)) == 64
     assert tile_tokens_for_load(24.5) == 32
+    from dsv2lite.engine import shared_in_grouped
+
+    assert shared_in_grouped(64, 16) and shared_in_grouped(64, 64) and shared_in_grouped(256, 64)
+    assert not shared_in_grouped(256, 32) and not shared_in_grouped(256, 16) and shared_in_grouped(100, 32)
     c = CompressedKVCache(2, [5, 7, 3], device="cpu")
     assert c.base.tolist() == [0, 5, 12] and c.total == 15 and c.data.shape == (2, 15, 576)
     c.pos.copy_(torch.tensor([1, 2, 3], dtype=torch.int32))

@@ -414,11 +414,13 @@ def test_moe_grouped_tile_sizes(rows, replicated):
         assert rel_err(out, outs[16]) < 1e-2, tt
 
 
-@pytest.mark.parametrize("rows,replicated", [(64, True), (130, False)])
-def test_moe_grouped_gateup_with_shared(rows, replicated):
-    """The 64-token grouped gate_up with the shared halves in the same launch: routed rows
-    equal dsv2_moe_grouped_gateup's bit for bit, the shared output matches the fp32 SwiGLU
-    reference and the dense shared gate_up."""
+@pytest.mark.parametrize("rows,replicated,tt", [(64, True, 64), (130, False, 64), (64, False, 16), (37, False, 16),
+                                                (200, False, 32), (130, True, 32)])
+def test_moe_grouped_gateup_with_shared(rows, replicated, tt):
+    """The grouped gate_up / down with the shared halves in the same launches (16-, 32- and
+    64-token tiles): routed rows equal the plain grouped launches' bit for bit, the shared
+    output matches the fp32 SwiGLU reference and the dense shared gate_up, the fp32 halves
+    sum to the shared down projection, and the combine agrees with the oracle."""
     gu, dn, sgu, sdn = _moe_layer(70)
     xn = rnd(rows, 2048, seed=71)
     g = torch.Generator().manual_seed(72)
@@ -428,20 +430,20 @@ def test_moe_grouped_gateup_with_shared(rows, replicated):
         ids = torch.stack([torch.randperm(64, generator=g)[:6] for _ in range(rows)])
     ids32 = ids.to(torch.int32).to(DEV)
     R = rows * 6
-    max_tiles = math.ceil(R / 64) + 64
+    max_tiles = math.ceil(R / tt) + 64
     srt = torch.empty(R, dtype=torch.int32, device=DEV)
     rpos = torch.empty(R, dtype=torch.int32, device=DEV)
     tiles = torch.empty(max_tiles, 4, dtype=torch.int32, device=DEV)
     nt = torch.empty(1, dtype=torch.int32, device=DEV)
-    call("dsv2_moe_bucket", ids32.data_ptr(), rows, 64, srt.data_ptr(), rpos.data_ptr(), tiles.data_ptr(),
+    call("dsv2_moe_bucket", ids32.data_ptr(), rows, tt, srt.data_ptr(), rpos.data_ptr(), tiles.data_ptr(),
          nt.data_ptr(), st())
     hs_ref = torch.empty(R, 1408, dtype=BF, device=DEV)
-    call("dsv2_moe_grouped_gateup", xn.data_ptr(), srt.data_ptr(), tiles.data_ptr(), nt.data_ptr(), max_tiles, 64,
+    call("dsv2_moe_grouped_gateup", xn.data_ptr(), srt.data_ptr(), tiles.data_ptr(), nt.data_ptr(), max_tiles, tt,
          gu.data_ptr(), 1408, hs_ref.data_ptr(), st())
     hs = torch.empty_like(hs_ref)
     sh = torch.empty(rows, 2816, dtype=BF, device=DEV)
     call("dsv2_moe_grouped_gateup_shared", xn.data_ptr(), rows, srt.data_ptr(), tiles.data_ptr(), nt.data_ptr(),
-         max_tiles, gu.data_ptr(), sgu.data_ptr(), 1408, hs.data_ptr(), sh.data_ptr(), st())
+         max_tiles, tt, gu.data_ptr(), sgu.data_ptr(), 1408, hs.data_ptr(), sh.data_ptr(), st())
     assert torch.equal(hs, hs_ref)
     acc = xn.float() @ sgu.float().t()
     ref = rb(rb(torch.nn.functional.silu(rb(acc[:, :2816]))) * rb(acc[:, 2816:]))
@@ -453,11 +455,11 @@ def test_moe_grouped_gateup_with_shared(rows, replicated):
     # down: routed rows equal dsv2_moe_grouped_down's; the shared halves' fp32 partials sum to
     # the shared down projection; the combine of both paths agrees with the oracle
     ys_ref = torch.empty(R, 2048, dtype=BF, device=DEV)
-    call("dsv2_moe_grouped_down", hs.data_ptr(), tiles.data_ptr(), nt.data_ptr(), max_tiles, 64, dn.data_ptr(), 1408,
+    call("dsv2_moe_grouped_down", hs.data_ptr(), tiles.data_ptr(), nt.data_ptr(), max_tiles, tt, dn.data_ptr(), 1408,
          ys_ref.data_ptr(), st())
     ys = torch.empty_like(ys_ref)
     parts = torch.empty(2, rows, 2048, dtype=torch.float32, device=DEV)
-    call("dsv2_moe_grouped_down_shared", hs.data_ptr(), rows, tiles.data_ptr(), nt.data_ptr(), max_tiles,
+    call("dsv2_moe_grouped_down_shared", hs.data_ptr(), rows, tiles.data_ptr(), nt.data_ptr(), max_tiles, tt,
          dn.data_ptr(), sh.data_ptr(), sdn.data_ptr(), 1408, ys.data_ptr(), parts.data_ptr(), st())
     assert torch.equal(ys, ys_ref)
     sh_ref = sh.float() @ sdn.float().t()
