@@ -94,27 +94,29 @@ def time_dominant_kernel(eng, family: str, reps: int = 4) -> dict:
         def launch(L):
             call("dsv2_moe_route_gateup", ptr(b.xn), B, ptr(b.ids32), ptr(L.w_gu), ptr(L.sh_gu), c.moe_inter,
                  ptr(b.hbuf), stream_ptr())
-    elif b.tile_tokens == 64:
-        # 64-token tiles: the step's launch also carries the shared experts' gate_up
-        name = ("gemm_dma_kernel<true> via dsv2_moe_grouped_gateup_shared (expert-grouped gate_up+SwiGLU on "
-                "MFMA, 64-token tiles, + the 2 shared-expert halves)")
-        n_exp = int(torch.unique(b.ids32[:B]).numel())
-        bytes_per = (n_exp * 2 * c.moe_inter * c.hidden * 2 + 2 * c.shared_inter * c.hidden * 2
-                     + B * 6 * c.moe_inter * 2 + B * c.shared_inter * 2)
-
-        def launch(L):
-            call("dsv2_moe_grouped_gateup_shared", ptr(b.xn), B, ptr(b.sorted), ptr(b.tiles), ptr(b.ntiles),
-                 b.max_tiles, 64, ptr(L.w_gu), ptr(L.sh_gu), c.moe_inter, ptr(b.hs), ptr(b.shmid), stream_ptr())
     else:
+        from dsv2lite.engine import shared_in_grouped
+
         sym = {16: "gemm_xlds_kernel<1, true, 4, true, 2, 2, 1, false>",
-               32: "gemm_xlds_kernel<2, true, 4, true, 2, 4, 2, true>"}[b.tile_tokens]
-        name = f"{sym} via dsv2_moe_grouped_gateup (expert-grouped gate_up+SwiGLU on MFMA, {b.tile_tokens}-token tiles)"
+               32: "gemm_xlds_kernel<2, true, 4, true, 2, 4, 2, true>", 64: "gemm_dma_kernel<true>"}[b.tile_tokens]
         n_exp = int(torch.unique(b.ids32[:B]).numel())
         bytes_per = n_exp * 2 * c.moe_inter * c.hidden * 2 + B * 6 * c.moe_inter * 2
+        if shared_in_grouped(B, b.tile_tokens):
+            # the step's launch also carries the shared experts' gate_up
+            name = (f"{sym} via dsv2_moe_grouped_gateup_shared (expert-grouped gate_up+SwiGLU on MFMA, "
+                    f"{b.tile_tokens}-token tiles, + the 2 shared-expert halves)")
+            bytes_per += 2 * c.shared_inter * c.hidden * 2 + B * c.shared_inter * 2
 
-        def launch(L):
-            call("dsv2_moe_grouped_gateup", ptr(b.xn), ptr(b.sorted), ptr(b.tiles), ptr(b.ntiles), b.max_tiles,
-                 b.tile_tokens, ptr(L.w_gu), c.moe_inter, ptr(b.hs), stream_ptr())
+            def launch(L):
+                call("dsv2_moe_grouped_gateup_shared", ptr(b.xn), B, ptr(b.sorted), ptr(b.tiles), ptr(b.ntiles),
+                     b.max_tiles, b.tile_tokens, ptr(L.w_gu), ptr(L.sh_gu), c.moe_inter, ptr(b.hs), ptr(b.shmid),
+                     stream_ptr())
+        else:
+            name = f"{sym} via dsv2_moe_grouped_gateup (expert-grouped gate_up+SwiGLU on MFMA, {b.tile_tokens}-token tiles)"
+
+            def launch(L):
+                call("dsv2_moe_grouped_gateup", ptr(b.xn), ptr(b.sorted), ptr(b.tiles), ptr(b.ntiles), b.max_tiles,
+                     b.tile_tokens, ptr(L.w_gu), c.moe_inter, ptr(b.hs), stream_ptr())
     s = torch.cuda.Stream()
     with torch.cuda.stream(s):
         launch(moe_layers[0])
