@@ -1,6 +1,6 @@
 """Decode-throughput benchmark of the HIP DeepSeek-V2-Lite decode step on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1|2|3|r64|r256] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1|2|3|4|r64|r256] [--no-cpu-baseline]
 
 Default workload: full 27-layer random-init DeepSeek-V2-Lite
 bf16 (N(0,0.02), seed 0), bsz=1, a 128-token prompt of uniform random ids (seed
@@ -8,7 +8,8 @@ bf16 (N(0,0.02), seed 0), bsz=1, a 128-token prompt of uniform random ids (seed
 whole step replayed as one hipGraph.  Prints ONE JSON line.  --config 2|3 are the
 bsz=64/256 random-prompt workloads; r64|r256 the reference's own published workload (one
 24-token prompt replicated over the batch), whose vs_baseline is value / the published A100
-batch-family TPS for it.
+batch-family TPS for it.  --config 4 is the isolated absorbed-MLA decode microbenchmark
+(bsz=128, KV lengths U[256,8192]); its value is compressed-cache GB/s.
 
 Extra fields:
   roofline      -- dominant kernel of the step: algorithmic bytes per launch /
@@ -248,6 +249,120 @@ def summarize_trace(db: str, out: str, title: str, command: str, marker: str = "
         f.write("\n".join(L) + "\n")
 
 
+def bench_mla_micro(args) -> dict:
+    """the isolated absorbed-MLA decode (split-KV decode + LSE combine to
+    the 16x512 latent output) at bsz=128, per-row KV lengths U[256, 8192] (seed 3), q and the
+    compressed cache N(0,1) bf16.  value = cache bytes streamed per second over K graph
+    replays of the pair; roofline = the decode kernel alone (HIP events around 26-launch
+    graphs, as for the step's dominant kernel)."""
+    from triton_kernels._hip import call, ptr, stream_ptr
+    from triton_kernels.attention_decode_batch import plan_splits
+
+    import dsv2lite
+
+    cfg = dsv2lite.DSV2Config()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    B = 128
+    g = torch.Generator().manual_seed(3)
+    lens = torch.randint(256, 8193, (B,), generator=g).tolist()
+    base = torch.tensor([0] + list(torch.cumsum(torch.tensor(lens), 0)[:-1].tolist()), dtype=torch.int64)
+    cache = torch.randn(sum(lens), 576, generator=g).to(torch.bfloat16).to(dev)
+    q = torch.randn(B, 16, 576, generator=g).to(torch.bfloat16).to(dev)
+    pos = torch.tensor([n - 1 for n in lens], dtype=torch.int32, device=dev)
+    base_d = base.to(dev)
+    split, ns = plan_splits(B, max(lens))
+    po = torch.empty(B, ns, 16, 512, device=dev)
+    pm = torch.empty(B, ns, 16, 2, device=dev)
+    olat = torch.empty(B, 16, 512, dtype=torch.bfloat16, device=dev)
+    scale = cfg.softmax_scale
+
+    def decode():
+        call("dsv2_mla_decode", ptr(q), ptr(cache), ptr(base_d), ptr(pos), B, split, ns, scale, ptr(po), ptr(pm),
+             stream_ptr())
+
+    def pair():
+        decode()
+        call("dsv2_mla_combine", ptr(po), ptr(pm), ptr(pos), B, split, ns, None, ptr(olat), 16 * 512, stream_ptr())
+
+    def graph_of(fn, n):
+        s = torch.cuda.Stream()
+        with torch.cuda.stream(s):
+            fn()
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for _ in range(n):
+                fn()
+        return gr
+
+    kb = sum(lens) * 1152 + B * 16 * 576 * 2 + B * ns * 16 * 514 * 4  # cache + q reads, partial writes
+    gp = graph_of(pair, 1)
+    for _ in range(args.warmup):
+        gp.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        gp.replay()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    gd = graph_of(decode, 26)
+    gd.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(4):
+        gd.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    avg = e0.elapsed_time(e1) / 1e3 / (26 * 4)
+    roof = {"kernel": "mla_decode_kernel (split-KV absorbed-MLA decode, MFMA)", "bound": "hbm",
+            "achieved": kb / avg / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": kb / avg / HBM_PEAK,
+            "traffic": measured_traffic(4, "mla_decode_kernel"), "bytes_per_launch": kb, "avg_us": avg * 1e6}
+    value = kb * args.steps / dt / 1e9
+    out = {
+        "metric": "absorbed-MLA decode kernel: compressed-cache GB/s (BASELINE config 4)", "value": round(value, 1),
+        "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(dt / args.steps * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: q and compressed cache N(0,1) bf16, KV lengths U[256,8192] seed 3",
+        "config": {"workload": "C4: absorbed-MLA decode microbenchmark, bsz=128, 16 heads, 512+64, split-KV + "
+                               "LSE combine", "global_batch": B, "seq_len": max(lens), "kv_tokens": sum(lens),
+                   "split_tokens": split, "max_splits": ns, "parallelism": "none (1 GPU)"},
+        "roofline": roof,
+    }
+    if args.copy_calibration:
+        _copy_calibration(out, dev)
+    if not args.no_cpu_baseline:
+        _log("cpu baseline (fp32 attention on the host)")
+        torch.set_num_threads(os.cpu_count() or 1)
+        qc, cc = q.float().cpu(), cache.float().cpu()
+        rows, tc = 0, 0.0
+        while tc < 10.0 and rows < B:  # rows in order until about 10 s of host work
+            c = cc[int(base[rows]):int(base[rows]) + lens[rows]]
+            t0 = time.perf_counter()
+            p = torch.softmax((qc[rows] @ c.t()) * scale, dim=-1)
+            _ = p @ c[:, :512]
+            tc += time.perf_counter() - t0
+            rows += 1
+        cb = sum(lens[:rows]) * 1152
+        out["cpu_baseline"] = {"value": cb / tc / 1e9, "unit": "GB/s", "cores": torch.get_num_threads(),
+                               "kind": "port", "sample": f"rows 0-{rows - 1} ({sum(lens[:rows])} cached tokens), "
+                                                         f"fp32 torch softmax(q K^T) V on the host, {tc:.2f}s"}
+    return out
+
+
+def _copy_calibration(out: dict, dev) -> None:
+    """Three plain 512 MiB device copies at the end of the run: the PMC byte counters of a
+    copy of known size scale the dominant kernel's (--pmc-traffic)."""
+    src = torch.empty(256 * 2**20, dtype=torch.float16, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    out["copy_calibration_bytes"] = {"read": src.nbytes, "write": dst.nbytes}
+
+
 def cpu_baseline(max_seconds: float = 30.0) -> dict:
     """Oracle (PyTorch eager, HF math) on the host cores, BASELINE config 0."""
     from oracle import dsv2_oracle as O
@@ -303,7 +418,7 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=99)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="1", choices=[str(k) for k in CONFIGS])
+    ap.add_argument("--config", default="1", choices=[str(k) for k in CONFIGS] + ["4"])
     ap.add_argument("--family", choices=("small", "batch"), default=None)
     ap.add_argument("--mla-path", choices=("fused", "split"), default="fused",
                     help="small family: one fused MLA kernel per layer, or prepare + split-KV decode + combine")
@@ -336,6 +451,9 @@ def main() -> None:
     import dsv2lite
 
     args.config = int(args.config) if args.config.isdigit() else args.config
+    if args.config == 4:
+        print(json.dumps(bench_mla_micro(args)), flush=True)
+        return
     spec = CONFIGS[args.config]
     family = args.family or spec["family"]
     cfg = dsv2lite.DSV2Config()
@@ -404,13 +522,7 @@ def main() -> None:
         "setup_s": {"init_weights": round(t_init, 2), "prefill": round(t_prefill, 3)},
     }
     if args.copy_calibration:
-        src = torch.empty(256 * 2**20, dtype=torch.float16, device=dev).fill_(1.0)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        out["copy_calibration_bytes"] = {"read": src.nbytes, "write": dst.nbytes}
-        del src, dst
+        _copy_calibration(out, dev)
     if not args.no_cpu_baseline:
         _log("cpu baseline (oracle, config 0)")
         out["cpu_baseline"] = cpu_baseline()

@@ -488,6 +488,7 @@ def _mla_reference(q, cache_rows, lens, scale):
 
 
 @pytest.mark.parametrize("B,lo,hi,seed,split", [(1, 1, 40, 50, None), (3, 1, 300, 51, None), (16, 256, 8192, 3, None),
+                                                (128, 256, 8192, 3, None),
                                                 (2, 500, 1300, 52, 1056), (3, 40, 200, 53, 128), (4, 1, 97, 54, 96)])
 def test_mla_decode_combine_vs_fp32(B, lo, hi, seed, split):
     """Split plan of the engine, or a fixed one: 33 tiles (odd) / 4 tiles (even, last one
