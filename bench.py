@@ -271,7 +271,11 @@ def bench_mla_micro(args) -> dict:
     q = torch.randn(B, 16, 576, generator=g).to(torch.bfloat16).to(dev)
     pos = torch.tensor([n - 1 for n in lens], dtype=torch.int32, device=dev)
     base_d = base.to(dev)
+    # the engine's plan (by the longest row); measured against it on MI355X, decode kernel:
+    # split 2048 (4 splits) 132 us, 1536 154 us, 1120 155 us, 1024 148 us, 768 137 us
     split, ns = plan_splits(B, max(lens))
+    if args.mla_split:
+        split, ns = args.mla_split, math.ceil(max(lens) / args.mla_split)
     po = torch.empty(B, ns, 16, 512, device=dev)
     pm = torch.empty(B, ns, 16, 2, device=dev)
     olat = torch.empty(B, 16, 512, dtype=torch.bfloat16, device=dev)
@@ -431,6 +435,7 @@ def main() -> None:
     ap.add_argument("--pmc-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="no GPU: HBM bytes per dispatch of --kernel from two --pmc runs (FETCH_SIZE, WRITE_SIZE) "
                          "scaled by the run's calibration copies; written to --out")
+    ap.add_argument("--mla-split", type=int, default=0, help="config 4: split_tokens override (multiple of 32)")
     ap.add_argument("--kernel", default=None)
     ap.add_argument("--out", default=None)
     ap.add_argument("--title", default="")
