@@ -49,12 +49,13 @@ def moe_tile_tokens(rows: int, n_experts: int = 64, top_k: int = 6) -> int:
 
 
 def tile_tokens_for_load(load: float) -> int:
-    """Token tile for a mean of `load` routes per routed expert.  Measured on MI355X (gate_up +
-    down per layer): 16-token tiles at 6 routes/expert (bsz=64, random prompts), 32-token
-    tiles at 24 (bsz=256: 250 us vs 289 us with 16; 64-token tiles, on the direct-to-LDS ring
-    GEMM, tie with 32 there: 21.73k vs 21.77k tok/s), 64-token tiles when every row takes
-    the same 6 experts (bsz=64: 19.1k tok/s vs 17.0k with 32)."""
-    return 16 if load <= 10 else (32 if load <= 40 else 64)
+    """Token tile for a mean of `load` routes per routed expert.  Measured on MI355X, whole
+    decode step (the 64-token tiles run on the direct-to-LDS ring GEMM, every size with the
+    shared experts folded in where shared_in_grouped allows): bsz=64 random prompts (about
+    7 routes per expert) 8.71k tok/s with 32-token tiles vs 8.58k with 16 and 8.13k with 64;
+    bsz=256 (about 25) 22.42k with 64 vs 21.79k with 32; every row on the same 6 experts
+    (64 or 256 routes per expert) 64."""
+    return 16 if load <= 3 else (32 if load <= 12 else 64)
 
 
 def shared_in_grouped(rows: int, tile_tokens: int) -> bool:

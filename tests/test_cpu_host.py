@@ -90,16 +90,16 @@ def test_moe_tile_choice_and_cache_layout():
     from dsv2lite.cache import CompressedKVCache
     from dsv2lite.engine import moe_tile_tokens
 
-    assert moe_tile_tokens(1) == 16 and moe_tile_tokens(64) == 16 and moe_tile_tokens(256) == 32
-    assert moe_tile_tokens(512) == 64
+    assert moe_tile_tokens(1) == 16 and moe_tile_tokens(16) == 16 and moe_tile_tokens(64) == 32
+    assert moe_tile_tokens(256) == 64 and moe_tile_tokens(512) == 64
     from dsv2lite.engine import routing_load, tile_tokens_for_load
 
     g = torch.Generator().manual_seed(0)
     uniform = torch.stack([torch.randperm(64, generator=g)[:6] for _ in range(64)])
     same = torch.tensor([7, 16, 25, 34, 43, 52]).repeat(64, 1)
-    assert 6 < routing_load(uniform) < 10 and tile_tokens_for_load(routing_load(uniform)) == 16
+    assert 6 < routing_load(uniform) < 10 and tile_tokens_for_load(routing_load(uniform)) == 32
     assert routing_load(same) == 64 and tile_tokens_for_load(routing_load(same)) == 64
-    assert tile_tokens_for_load(24.5) == 32
+    assert tile_tokens_for_load(24.5) == 64 and tile_tokens_for_load(2.0) == 16
     from dsv2lite.engine import shared_in_grouped
 
     assert shared_in_grouped(64, 16) and shared_in_grouped(64, 64) and shared_in_grouped(256, 64)
