@@ -232,3 +232,20 @@ def test_greedy_agreement_teacher_forced_40_steps(model, family):
         tok = int(torch.argmax(ref))
     print(f"{family}: greedy agreement {agree}/{steps}", flush=True)
     assert agree / steps >= 0.95, (agree, steps)
+
+
+@pytest.mark.parametrize("family,bsz", [("small", 1), ("batch", 3)])
+def test_run_cli_end_to_end(family, bsz):
+    """src/run.py (the reference's CLI surface) runs the captured decode on the GPU with a
+    3-layer random-init model: prefill, graph replays, JSON result with the reference's keys
+    and the requested number of generated tokens per row."""
+    from src import run as R
+
+    out = R.main(["--kernel-family", family, "--batch-size", str(bsz), "--layers", "3", "--max-new-tokens", "5",
+                  "--prompt-len", "16", "--dump-token-ids"])
+    assert out["batch_size"] == bsz and out["tps"] > 0 and out["decode_tokens"] > 0
+    assert out["path"] == R.PATH_NAMES[family]
+    ids = out["generated_token_ids"]
+    ids = [ids] if bsz == 1 else ids  # the reference's JSON keeps one row flat (run.py:691-705)
+    assert len(ids) == bsz and all(len(r) == 5 for r in ids)
+    assert all(0 <= t < 102400 for r in ids for t in r)
