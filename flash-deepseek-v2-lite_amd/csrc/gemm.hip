@@ -28,8 +28,8 @@ struct GemmArgs {
   void* Y;
   int64_t ys, yg;
   bool out_f32;
-  // grouped ring GEMM: the shared-expert halves (one 64-token tile per `rows` chunk and half,
-  // after the table's tiles): half h reads token t at X2 + h*x2g + t*x2s, its (gate) weight
+  // grouped launches: the shared-expert halves (a token tile of the launch's size per chunk
+  // of `rows` and half, ahead of the table's tiles): half h reads token t at X2 + h*x2g + t*x2s, its (gate) weight
   // rows at W2 + h*w2g with row stride w2ld (SwiGLU: up row = gate row + w2up), and writes
   // Y2[h * y2g + t * y2s + n] (SwiGLU: bf16; plain: the fp32 partial sum; no residual)
   const bf16_t* X2;
@@ -402,7 +402,8 @@ __device__ __forceinline__ void gemm_store4(const GemmArgs& a, int g, int slot, 
   }
 }
 
-// Direct-to-LDS ring shape for dense weights and 128+ tokens: a 4-wave workgroup owns 64
+// Direct-to-LDS ring shape for dense weights at 128+ tokens (the lm_head from 33) and for the
+// expert-grouped MoE's 64-token tiles: a 4-wave workgroup owns 64
 // features x 64 tokens (each wave 32 x 32, 2 x 2 MFMA blocks).  K streams in 64-wide chunks
 // through a ring of kDmaStages 16 KB LDS stages filled by global_load_lds (16 bytes per
 // lane straight into LDS, no register round trip): every load covers 8 rows x 128 B, and
