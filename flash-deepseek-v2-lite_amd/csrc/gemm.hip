@@ -29,9 +29,10 @@ struct GemmArgs {
   int64_t ys, yg;
   bool out_f32;
   // grouped launches: the shared-expert halves (a token tile of the launch's size per chunk
-  // of `rows` and half, ahead of the table's tiles): half h reads token t at X2 + h*x2g + t*x2s, its (gate) weight
-  // rows at W2 + h*w2g with row stride w2ld (SwiGLU: up row = gate row + w2up), and writes
-  // Y2[h * y2g + t * y2s + n] (SwiGLU: bf16; plain: the fp32 partial sum; no residual)
+  // of `rows` and half, ahead of the table's tiles): half h reads token t at
+  // X2 + h*x2g + t*x2s, its (gate) weight rows at W2 + h*w2g with row stride w2ld (SwiGLU:
+  // up row = gate row + w2up), and writes Y2[h * y2g + t * y2s + n] (SwiGLU: bf16; plain:
+  // the fp32 partial sum; no residual)
   const bf16_t* X2;
   int64_t x2s, x2g;
   const bf16_t* W2;
