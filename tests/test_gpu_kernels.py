@@ -415,7 +415,7 @@ def test_moe_grouped_tile_sizes(rows, replicated):
 
 
 @pytest.mark.parametrize("rows,replicated,tt", [(64, True, 64), (130, False, 64), (64, False, 16), (37, False, 16),
-                                                (200, False, 32), (130, True, 32)])
+                                                (200, False, 32), (130, True, 32), (1024, False, 64)])
 def test_moe_grouped_gateup_with_shared(rows, replicated, tt):
     """The grouped gate_up / down with the shared halves in the same launches (16-, 32- and
     64-token tiles): routed rows equal the plain grouped launches' bit for bit, the shared
