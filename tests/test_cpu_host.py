@@ -173,3 +173,38 @@ def test_run_cli_refuses_checkpoint_and_needs_gpu():
     if not torch.cuda.is_available():
         with pytest.raises(RuntimeError, match="GPU is required"):
             R.main([])
+
+
+def test_bench_pmc_traffic_scaling_and_tail(tmp_path):
+    """bench.py --pmc-traffic: per-dispatch counters of the kernel scaled by the calibration
+    copies; only the last DOMINANT_DISPATCHES dispatches of the kernel count (the timing
+    graph's), so earlier launches of the same symbol (prefill) do not mix in."""
+    import csv
+    import importlib
+    import sys
+
+    sys.path.insert(0, str(ROOT))
+    bench = importlib.import_module("bench")
+    n = bench.DOMINANT_DISPATCHES
+
+    def write(path, per_kernel, copy_kib):
+        rows, d = [], 0
+        for v in [10_000.0] * 7 + [per_kernel] * n:  # 7 prefill launches with other counts
+            d += 1
+            rows.append({"Dispatch_Id": d, "Kernel_Name": "void mykernel<1>(Args)", "Counter_Value": v})
+        for v in copy_kib:
+            d += 1
+            rows.append({"Dispatch_Id": d, "Kernel_Name": "__amd_rocclr_copyBuffer", "Counter_Value": v})
+        with open(path, "w", newline="") as f:
+            w = csv.DictWriter(f, fieldnames=["Dispatch_Id", "Kernel_Name", "Counter_Value"])
+            w.writeheader()
+            w.writerows(rows)
+
+    fpath, wpath = tmp_path / "f.csv", tmp_path / "w.csv"
+    write(fpath, 1000.0, [262144.0, 262145.0, 262146.0])  # 512 MiB copy reads 256 MiB-worth: scale 2
+    write(wpath, 10.0, [524288.0] * 3)
+    res = bench.pmc_traffic(str(fpath), str(wpath), "mykernel<1>", 512 * 2**20, str(tmp_path / "t.json"), "cmd")
+    assert res["dispatches"] == [n, n]
+    assert res["fetch_kib_per_dispatch"] == 1000.0 and res["write_kib_per_dispatch"] == 10.0
+    f_scale = 512 * 2**20 / (262145.0 * 1024)
+    assert math.isclose(res["traffic_bytes_per_dispatch"], 1000.0 * 1024 * f_scale + 10.0 * 1024, rel_tol=1e-12)
