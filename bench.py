@@ -2,7 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1|2|3|4|r64|r256] [--no-cpu-baseline]
 
-Default workload: full 27-layer random-init DeepSeek-V2-Lite
+Default workload (benchmark config 1): full 27-layer random-init DeepSeek-V2-Lite
 bf16 (N(0,0.02), seed 0), bsz=1, a 128-token prompt of uniform random ids (seed
 1), eager prefill, then K greedy decode steps with the small kernel family, the
 whole step replayed as one hipGraph.  Prints ONE JSON line.  --config 2|3 are the
@@ -20,7 +20,7 @@ Extra fields:
   step_roofline -- algorithmic bytes per step (weights of the experts actually hit,
                    counted from the router output, + compressed KV read) / step time.
   cpu_baseline  -- the CPU oracle (PyTorch eager restatement of the HF math) timed on
-                   this host on BASELINE config 0 (one MoE layer: prefill 256 + 32
+                   this host on benchmark config 0 (one MoE layer: prefill 256 + 32
                    decode steps) and scaled to whole-model tokens/s.
 """
 
@@ -250,7 +250,7 @@ def summarize_trace(db: str, out: str, title: str, command: str, marker: str = "
 
 
 def bench_mla_micro(args) -> dict:
-    """the isolated absorbed-MLA decode (split-KV decode + LSE combine to
+    """benchmark config 4: the isolated absorbed-MLA decode (split-KV decode + LSE combine to
     the 16x512 latent output) at bsz=128, per-row KV lengths U[256, 8192] (seed 3), q and the
     compressed cache N(0,1) bf16.  value = cache bytes streamed per second over K graph
     replays of the pair; roofline = the decode kernel alone (HIP events around 26-launch
@@ -325,7 +325,7 @@ def bench_mla_micro(args) -> dict:
             "traffic": measured_traffic(4, "mla_decode_kernel"), "bytes_per_launch": kb, "avg_us": avg * 1e6}
     value = kb * args.steps / dt / 1e9
     out = {
-        "metric": "absorbed-MLA decode kernel: compressed-cache GB/s (BASELINE config 4)", "value": round(value, 1),
+        "metric": "absorbed-MLA decode kernel: compressed-cache GB/s (benchmark config 4)", "value": round(value, 1),
         "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(dt / args.steps * 1e3, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16",
@@ -368,7 +368,7 @@ def _copy_calibration(out: dict, dev) -> None:
 
 
 def cpu_baseline(max_seconds: float = 30.0) -> dict:
-    """Oracle (PyTorch eager, HF math) on the host cores, BASELINE config 0."""
+    """Oracle (PyTorch eager, HF math) on the host cores, benchmark config 0."""
     from oracle import dsv2_oracle as O
 
     cores = os.cpu_count() or 1

@@ -12,7 +12,7 @@ random-init DeepSeek-V2-Lite (N(0,0.02) bf16, seed --seed), and the prompt is
 ``--prompt-len`` uniform random token ids (seed --prompt-seed).  As in the
 reference (run.py:733-741) one prompt is replicated across the batch unless
 ``--prompt-len-range`` draws one length (and prompt) per row.  ``--config N``
-selects BASELINE config N (1: bsz=1 prompt 128 small; 2: bsz=64 lengths
+selects benchmark config N (1: bsz=1 prompt 128 small; 2: bsz=64 lengths
 U[256,1024] batch; 3: bsz=256 prompt 2048 batch).
 
 Flow per batch size (run.py:591-688): prefill -> snapshot -> 3 eager warmup
