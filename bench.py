@@ -301,13 +301,13 @@ def bench_mla_micro(args) -> dict:
         return gr
 
     kb = sum(lens) * 1152 + B * 16 * 576 * 2 + B * ns * 16 * 514 * 4  # cache + q reads, partial writes
-    gp = graph_of(pair, 1)
-    for _ in range(args.warmup):
-        gp.replay()
+    # the K timed steps are one graph of K decode + combine pairs (a graph launch per pair
+    # would time the host's launch rate, not the GPU's)
+    gw, gk = graph_of(pair, max(args.warmup, 1)), graph_of(pair, args.steps)
+    gw.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        gp.replay()
+    gk.replay()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     gd = graph_of(decode, 26)
