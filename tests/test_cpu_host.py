@@ -208,3 +208,13 @@ def test_bench_pmc_traffic_scaling_and_tail(tmp_path):
     assert res["fetch_kib_per_dispatch"] == 1000.0 and res["write_kib_per_dispatch"] == 10.0
     f_scale = 512 * 2**20 / (262145.0 * 1024)
     assert math.isclose(res["traffic_bytes_per_dispatch"], 1000.0 * 1024 * f_scale + 10.0 * 1024, rel_tol=1e-12)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py --gpus N>1 exits with a message before touching a GPU (this build measures one)."""
+    import subprocess
+    import sys
+
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 2 and "one GPU" in r.stderr and r.stdout == ""

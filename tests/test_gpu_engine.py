@@ -249,3 +249,29 @@ def test_run_cli_end_to_end(family, bsz):
     ids = [ids] if bsz == 1 else ids  # the reference's JSON keeps one row flat (run.py:691-705)
     assert len(ids) == bsz and all(len(r) == 5 for r in ids)
     assert all(0 <= t < 102400 for r in ids for t in r)
+
+
+def test_bench_json_contract():
+    """bench.py (the driver's entry point) prints ONE JSON line with the contract's keys, a
+    roofline object for the dominant kernel and (here skipped) no cpu_baseline."""
+    import json
+    import math
+    import os
+    import subprocess
+    import sys
+
+    from golden_utils import ROOT
+
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--steps", "3", "--warmup", "1", "--no-cpu-baseline"],
+                       capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0, r.stderr[-2000:]
+    lines = [ln for ln in r.stdout.splitlines() if ln.strip()]
+    assert len(lines) == 1
+    d = json.loads(lines[0])
+    for k in ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "higher_is_better", "scaling",
+              "vs_baseline", "dtype", "data", "config", "roofline"):
+        assert k in d, k
+    assert d["n_gpus"] == 1 and d["steps"] == 3 and d["value"] > 0 and "workload" in d["config"]
+    roof = d["roofline"]
+    assert roof["bound"] == "hbm" and roof["unit"] == "GB/s" and 0 < roof["frac"] < 1
+    assert math.isclose(roof["frac"], roof["achieved"] / roof["peak"], rel_tol=1e-9)
