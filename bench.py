@@ -271,9 +271,10 @@ def bench_mla_micro(args) -> dict:
     q = torch.randn(B, 16, 576, generator=g).to(torch.bfloat16).to(dev)
     pos = torch.tensor([n - 1 for n in lens], dtype=torch.int32, device=dev)
     base_d = base.to(dev)
-    # the engine's plan (by the longest row); measured against it on MI355X, decode kernel:
-    # split 2048 (4 splits) 132 us, 1536 154 us, 1120 155 us, 1024 148 us, 768 137 us
-    split, ns = plan_splits(B, max(lens))
+    # the planner with 512 workgroups, which suits these very unequal lengths (the engine's
+    # 256 suits its equal-length batches); measured on MI355X, decode kernel: split 2048 (4
+    # splits) 132 us, 4064 171 us, 1536 154 us, 1120 155 us, 1024 148 us, 768 137 us
+    split, ns = plan_splits(B, max(lens), target_wgs=512)
     if args.mla_split:
         split, ns = args.mla_split, math.ceil(max(lens) / args.mla_split)
     po = torch.empty(B, ns, 16, 512, device=dev)

@@ -49,12 +49,16 @@ def pack_attention_weights(attn: torch.nn.Module) -> AttentionPackedWeights:
                                   attn.o_proj.weight.detach().contiguous())
 
 
-def plan_splits(rows: int, max_ctx: int, target_wgs: int = 512) -> tuple[int, int]:
+def plan_splits(rows: int, max_ctx: int, target_wgs: int = 256) -> tuple[int, int]:
     """(split_tokens, max_splits) for the split-KV decode: about target_wgs workgroups,
-    split_tokens a multiple of 32, at most 64 splits per row.  512 = two resident
-    workgroups per CU in one round; each streams its split with two tiles in flight, which
-    measured faster on MI355X than twice as many half-length splits (bsz=256 x 2098 tokens:
-    109 vs 118 us per layer; bsz=128 x U[256,8192]: 135 vs 160 us)."""
+    split_tokens a multiple of 32, at most 64 splits per row.  256 = one workgroup per CU;
+    each streams its split with two tiles in flight.  Measured on MI355X over the whole
+    decode step against 512: bsz=256 x 2048-token prompts 22.72k vs 22.44k tok/s, bsz=64 x
+    U[256,1024] 8.80k vs 8.70k, reference workload 52.6k vs 51.3k (bsz=256) and 22.0k vs
+    22.0k (bsz=64); 128 (8.55k at bsz=64) and 1024 (bsz=256 x 2098 tokens: 118 vs 109 us per
+    layer) are slower.  Rows of very unequal lengths want more, shorter splits (bsz=128 x
+    U[256,8192]: 512 -> 2048-token splits 132 us, 256 -> 4064-token splits 171 us); capping
+    the split at 2048 tokens instead cost the equal-length bsz=256 step 8%."""
     per_row = max(1, min(64, math.ceil(target_wgs / max(rows, 1))))
     split = max(32, math.ceil(math.ceil(max_ctx / per_row) / 32) * 32)
     split = max(split, math.ceil(max_ctx / 64 / 32) * 32)
