@@ -270,6 +270,7 @@ def bench_mla_micro(args) -> dict:
     cache = torch.randn(sum(lens), 576, generator=g).to(torch.bfloat16).to(dev)
     q = torch.randn(B, 16, 576, generator=g).to(torch.bfloat16).to(dev)
     pos = torch.tensor([n - 1 for n in lens], dtype=torch.int32, device=dev)
+    cap = torch.tensor(lens, dtype=torch.int32, device=dev)
     base_d = base.to(dev)
     # the planner with 512 workgroups, which suits these very unequal lengths (the engine's
     # 256 suits its equal-length batches); measured on MI355X, decode kernel: split 2048 (4
@@ -283,12 +284,13 @@ def bench_mla_micro(args) -> dict:
     scale = cfg.softmax_scale
 
     def decode():
-        call("dsv2_mla_decode", ptr(q), ptr(cache), ptr(base_d), ptr(pos), B, split, ns, scale, ptr(po), ptr(pm),
-             stream_ptr())
+        call("dsv2_mla_decode", ptr(q), ptr(cache), ptr(base_d), ptr(pos), ptr(cap), B, split, ns, scale, ptr(po),
+             ptr(pm), stream_ptr())
 
     def pair():
         decode()
-        call("dsv2_mla_combine", ptr(po), ptr(pm), ptr(pos), B, split, ns, None, ptr(olat), 16 * 512, stream_ptr())
+        call("dsv2_mla_combine", ptr(po), ptr(pm), ptr(pos), ptr(cap), B, split, ns, None, ptr(olat), 16 * 512,
+             stream_ptr())
 
     def graph_of(fn, n):
         s = torch.cuda.Stream()

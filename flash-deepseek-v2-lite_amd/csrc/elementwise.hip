@@ -92,6 +92,32 @@ extern "C" int dsv2_residual_add_bf16(const void* a, const void* b, void* out, i
   return dsv2_launch_status("residual_add");
 }
 
+// fp16 variant: o = fp16(fp32(a) + fp32(b)) with round-to-nearest-even conversions
+__global__ void residual_add_f16_kernel(const uint4* __restrict__ a, const uint4* __restrict__ b,
+                                        uint4* __restrict__ o, int64_t nch) {
+  typedef _Float16 halfx8_t __attribute__((ext_vector_type(8)));
+  const int64_t c = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (c >= nch) return;
+  const halfx8_t va = __builtin_bit_cast(halfx8_t, a[c]), vb = __builtin_bit_cast(halfx8_t, b[c]);
+  halfx8_t r;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = static_cast<_Float16>(static_cast<float>(va[i]) + static_cast<float>(vb[i]));
+  o[c] = __builtin_bit_cast(uint4, r);
+}
+
+extern "C" int dsv2_residual_add_f16(const void* a, const void* b, void* out, int64_t n, void* stream) {
+  DSV2_REQUIRE(a && b && out, DSV2_E_NULL, "residual_add_f16: null pointer");
+  DSV2_REQUIRE(n >= 0 && n % 8 == 0, DSV2_E_SHAPE, "residual_add_f16: n=%lld must be a multiple of 8",
+               (long long)n);
+  DSV2_REQUIRE(dsv2_aligned16(a) && dsv2_aligned16(b) && dsv2_aligned16(out), DSV2_E_ALIGN,
+               "residual_add_f16: pointers must be 16-byte aligned");
+  if (n == 0) return DSV2_OK;
+  const int64_t nch = n / 8;
+  hipLaunchKernelGGL(residual_add_f16_kernel, dim3((unsigned)((nch + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint4*)a, (const uint4*)b, (uint4*)out, nch);
+  return dsv2_launch_status("residual_add_f16");
+}
+
 // ---------------------------------------------------------------------------
 __global__ void silu_mul_kernel(const bf16_t* __restrict__ g, const bf16_t* __restrict__ u,
                                 bf16_t* __restrict__ o, int64_t nch) {
@@ -118,38 +144,48 @@ extern "C" int dsv2_silu_mul_bf16(const void* gate, const void* up, void* out, i
 }
 
 // ---------------------------------------------------------------------------
-__global__ void prepare_inputs_kernel(const int64_t* __restrict__ cache_position, int64_t* __restrict__ mask,
-                                      int64_t* __restrict__ position_ids, int max_len) {
+__global__ void prepare_inputs_kernel(const int64_t* __restrict__ cache_position, const int64_t* __restrict__ index,
+                                      int64_t* __restrict__ mask, int64_t* __restrict__ position_ids, int max_len) {
   const int b = blockIdx.y;
   const int j = blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t pos = cache_position[0];
-  if (j < max_len) mask[(int64_t)b * max_len + j] = (j <= pos) ? 1 : 0;
+  if (j < max_len) {
+    const int64_t idx = index ? index[j] : j;
+    mask[(int64_t)b * max_len + j] = (idx <= pos) ? 1 : 0;
+  }
   if (blockIdx.x == 0 && threadIdx.x == 0) position_ids[b] = pos;
 }
 
-extern "C" int dsv2_prepare_decode_inputs(const int64_t* cache_position, int64_t* attention_mask,
-                                          int64_t* position_ids, int batch, int max_len, void* stream) {
+extern "C" int dsv2_prepare_decode_inputs(const int64_t* cache_position, const int64_t* attention_mask_index,
+                                          int64_t* attention_mask, int64_t* position_ids, int batch, int max_len,
+                                          void* stream) {
   DSV2_REQUIRE(cache_position && attention_mask && position_ids, DSV2_E_NULL, "prepare_decode_inputs: null pointer");
   DSV2_REQUIRE(batch >= 0 && max_len > 0 && batch <= 65535, DSV2_E_SHAPE, "prepare_decode_inputs: bad shape");
   if (batch == 0) return DSV2_OK;
   hipLaunchKernelGGL(prepare_inputs_kernel, dim3((max_len + 255) / 256, batch), dim3(256), 0, (hipStream_t)stream,
-                     cache_position, attention_mask, position_ids, max_len);
+                     cache_position, attention_mask_index, attention_mask, position_ids, max_len);
   return dsv2_launch_status("prepare_decode_inputs");
 }
 
 // ---------------------------------------------------------------------------
 __global__ void copy_token_rows_kernel(const uint4* __restrict__ src, int64_t src_bstride16, uint4* __restrict__ dst,
-                                       int64_t dst_bstride16, int64_t row16, const int64_t* __restrict__ cache_position) {
+                                       int64_t dst_bstride16, int64_t row16, const int64_t* __restrict__ cache_position,
+                                       int64_t max_tokens, int32_t* __restrict__ status) {
   const int b = blockIdx.y;
   const int64_t pos = cache_position[0];
+  if (pos < 0 || pos >= max_tokens) {  // past the cache: nothing is written, the status is flagged
+    if (status && threadIdx.x == 0 && blockIdx.x == 0) atomicOr(status, DSV2_DEVERR_CACHE_FULL);
+    return;
+  }
   for (int64_t c = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; c < row16; c += (int64_t)gridDim.x * blockDim.x)
     dst[b * dst_bstride16 + pos * row16 + c] = src[b * src_bstride16 + c];
 }
 
 extern "C" int dsv2_copy_token_rows(const void* src, int64_t src_batch_stride, void* dst, int64_t dst_batch_stride,
-                                    int64_t row_bytes, const int64_t* cache_position, int batch, void* stream) {
+                                    int64_t row_bytes, const int64_t* cache_position, int64_t max_tokens, int batch,
+                                    int32_t* status, void* stream) {
   DSV2_REQUIRE(src && dst && cache_position, DSV2_E_NULL, "copy_token_rows: null pointer");
-  DSV2_REQUIRE(batch >= 0 && batch <= 65535 && row_bytes > 0 && row_bytes % 16 == 0, DSV2_E_SHAPE,
+  DSV2_REQUIRE(batch >= 0 && batch <= 65535 && row_bytes > 0 && row_bytes % 16 == 0 && max_tokens > 0, DSV2_E_SHAPE,
                "copy_token_rows: bad shape");
   DSV2_REQUIRE(dsv2_aligned16(src) && dsv2_aligned16(dst) && src_batch_stride % 16 == 0 &&
                    dst_batch_stride % 16 == 0,
@@ -158,26 +194,31 @@ extern "C" int dsv2_copy_token_rows(const void* src, int64_t src_batch_stride, v
   const int64_t row16 = row_bytes / 16;
   const unsigned gx = (unsigned)((row16 + 255) / 256 < 64 ? (row16 + 255) / 256 : 64);
   hipLaunchKernelGGL(copy_token_rows_kernel, dim3(gx, batch), dim3(256), 0, (hipStream_t)stream, (const uint4*)src,
-                     src_batch_stride / 16, (uint4*)dst, dst_batch_stride / 16, row16, cache_position);
+                     src_batch_stride / 16, (uint4*)dst, dst_batch_stride / 16, row16, cache_position, max_tokens,
+                     status);
   return dsv2_launch_status("copy_token_rows");
 }
 
 // ---------------------------------------------------------------------------
 __global__ void fill_positions_kernel(const int64_t* __restrict__ cache_position, int32_t* __restrict__ pos,
-                                      int64_t* __restrict__ base, int64_t cap, int batch) {
+                                      int64_t* __restrict__ base, int32_t* __restrict__ capv, int64_t cap, int batch) {
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= batch) return;
-  pos[b] = static_cast<int32_t>(cache_position[0]);
+  // positions outside int32 saturate; the capacity check downstream then rejects them
+  const int64_t p = cache_position[0];
+  pos[b] = static_cast<int32_t>(p < 0 ? -1 : (p > 0x7fffffff ? 0x7fffffff : p));
   if (base) base[b] = (int64_t)b * cap;
+  if (capv) capv[b] = static_cast<int32_t>(cap);
 }
 
-extern "C" int dsv2_fill_positions(const int64_t* cache_position, int32_t* pos, int64_t* base,
+extern "C" int dsv2_fill_positions(const int64_t* cache_position, int32_t* pos, int64_t* base, int32_t* cap,
                                    int64_t per_row_capacity, int batch, void* stream) {
   DSV2_REQUIRE(cache_position && pos, DSV2_E_NULL, "fill_positions: null pointer");
-  DSV2_REQUIRE(batch >= 0, DSV2_E_SHAPE, "fill_positions: bad batch");
+  DSV2_REQUIRE(batch >= 0 && batch <= (1 << 24) && per_row_capacity > 0 && per_row_capacity <= 0x7fffffff,
+               DSV2_E_SHAPE, "fill_positions: bad batch or capacity");
   if (batch == 0) return DSV2_OK;
   hipLaunchKernelGGL(fill_positions_kernel, dim3((batch + 255) / 256), dim3(256), 0, (hipStream_t)stream,
-                     cache_position, pos, base, per_row_capacity, batch);
+                     cache_position, pos, base, cap, per_row_capacity, batch);
   return dsv2_launch_status("fill_positions");
 }
 

@@ -36,11 +36,12 @@ template <bool ABSORB>
 __global__ __launch_bounds__(256) void mla_prepare_kernel(const bf16_t* __restrict__ qkva, int64_t qs, int rows,
                                                           const int32_t* __restrict__ pos,
                                                           const int64_t* __restrict__ base,
+                                                          const int32_t* __restrict__ cap,
                                                           const bf16_t* __restrict__ kvw, float eps,
                                                           const bf16_t* __restrict__ cosT,
                                                           const bf16_t* __restrict__ sinT, int max_pos,
                                                           const bf16_t* __restrict__ w_ukt, bf16_t* __restrict__ cache,
-                                                          bf16_t* __restrict__ qout) {
+                                                          bf16_t* __restrict__ qout, int32_t* __restrict__ status) {
   constexpr int RB = ABSORB ? 8 : 1;  // RoPE/cache only: one row per workgroup
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int b0 = blockIdx.y * RB;
@@ -94,6 +95,11 @@ __global__ __launch_bounds__(256) void mla_prepare_kernel(const bf16_t* __restri
       unpack8(ldg16(kvw + lane * 8), g);
 #pragma unroll
       for (int i = 0; i < 8; ++i) f[i] = g[i] * rbf(f[i] * rs);
+      // a position outside [0, cap) would land in another row's slots: skip it and flag
+      if (pos[b] < 0 || pos[b] >= cap[b]) {
+        if (lane == 0 && status) atomicOr(status, DSV2_DEVERR_CACHE_FULL);
+        continue;
+      }
       bf16_t* crow = cache + (base[b] + pos[b]) * kRow;
       *reinterpret_cast<uint4*>(crow + lane * 8) = pack8(f);
       if (lane < 32) rope_pair(q + 3584, cs, sn, crow + kLat, lane);
@@ -102,10 +108,10 @@ __global__ __launch_bounds__(256) void mla_prepare_kernel(const bf16_t* __restri
 }
 
 extern "C" int dsv2_mla_prepare(const void* qkva, int64_t qkva_stride, int rows, const int32_t* pos,
-                                const int64_t* base, const void* kv_norm_w, float eps, const void* rope_cos,
-                                const void* rope_sin, int max_pos, const void* w_ukt, void* cache, void* q_out,
-                                void* stream) {
-  DSV2_REQUIRE(qkva && pos && base && kv_norm_w && rope_cos && rope_sin && cache && q_out, DSV2_E_NULL,
+                                const int64_t* base, const int32_t* cap, const void* kv_norm_w, float eps,
+                                const void* rope_cos, const void* rope_sin, int max_pos, const void* w_ukt,
+                                void* cache, void* q_out, int32_t* status, void* stream) {
+  DSV2_REQUIRE(qkva && pos && base && cap && kv_norm_w && rope_cos && rope_sin && cache && q_out, DSV2_E_NULL,
                "mla_prepare: null pointer");
   DSV2_REQUIRE(rows >= 0 && rows <= 65535 && max_pos > 0 && qkva_stride >= kQkvA, DSV2_E_SHAPE,
                "mla_prepare: bad shape");
@@ -116,12 +122,12 @@ extern "C" int dsv2_mla_prepare(const void* qkva, int64_t qkva_stride, int rows,
   const dim3 grid(w_ukt ? kHeads * kLat / 64 : 1, w_ukt ? (rows + 7) / 8 : rows);
   if (w_ukt)
     hipLaunchKernelGGL(mla_prepare_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, (const bf16_t*)qkva,
-                       qkva_stride, rows, pos, base, (const bf16_t*)kv_norm_w, eps, (const bf16_t*)rope_cos,
-                       (const bf16_t*)rope_sin, max_pos, (const bf16_t*)w_ukt, (bf16_t*)cache, (bf16_t*)q_out);
+                       qkva_stride, rows, pos, base, cap, (const bf16_t*)kv_norm_w, eps, (const bf16_t*)rope_cos,
+                       (const bf16_t*)rope_sin, max_pos, (const bf16_t*)w_ukt, (bf16_t*)cache, (bf16_t*)q_out, status);
   else
     hipLaunchKernelGGL(mla_prepare_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, (const bf16_t*)qkva,
-                       qkva_stride, rows, pos, base, (const bf16_t*)kv_norm_w, eps, (const bf16_t*)rope_cos,
-                       (const bf16_t*)rope_sin, max_pos, nullptr, (bf16_t*)cache, (bf16_t*)q_out);
+                       qkva_stride, rows, pos, base, cap, (const bf16_t*)kv_norm_w, eps, (const bf16_t*)rope_cos,
+                       (const bf16_t*)rope_sin, max_pos, nullptr, (bf16_t*)cache, (bf16_t*)q_out, status);
   return dsv2_launch_status("mla_prepare");
 }
 
@@ -131,13 +137,14 @@ extern "C" int dsv2_mla_prepare(const void* qkva, int64_t qkva_stride, int rows,
 __global__ __launch_bounds__(256, 2) void mla_decode_kernel(const bf16_t* __restrict__ q,
                                                             const bf16_t* __restrict__ cache,
                                                             const int64_t* __restrict__ base,
-                                                            const int32_t* __restrict__ pos, int split_tokens,
+                                                            const int32_t* __restrict__ pos,
+                                                            const int32_t* __restrict__ cap, int split_tokens,
                                                             int max_splits, float scale_log2,
                                                             float* __restrict__ part_o, float* __restrict__ part_ml) {
   __shared__ __attribute__((aligned(16))) bf16_t lds[2][kTile * kLdsRow];
   __shared__ floatx4_t spart[4][64];  // per-wave partial S^T (one 16-token block, half of K)
   const int s = blockIdx.x, b = blockIdx.y;
-  const int len = pos[b] + 1;
+  const int len = min(pos[b] + 1, cap[b]);  // never past the row's own slots
   const int t_begin = s * split_tokens;
   if (t_begin >= len) return;
   const int t_end = min(len, t_begin + split_tokens);
@@ -275,10 +282,10 @@ __global__ __launch_bounds__(256, 2) void mla_decode_kernel(const bf16_t* __rest
   }
 }
 
-extern "C" int dsv2_mla_decode(const void* q, const void* cache, const int64_t* base, const int32_t* pos, int rows,
-                               int split_tokens, int max_splits, float softmax_scale, float* part_o, float* part_ml,
-                               void* stream) {
-  DSV2_REQUIRE(q && cache && base && pos && part_o && part_ml, DSV2_E_NULL, "mla_decode: null pointer");
+extern "C" int dsv2_mla_decode(const void* q, const void* cache, const int64_t* base, const int32_t* pos,
+                               const int32_t* cap, int rows, int split_tokens, int max_splits, float softmax_scale,
+                               float* part_o, float* part_ml, void* stream) {
+  DSV2_REQUIRE(q && cache && base && pos && cap && part_o && part_ml, DSV2_E_NULL, "mla_decode: null pointer");
   DSV2_REQUIRE(rows >= 0 && rows <= 65535 && split_tokens > 0 && split_tokens % kTile == 0 && max_splits > 0 &&
                    max_splits <= 64,
                DSV2_E_SHAPE, "mla_decode: bad shape (split_tokens %% 32, 1 <= max_splits <= 64)");
@@ -287,7 +294,7 @@ extern "C" int dsv2_mla_decode(const void* q, const void* cache, const int64_t* 
   if (rows == 0) return DSV2_OK;
   const float scale_log2 = softmax_scale * 1.4426950408889634f;
   hipLaunchKernelGGL(mla_decode_kernel, dim3(max_splits, rows), dim3(256), 0, (hipStream_t)stream,
-                     (const bf16_t*)q, (const bf16_t*)cache, base, pos, split_tokens, max_splits, scale_log2, part_o,
+                     (const bf16_t*)q, (const bf16_t*)cache, base, pos, cap, split_tokens, max_splits, scale_log2, part_o,
                      part_ml);
   return dsv2_launch_status("mla_decode");
 }
@@ -298,13 +305,14 @@ extern "C" int dsv2_mla_decode(const void* q, const void* cache, const int64_t* 
 template <bool UV>
 __global__ __launch_bounds__(256) void mla_combine_kernel(const float* __restrict__ part_o,
                                                           const float* __restrict__ part_ml,
-                                                          const int32_t* __restrict__ pos, int split_tokens,
+                                                          const int32_t* __restrict__ pos,
+                                                          const int32_t* __restrict__ cap, int split_tokens,
                                                           int max_splits, const bf16_t* __restrict__ w_uv,
                                                           bf16_t* __restrict__ out, int64_t os) {
   __shared__ float olat[kLat];
   __shared__ float wsp[64];
   const int b = blockIdx.x, h = blockIdx.y, part = blockIdx.z, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int len = pos[b] + 1;
+  const int len = min(pos[b] + 1, cap[b]);  // the tokens dsv2_mla_decode attended
   const int ns = min((len + split_tokens - 1) / split_tokens, max_splits);
   // W_UV rows of this workgroup (part*32 + wv*8 .. +8) are requested before the merge
   uint4 wr[8];
@@ -364,10 +372,10 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(const float* __restric
   if (lane == 0) *reinterpret_cast<uint4*>(out + b * os + h * 128 + part * 32 + wv * 8) = pack8(r);
 }
 
-extern "C" int dsv2_mla_combine(const float* part_o, const float* part_ml, const int32_t* pos, int rows,
-                                int split_tokens, int max_splits, const void* w_uv, void* out, int64_t out_stride,
-                                void* stream) {
-  DSV2_REQUIRE(part_o && part_ml && pos && out, DSV2_E_NULL, "mla_combine: null pointer");
+extern "C" int dsv2_mla_combine(const float* part_o, const float* part_ml, const int32_t* pos, const int32_t* cap,
+                                int rows, int split_tokens, int max_splits, const void* w_uv, void* out,
+                                int64_t out_stride, void* stream) {
+  DSV2_REQUIRE(part_o && part_ml && pos && cap && out, DSV2_E_NULL, "mla_combine: null pointer");
   DSV2_REQUIRE(rows >= 0 && rows <= 65535 && split_tokens > 0 && max_splits > 0 && max_splits <= 64, DSV2_E_SHAPE,
                "mla_combine: bad shape");
   DSV2_REQUIRE(out_stride % 8 == 0 && dsv2_aligned16(out) && (!w_uv || dsv2_aligned16(w_uv)), DSV2_E_ALIGN,
@@ -375,9 +383,9 @@ extern "C" int dsv2_mla_combine(const float* part_o, const float* part_ml, const
   if (rows == 0) return DSV2_OK;
   if (w_uv)
     hipLaunchKernelGGL(mla_combine_kernel<true>, dim3(rows, kHeads, 4), dim3(256), 0, (hipStream_t)stream, part_o,
-                       part_ml, pos, split_tokens, max_splits, (const bf16_t*)w_uv, (bf16_t*)out, out_stride);
+                       part_ml, pos, cap, split_tokens, max_splits, (const bf16_t*)w_uv, (bf16_t*)out, out_stride);
   else
     hipLaunchKernelGGL(mla_combine_kernel<false>, dim3(rows, kHeads), dim3(256), 0, (hipStream_t)stream, part_o,
-                       part_ml, pos, split_tokens, max_splits, nullptr, (bf16_t*)out, out_stride);
+                       part_ml, pos, cap, split_tokens, max_splits, nullptr, (bf16_t*)out, out_stride);
   return dsv2_launch_status("mla_combine");
 }

@@ -21,12 +21,14 @@ constexpr int kRow = 576, kLat = 512, kWaves = 16, kBatch = 4;
 __global__ __launch_bounds__(1024) void mla_fused_kernel(const bf16_t* __restrict__ qkva, int64_t qs,
                                                          const int32_t* __restrict__ pos,
                                                          const int64_t* __restrict__ base,
+                                                         const int32_t* __restrict__ cap,
                                                          const bf16_t* __restrict__ kvw, float eps,
                                                          const bf16_t* __restrict__ cosT,
                                                          const bf16_t* __restrict__ sinT, int max_pos,
                                                          const bf16_t* __restrict__ w_ukt,
                                                          const bf16_t* __restrict__ w_uv, bf16_t* __restrict__ cache,
-                                                         float scale_log2, bf16_t* __restrict__ out, int64_t os) {
+                                                         float scale_log2, bf16_t* __restrict__ out, int64_t os,
+                                                         int32_t* __restrict__ status) {
   __shared__ float qv[kRow];    // q_lat (bf16-rounded) | rotated q_pe
   __shared__ float nrow[kRow];  // the new token's cache row
   __shared__ float wm[kWaves], wl[kWaves];
@@ -34,8 +36,12 @@ __global__ __launch_bounds__(1024) void mla_fused_kernel(const bf16_t* __restric
   __shared__ float olat[kLat];
   const int b = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const bf16_t* q = qkva + b * qs;
-  const int p = pos[b];
-  const int pc = p < 0 ? 0 : (p >= max_pos ? max_pos - 1 : p);
+  // the new token goes to slot pos; the row owns slots [0, cap): a position at or past cap
+  // attends the cap cached rows, is not stored, and sets DSV2_DEVERR_CACHE_FULL
+  const int pr = pos[b], cp = cap[b];
+  const bool fits = pr >= 0 && pr < cp;
+  const int p = pr < 0 ? 0 : (pr > cp ? cp : pr);  // cached rows read: [0, p)
+  const int pc = p >= max_pos ? max_pos - 1 : p;
   const bf16_t* cs = cosT + (int64_t)pc * 64;
   const bf16_t* sn = sinT + (int64_t)pc * 64;
   const bf16_t* crow0 = cache + base[b] * kRow;
@@ -110,13 +116,15 @@ __global__ __launch_bounds__(1024) void mla_fused_kernel(const bf16_t* __restric
       nrow[lane * 8 + i] = f[i];
     }
     bf16_t* crow = cache + (base[b] + p) * kRow;
-    if (h == 0) *reinterpret_cast<uint4*>(crow + lane * 8) = pack8(f);
+    const bool store = h == 0 && fits;
+    if (h == 0 && !fits && lane == 0 && status) atomicOr(status, DSV2_DEVERR_CACHE_FULL);
+    if (store) *reinterpret_cast<uint4*>(crow + lane * 8) = pack8(f);
     if (lane < 32) {
       const float v0 = rbf(re * c0 - ro * s0);
       const float v1 = rbf(ro * c1 + re * s1);
       nrow[kLat + lane] = v0;
       nrow[kLat + 32 + lane] = v1;
-      if (h == 0) {
+      if (store) {
         crow[kLat + lane] = f2bf(v0);
         crow[kLat + 32 + lane] = f2bf(v1);
       }
@@ -231,10 +239,12 @@ __global__ __launch_bounds__(1024) void mla_fused_kernel(const bf16_t* __restric
 }
 
 extern "C" int dsv2_mla_fused(const void* qkva, int64_t qkva_stride, int rows, const int32_t* pos,
-                              const int64_t* base, const void* kv_norm_w, float eps, const void* rope_cos,
-                              const void* rope_sin, int max_pos, const void* w_ukt, const void* w_uv, void* cache,
-                              float softmax_scale, void* out, int64_t out_stride, void* stream) {
-  DSV2_REQUIRE(qkva && pos && base && kv_norm_w && rope_cos && rope_sin && w_ukt && w_uv && cache && out, DSV2_E_NULL,
+                              const int64_t* base, const int32_t* cap, const void* kv_norm_w, float eps,
+                              const void* rope_cos, const void* rope_sin, int max_pos, const void* w_ukt,
+                              const void* w_uv, void* cache, float softmax_scale, void* out, int64_t out_stride,
+                              int32_t* status, void* stream) {
+  DSV2_REQUIRE(qkva && pos && base && cap && kv_norm_w && rope_cos && rope_sin && w_ukt && w_uv && cache && out,
+               DSV2_E_NULL,
                "mla_fused: null pointer");
   DSV2_REQUIRE(rows >= 0 && rows <= 65535 && max_pos > 0 && qkva_stride >= 3648, DSV2_E_SHAPE,
                "mla_fused: bad shape");
@@ -243,8 +253,8 @@ extern "C" int dsv2_mla_fused(const void* qkva, int64_t qkva_stride, int rows, c
                DSV2_E_ALIGN, "mla_fused: alignment");
   if (rows == 0) return DSV2_OK;
   hipLaunchKernelGGL(mla_fused_kernel, dim3(rows, 16), dim3(1024), 0, (hipStream_t)stream, (const bf16_t*)qkva,
-                     qkva_stride, pos, base, (const bf16_t*)kv_norm_w, eps, (const bf16_t*)rope_cos,
+                     qkva_stride, pos, base, cap, (const bf16_t*)kv_norm_w, eps, (const bf16_t*)rope_cos,
                      (const bf16_t*)rope_sin, max_pos, (const bf16_t*)w_ukt, (const bf16_t*)w_uv, (bf16_t*)cache,
-                     softmax_scale * 1.4426950408889634f, (bf16_t*)out, out_stride);
+                     softmax_scale * 1.4426950408889634f, (bf16_t*)out, out_stride, status);
   return dsv2_launch_status("mla_fused");
 }

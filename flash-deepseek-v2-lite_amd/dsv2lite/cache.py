@@ -10,11 +10,18 @@ the position of its next token; the decode step writes row base+pos and the
 argmax kernel advances pos.  Rows at or beyond pos are never read, so
 snapshot/restore of the prompt state (src/run.py:161-170, 212-217, 547-555) only
 saves and restores ``pos``.
+
+``cap[b]`` (int32, device) is the capacity of sequence b.  The MLA kernels store a
+new token only at 0 <= pos < cap and never read past cap; a position at or past cap
+writes nothing and sets DSV2_DEVERR_CACHE_FULL in ``status`` (int32, device), which
+``check_status`` raises on -- the reference's overflow error (src/run.py:131-134).
 """
 
 from __future__ import annotations
 
 import torch
+
+DEVERR_CACHE_FULL = 1  # DSV2_DEVERR_CACHE_FULL of include/dsv2lite.h
 
 
 class CompressedKVCache:
@@ -30,12 +37,22 @@ class CompressedKVCache:
         self.row = row
         self.data = torch.zeros(n_layers, self.total, row, dtype=torch.bfloat16, device=device)
         self.base = torch.tensor(bases, dtype=torch.int64, device=device)
+        self.cap = torch.tensor(self.capacities, dtype=torch.int32, device=device)
         self.pos = torch.zeros(len(capacities), dtype=torch.int32, device=device)
+        self.status = torch.zeros(1, dtype=torch.int32, device=device)
         self.max_capacity = max(self.capacities)
 
     @property
     def batch(self) -> int:
         return len(self.capacities)
+
+    def check_status(self) -> None:
+        """Raise if a kernel flagged a cache write past a row's capacity (synchronises)."""
+        st = int(self.status.item())
+        if st & DEVERR_CACHE_FULL:
+            self.status.zero_()
+            raise RuntimeError("KV cache capacity exhausted: a decode step reached a row's capacity "
+                               f"(capacities {self.capacities}); nothing was written past it")
 
     def layer(self, i: int) -> torch.Tensor:
         return self.data[i]

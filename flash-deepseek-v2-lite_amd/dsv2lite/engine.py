@@ -155,42 +155,44 @@ class DecodeEngine:
         self._host_pos = [0] * self.B  # host mirror of cache.pos, for capacity checks only
 
     # ------------------------------------------------------------------ layers
-    def _attention(self, L, li: int, b: RowBuffers, R: int, pos, base, family: str, st: int) -> None:
+    def _attention(self, L, li: int, b: RowBuffers, R: int, pos, base, cap, family: str, st: int) -> None:
         c = self.cfg
         cache = self.cache.layer(li)
         if family == "small" and self.fused_mla and b is self.buf:
             call("dsv2_gemv_bf16", ptr(b.h), c.hidden, R, c.hidden, ptr(L.w_qkva), c.qkva_dim, ptr(L.ln_in), c.eps,
                  None, 0, ptr(b.qkva), c.qkva_dim, 0, st)
-            call("dsv2_mla_fused", ptr(b.qkva), c.qkva_dim, R, ptr(pos), ptr(base), ptr(L.kv_norm), c.eps,
-                 ptr(self.cos), ptr(self.sin), self.max_pos, ptr(L.w_ukt), ptr(L.w_uv), ptr(cache), self.scale,
-                 ptr(b.attn), c.hidden, st)
+            call("dsv2_mla_fused", ptr(b.qkva), c.qkva_dim, R, ptr(pos), ptr(base), ptr(cap), ptr(L.kv_norm),
+                 c.eps, ptr(self.cos), ptr(self.sin), self.max_pos, ptr(L.w_ukt), ptr(L.w_uv), ptr(cache),
+                 self.scale, ptr(b.attn), c.hidden, ptr(self.cache.status), st)
             call("dsv2_gemv_bf16", ptr(b.attn), c.hidden, R, c.hidden, ptr(L.w_o), c.hidden, None, 0.0, ptr(b.h),
                  c.hidden, ptr(b.h), c.hidden, 0, st)
             return
         if family == "small":
             call("dsv2_gemv_bf16", ptr(b.h), c.hidden, R, c.hidden, ptr(L.w_qkva), c.qkva_dim, ptr(L.ln_in), c.eps,
                  None, 0, ptr(b.qkva), c.qkva_dim, 0, st)
-            call("dsv2_mla_prepare", ptr(b.qkva), c.qkva_dim, R, ptr(pos), ptr(base), ptr(L.kv_norm), c.eps,
-                 ptr(self.cos), ptr(self.sin), self.max_pos, ptr(L.w_ukt), ptr(cache), ptr(b.q), st)
+            call("dsv2_mla_prepare", ptr(b.qkva), c.qkva_dim, R, ptr(pos), ptr(base), ptr(cap), ptr(L.kv_norm),
+                 c.eps, ptr(self.cos), ptr(self.sin), self.max_pos, ptr(L.w_ukt), ptr(cache), ptr(b.q),
+                 ptr(self.cache.status), st)
         else:
             call("dsv2_gemm_bf16", ptr(b.xn), c.hidden, 0, R, c.hidden, ptr(L.w_qkva), 0, c.qkva_dim, 1, None, 0,
                  ptr(b.qkva), c.qkva_dim, 0, 0, st)
-            call("dsv2_mla_prepare", ptr(b.qkva), c.qkva_dim, R, ptr(pos), ptr(base), ptr(L.kv_norm), c.eps,
-                 ptr(self.cos), ptr(self.sin), self.max_pos, None, ptr(cache), ptr(b.q), st)
+            call("dsv2_mla_prepare", ptr(b.qkva), c.qkva_dim, R, ptr(pos), ptr(base), ptr(cap), ptr(L.kv_norm),
+                 c.eps, ptr(self.cos), ptr(self.sin), self.max_pos, None, ptr(cache), ptr(b.q),
+                 ptr(self.cache.status), st)
             # q_lat[r, h, :512] = W_UK_h^T q_nope[r, h]: 16 head groups, K = 128
             call("dsv2_gemm_bf16", ptr(b.qkva), c.qkva_dim, c.q_head, R, c.qk_nope, ptr(L.w_ukt),
                  c.kv_rank * c.qk_nope, c.kv_rank, c.n_heads, None, 0, ptr(b.q), c.n_heads * c.cache_row,
                  c.cache_row, 0, st)
-        call("dsv2_mla_decode", ptr(b.q), ptr(cache), ptr(base), ptr(pos), R, b.split_tokens, b.max_splits,
-             self.scale, ptr(b.part_o), ptr(b.part_ml), st)
+        call("dsv2_mla_decode", ptr(b.q), ptr(cache), ptr(base), ptr(pos), ptr(cap), R, b.split_tokens,
+             b.max_splits, self.scale, ptr(b.part_o), ptr(b.part_ml), st)
         if family == "small":
-            call("dsv2_mla_combine", ptr(b.part_o), ptr(b.part_ml), ptr(pos), R, b.split_tokens, b.max_splits,
-                 ptr(L.w_uv), ptr(b.attn), c.hidden, st)
+            call("dsv2_mla_combine", ptr(b.part_o), ptr(b.part_ml), ptr(pos), ptr(cap), R, b.split_tokens,
+                 b.max_splits, ptr(L.w_uv), ptr(b.attn), c.hidden, st)
             call("dsv2_gemv_bf16", ptr(b.attn), c.hidden, R, c.hidden, ptr(L.w_o), c.hidden, None, 0.0, ptr(b.h),
                  c.hidden, ptr(b.h), c.hidden, 0, st)
         else:
-            call("dsv2_mla_combine", ptr(b.part_o), ptr(b.part_ml), ptr(pos), R, b.split_tokens, b.max_splits,
-                 None, ptr(b.olat), c.n_heads * c.kv_rank, st)
+            call("dsv2_mla_combine", ptr(b.part_o), ptr(b.part_ml), ptr(pos), ptr(cap), R, b.split_tokens,
+                 b.max_splits, None, ptr(b.olat), c.n_heads * c.kv_rank, st)
             # attn[r, h*128 + i] = W_UV_h o_lat[r, h]: 16 head groups, K = 512
             call("dsv2_gemm_bf16", ptr(b.olat), c.n_heads * c.kv_rank, c.kv_rank, R, c.kv_rank, ptr(L.w_uv),
                  c.v_dim * c.kv_rank, c.v_dim, c.n_heads, None, 0, ptr(b.attn), c.hidden, c.v_dim, 0, st)
@@ -254,8 +256,12 @@ class DecodeEngine:
                  H, ptr(b.h), H, 0, 0, st)
             call("dsv2_rmsnorm_bf16", ptr(b.h), H, ptr(next_norm), ptr(b.xn), H, R, H, c.eps, st)
 
-    def _layers(self, b: RowBuffers, R: int, ids: torch.Tensor, pos, base, family: str, st: int,
-                record: list | None = None) -> None:
+    def _layers(self, b: RowBuffers, R: int, ids: torch.Tensor, pos, base, cap, family: str, st: int,
+                record: list | None = None, rows: torch.Tensor | None = None) -> None:
+        """Enqueue the embedding gather and every layer for R kernel rows.  With `record`,
+        append per layer ("attn", li, h), ("layer", li, h) and ("router", li, ids, weights)
+        copies of the rows `rows` (device index tensor; all R rows when None)."""
+        sel = (lambda t: t[:R].clone()) if rows is None else (lambda t: t.index_select(0, rows))
         c = self.cfg
         call("dsv2_embed_gather_bf16", ptr(ids), ptr(self.w.embed), c.hidden, ptr(b.h), R, st)
         if family == "batch":
@@ -263,15 +269,15 @@ class DecodeEngine:
                  c.hidden, c.eps, st)
         n = len(self.w.layers)
         for li, L in enumerate(self.w.layers):
-            self._attention(L, li, b, R, pos, base, family, st)
+            self._attention(L, li, b, R, pos, base, cap, family, st)
             if record is not None:
-                record.append(("attn", li, b.h[:R].clone()))
+                record.append(("attn", li, sel(b.h)))
             next_norm = self.w.layers[li + 1].ln_in if li + 1 < n else self.w.norm
             self._mlp(L, li, b, R, family, next_norm, st)
             if record is not None:
-                record.append(("layer", li, b.h[:R].clone()))
+                record.append(("layer", li, sel(b.h)))
                 if L.moe:
-                    record.append(("router", li, b.ids32[:R].clone(), b.wts[:R].clone()))
+                    record.append(("router", li, sel(b.ids32), sel(b.wts)))
 
     def _head(self, b: RowBuffers, family: str, st: int, pos) -> None:
         c = self.cfg
@@ -292,10 +298,10 @@ class DecodeEngine:
     def step(self, record: list | None = None) -> None:
         """Enqueue one decode step for all rows: reads self.ids, writes self.logits and the
         next ids into self.ids, advances cache.pos.  No host synchronisation."""
-        if max(p + 1 for p in self._host_pos) > self.max_pos:
-            raise RuntimeError("KV cache capacity exhausted")
+        self._check_room()
         st = _hip.stream_ptr(self.device)
-        self._layers(self.buf, self.B, self.ids, self.cache.pos, self.cache.base, self.family, st, record)
+        self._layers(self.buf, self.B, self.ids, self.cache.pos, self.cache.base, self.cache.cap, self.family, st,
+                     record)
         self._head(self.buf, self.family, st, self.cache.pos)
         self._host_pos = [p + 1 for p in self._host_pos]
 
@@ -303,7 +309,9 @@ class DecodeEngine:
         """Eager prefill of one prompt per row (batch-family kernels, one kernel row per
         prompt token, chunks of <= max_prefill_rows rows in sequence order).  Writes the
         compressed cache, sets cache.pos = prompt lengths and self.ids = greedy first
-        tokens (returned).  Mirrors _prefill_once (src/run.py:526-544)."""
+        tokens (returned).  Mirrors _prefill_once (src/run.py:526-544).  With `record`, it
+        receives the per-layer records of each sequence's LAST prompt token, in the format of
+        a recorded decode step (row b = sequence b)."""
         if len(prompts) != self.B:
             raise ValueError(f"need {self.B} prompts, got {len(prompts)}")
         lens = [int(p.numel()) for p in prompts]
@@ -317,25 +325,36 @@ class DecodeEngine:
         posv = torch.cat([torch.arange(n, dtype=torch.int32) for n in lens])
         ids_all = torch.cat([p.reshape(-1).to(torch.int64).cpu() for p in prompts])
         base_all = self.cache.base.cpu()[seq]
+        cap_all = self.cache.cap.cpu()[seq]
         total = seq.numel()
         max_rows = min(self.max_prefill_rows, total)
         pb = RowBuffers(self.cfg, max_rows, "batch", self.max_pos, dev)
         last_h = torch.empty(self.B, self.cfg.hidden, dtype=BF16, device=dev)
         last_xn = torch.empty_like(last_h)
         st = _hip.stream_ptr(dev)
+        acc: dict = {}
         for s in range(0, total, max_rows):
             e = min(total, s + max_rows)
             R = e - s
             ids_c = ids_all[s:e].to(dev)
             pos_c = posv[s:e].to(dev)
             base_c = base_all[s:e].to(dev)
-            self._layers(pb, R, ids_c, pos_c, base_c, "batch", st, record)
+            cap_c = cap_all[s:e].to(dev)
             is_last = (posv[s:e] + 1) == torch.tensor(lens)[seq[s:e]]
             rows = torch.nonzero(is_last).flatten()
+            rows_d = rows.to(dev)
+            which = seq[s:e][rows].to(dev)
+            crec = [] if record is not None else None
+            self._layers(pb, R, ids_c, pos_c, base_c, cap_c, "batch", st, crec, rows_d)
+            for r in crec or ():
+                for j, t in enumerate(r[2:]):  # scatter the last-token rows to their sequences
+                    key = (r[0], r[1], j)
+                    if key not in acc:
+                        acc[key] = torch.zeros((self.B,) + tuple(t.shape[1:]), dtype=t.dtype, device=dev)
+                    acc[key].index_copy_(0, which, t)
             if rows.numel():
-                which = seq[s:e][rows].to(dev)
-                last_h.index_copy_(0, which, pb.h[rows.to(dev)])
-                last_xn.index_copy_(0, which, pb.xn[rows.to(dev)])
+                last_h.index_copy_(0, which, pb.h[rows_d])
+                last_xn.index_copy_(0, which, pb.xn[rows_d])
         # final norm is fused into the last layer's combine (pb.xn); lm_head + argmax
         c = self.cfg
         call("dsv2_gemm_bf16", ptr(last_xn), c.hidden, 0, self.B, c.hidden, ptr(self.w.lm_head), 0, c.vocab, 1, None,
@@ -343,6 +362,10 @@ class DecodeEngine:
         call("dsv2_argmax_f32", ptr(self.logits), self.B, c.vocab, ptr(self.ids), None, st)
         self.cache.pos.copy_(torch.tensor(lens, dtype=torch.int32))
         self._host_pos = list(lens)
+        if record is not None:
+            for (kind, li, j) in sorted(acc, key=lambda k: (k[1], ("attn", "layer", "router").index(k[0]), k[2])):
+                if j == 0:
+                    record.append((kind, li) + tuple(acc[(kind, li, jj)] for jj in range(3) if (kind, li, jj) in acc))
         self.buf.h.copy_(last_h)
         del pb
         return self.ids
@@ -387,13 +410,23 @@ class DecodeEngine:
         return g
 
     def check_errors(self) -> None:
-        """Raise if a kernel of the step reported a device-side failure (synchronises)."""
-        return None
+        """Raise if a kernel of the steps so far skipped a cache write past a row's capacity
+        (the device status word of the cache; synchronises).  step()/replay() refuse such a
+        step on the host first, so this fires only when pos was changed behind their back."""
+        self.cache.check_status()
+
+    def _check_room(self) -> None:
+        """Every row needs a free slot for its next token: pos[b] + 1 <= capacity[b]
+        (the reference raises on overflow, src/run.py:131-134)."""
+        full = [b for b, (p, c) in enumerate(zip(self._host_pos, self.cache.capacities)) if p + 1 > c]
+        if full:
+            raise RuntimeError(f"KV cache capacity exhausted for rows {full[:8]} "
+                               f"(positions {[self._host_pos[b] for b in full[:8]]}, "
+                               f"capacities {[self.cache.capacities[b] for b in full[:8]]})")
 
     def replay(self) -> None:
         if self.graph is None:
             raise RuntimeError("capture() first")
-        if max(p + 1 for p in self._host_pos) > self.max_pos:
-            raise RuntimeError("KV cache capacity exhausted")
+        self._check_room()
         self.graph.replay()
         self._host_pos = [p + 1 for p in self._host_pos]

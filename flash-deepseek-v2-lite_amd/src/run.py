@@ -107,6 +107,8 @@ def make_prompts(args: argparse.Namespace, batch_size: int, vocab: int) -> list[
         return [torch.randint(0, vocab, (n,), generator=g) for n in lens]
     if args.prompt_len <= 0:
         raise ValueError("prompt length must be positive")
+    if not getattr(args, "replicate", True):  # one prompt per row (benchmark config 3)
+        return [torch.randint(0, vocab, (args.prompt_len,), generator=g) for _ in range(batch_size)]
     one = torch.randint(0, vocab, (args.prompt_len,), generator=g)
     return [one.clone() for _ in range(batch_size)]
 

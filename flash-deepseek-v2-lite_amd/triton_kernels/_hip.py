@@ -15,7 +15,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libdsv2lite_hip.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 LINEAR_SWIGLU = 1
 LINEAR_OUT_F32 = 2
@@ -30,20 +30,24 @@ _SIGS = {
     "dsv2_last_error_message": ([], ctypes.c_char_p),
     "dsv2_rmsnorm_bf16": ([_p, _i64, _p, _p, _i64, _i32, _i32, _f32, _p], _i32),
     "dsv2_residual_add_bf16": ([_p, _p, _p, _i64, _p], _i32),
+    "dsv2_residual_add_f16": ([_p, _p, _p, _i64, _p], _i32),
     "dsv2_silu_mul_bf16": ([_p, _p, _p, _i64, _p], _i32),
-    "dsv2_prepare_decode_inputs": ([_p, _p, _p, _i32, _i32, _p], _i32),
-    "dsv2_copy_token_rows": ([_p, _i64, _p, _i64, _i64, _p, _i32, _p], _i32),
-    "dsv2_fill_positions": ([_p, _p, _p, _i64, _i32, _p], _i32),
+    "dsv2_prepare_decode_inputs": ([_p, _p, _p, _p, _i32, _i32, _p], _i32),
+    "dsv2_copy_token_rows": ([_p, _i64, _p, _i64, _i64, _p, _i64, _i32, _p, _p], _i32),
+    "dsv2_fill_positions": ([_p, _p, _p, _p, _i64, _i32, _p], _i32),
     "dsv2_embed_gather_bf16": ([_p, _p, _i32, _p, _i32, _p], _i32),
     "dsv2_argmax_f32": ([_p, _i32, _i32, _p, _p, _p], _i32),
     "dsv2_gemv_bf16": ([_p, _i64, _i32, _i32, _p, _i32, _p, _f32, _p, _i64, _p, _i64, _i32, _p], _i32),
     "dsv2_lm_head_argmax_workspace_size": ([_i32], _i64),
     "dsv2_lm_head_argmax_bf16": ([_p, _i64, _i32, _p, _i32, _p, _f32, _p, _p, _i64, _p, _p, _p], _i32),
     "dsv2_gemm_bf16": ([_p, _i64, _i64, _i32, _i32, _p, _i64, _i32, _i32, _p, _i64, _p, _i64, _i64, _i32, _p], _i32),
-    "dsv2_mla_prepare": ([_p, _i64, _i32, _p, _p, _p, _f32, _p, _p, _i32, _p, _p, _p, _p], _i32),
-    "dsv2_mla_decode": ([_p, _p, _p, _p, _i32, _i32, _i32, _f32, _p, _p, _p], _i32),
-    "dsv2_mla_combine": ([_p, _p, _p, _i32, _i32, _i32, _p, _p, _i64, _p], _i32),
-    "dsv2_mla_fused": ([_p, _i64, _i32, _p, _p, _p, _f32, _p, _p, _i32, _p, _p, _p, _f32, _p, _i64, _p], _i32),
+    "dsv2_mla_prepare": ([_p, _i64, _i32, _p, _p, _p, _p, _f32, _p, _p, _i32, _p, _p, _p, _p, _p], _i32),
+    "dsv2_mla_decode": ([_p, _p, _p, _p, _p, _i32, _i32, _i32, _f32, _p, _p, _p], _i32),
+    "dsv2_mla_combine": ([_p, _p, _p, _p, _i32, _i32, _i32, _p, _p, _i64, _p], _i32),
+    "dsv2_mla_fused": ([_p, _i64, _i32, _p, _p, _p, _p, _f32, _p, _p, _i32, _p, _p, _p, _f32, _p, _i64, _p, _p],
+                       _i32),
+    "dsv2_attention_decode_expanded": ([_p, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64,
+                                        _i32, _i32, _i32, _i32, _i32, _p, _f32, _p, _p], _i32),
     "dsv2_router_logits": ([_p, _i64, _p, _f32, _p, _i32, _p, _p, _p], _i32),
     "dsv2_moe_route_gateup_logits": ([_p, _i32, _p, _f32, _p, _p, _p, _p, _i32, _p, _p], _i32),
     "dsv2_router_topk6": ([_p, _i64, _p, _f32, _p, _f32, _i32, _p, _p, _p, _p, _p], _i32),

@@ -65,6 +65,59 @@ def plan_splits(rows: int, max_ctx: int, target_wgs: int = 256) -> tuple[int, in
     return split, math.ceil(max_ctx / split)
 
 
+# the small family runs the fused one-launch MLA while the cache is this short, like the
+# engine (dsv2lite.engine.FUSED_MLA_MAX_CTX); longer caches take the split-KV decode
+FUSED_MAX_CTX = 2048
+
+
+@dataclass
+class AttentionDecodeWorkspace:
+    """Per-(device, B, L) buffers of one attention call, cached on the packed weights like
+    the reference's workspace (attention_decode_batch.py:641-669); the returned output
+    aliases ``out`` and is overwritten by the next call with the same key."""
+
+    pos: torch.Tensor      # [B] int32
+    base: torch.Tensor     # [B] int64
+    cap: torch.Tensor      # [B] int32
+    status: torch.Tensor   # [1] int32: DSV2_DEVERR_* bits of every call so far
+    qkva: torch.Tensor     # [B, 3648]
+    q: torch.Tensor        # [B, 16, 576]
+    split: int
+    nsplit: int
+    part_o: torch.Tensor   # [B, nsplit, 16, 512] fp32
+    part_ml: torch.Tensor  # [B, nsplit, 16, 2] fp32
+    olat: torch.Tensor     # [B, 16, 512]
+    attn: torch.Tensor     # [B, 2048]
+    out: torch.Tensor      # [B, 1, 2048]
+
+
+def _workspace(packed: AttentionPackedWeights, dev: torch.device, B: int, L: int) -> AttentionDecodeWorkspace:
+    key = (dev.index if dev.index is not None else 0, B, L)
+    cache = packed.__dict__.setdefault("workspace_by_key", {})
+    ws = cache.get(key)
+    if ws is None:
+        e = lambda *shape, dt=torch.bfloat16: torch.empty(*shape, dtype=dt, device=dev)  # noqa: E731
+        split, nsplit = plan_splits(B, L)
+        ws = AttentionDecodeWorkspace(
+            pos=e(B, dt=torch.int32), base=e(B, dt=torch.int64), cap=e(B, dt=torch.int32),
+            status=torch.zeros(1, dtype=torch.int32, device=dev), qkva=e(B, QKVA), q=e(B, NH, ROW), split=split,
+            nsplit=nsplit, part_o=e(B, nsplit, NH, LAT, dt=torch.float32), part_ml=e(B, nsplit, NH, 2, dt=torch.float32),
+            olat=e(B, NH, LAT), attn=e(B, HID), out=e(B, 1, HID))
+        cache[key] = ws
+    return ws
+
+
+def check_cache_status(packed: AttentionPackedWeights) -> None:
+    """Raise if an attention call on these weights tried to write its new token at or past
+    the cache length L (nothing was written there; synchronises).  The reference raises on
+    a cache overflow (src/run.py:131-134)."""
+    for ws in packed.__dict__.get("workspace_by_key", {}).values():
+        if int(ws.status.item()) & 1:  # DSV2_DEVERR_CACHE_FULL
+            ws.status.zero_()
+            raise RuntimeError("attention decode: cache_position reached the cache length; the new token was not "
+                               "written")
+
+
 def _attention_decode(family: str, hidden_states, cos, sin, position_ids, cache_position, key_cache, value_cache,
                       packed: AttentionPackedWeights, softmax_scale: float) -> torch.Tensor:
     name = f"attention_decode[{family}]"
@@ -88,48 +141,98 @@ def _attention_decode(family: str, hidden_states, cos, sin, position_ids, cache_
     cos2, sin2 = cos.reshape(-1, ROPE), sin.reshape(-1, ROPE)
     max_pos = min(cos2.shape[0], L)
     x = hidden_states.reshape(B, HID).contiguous()
-    pos = torch.empty(B, dtype=torch.int32, device=dev)
-    base = torch.empty(B, dtype=torch.int64, device=dev)
-    qkva = torch.empty(B, QKVA, dtype=torch.bfloat16, device=dev)
-    q = torch.empty(B, NH, ROW, dtype=torch.bfloat16, device=dev)
-    split, nsplit = plan_splits(B, L)
-    part_o = torch.empty(B, nsplit, NH, LAT, dtype=torch.float32, device=dev)
-    part_ml = torch.empty(B, nsplit, NH, 2, dtype=torch.float32, device=dev)
-    attn = torch.empty(B, HID, dtype=torch.bfloat16, device=dev)
-    out = torch.empty(B, HID, dtype=torch.bfloat16, device=dev)
+    ws = _workspace(packed, dev, B, L)
+    attn2, out2 = ws.attn, ws.out.view(B, HID)
     st = _hip.stream_ptr(dev)
     call = _hip.call
-    call("dsv2_fill_positions", cache_position.data_ptr(), pos.data_ptr(), base.data_ptr(), L, B, st)
+    P = lambda t: t.data_ptr()  # noqa: E731
+    call("dsv2_fill_positions", P(cache_position), P(ws.pos), P(ws.base), P(ws.cap), L, B, st)
     if family == "small":
-        call("dsv2_gemv_bf16", x.data_ptr(), HID, B, HID, packed.w_qkva.data_ptr(), QKVA, None, 0.0, None, 0,
-             qkva.data_ptr(), QKVA, 0, st)
-        call("dsv2_mla_prepare", qkva.data_ptr(), QKVA, B, pos.data_ptr(), base.data_ptr(),
-             packed.kv_norm_weight.data_ptr(), packed.kv_norm_eps, cos2.data_ptr(), sin2.data_ptr(), max_pos,
-             packed.w_ukt.data_ptr(), key_cache.data_ptr(), q.data_ptr(), st)
-    else:
-        call("dsv2_gemm_bf16", x.data_ptr(), HID, 0, B, HID, packed.w_qkva.data_ptr(), 0, QKVA, 1, None, 0,
-             qkva.data_ptr(), QKVA, 0, 0, st)
-        call("dsv2_mla_prepare", qkva.data_ptr(), QKVA, B, pos.data_ptr(), base.data_ptr(),
-             packed.kv_norm_weight.data_ptr(), packed.kv_norm_eps, cos2.data_ptr(), sin2.data_ptr(), max_pos, None,
-             key_cache.data_ptr(), q.data_ptr(), st)
-        call("dsv2_gemm_bf16", qkva.data_ptr(), QKVA, NOPE + ROPE, B, NOPE, packed.w_ukt.data_ptr(), LAT * NOPE, LAT,
-             NH, None, 0, q.data_ptr(), NH * ROW, ROW, 0, st)
-    call("dsv2_mla_decode", q.data_ptr(), key_cache.data_ptr(), base.data_ptr(), pos.data_ptr(), B, split, nsplit,
-         float(softmax_scale), part_o.data_ptr(), part_ml.data_ptr(), st)
-    if family == "small":
-        call("dsv2_mla_combine", part_o.data_ptr(), part_ml.data_ptr(), pos.data_ptr(), B, split, nsplit,
-             packed.w_uv.data_ptr(), attn.data_ptr(), HID, st)
-        call("dsv2_gemv_bf16", attn.data_ptr(), HID, B, HID, packed.w_o.data_ptr(), HID, None, 0.0, None, 0,
-             out.data_ptr(), HID, 0, st)
-    else:
-        olat = torch.empty(B, NH, LAT, dtype=torch.bfloat16, device=dev)
-        call("dsv2_mla_combine", part_o.data_ptr(), part_ml.data_ptr(), pos.data_ptr(), B, split, nsplit, None,
-             olat.data_ptr(), NH * LAT, st)
-        call("dsv2_gemm_bf16", olat.data_ptr(), NH * LAT, LAT, B, LAT, packed.w_uv.data_ptr(), VD * LAT, VD, NH, None,
-             0, attn.data_ptr(), HID, VD, 0, st)
-        call("dsv2_gemm_bf16", attn.data_ptr(), HID, 0, B, HID, packed.w_o.data_ptr(), 0, HID, 1, None, 0,
-             out.data_ptr(), HID, 0, 0, st)
-    return out.reshape(B, 1, HID)
+        call("dsv2_gemv_bf16", P(x), HID, B, HID, P(packed.w_qkva), QKVA, None, 0.0, None, 0, P(ws.qkva), QKVA, 0, st)
+        if L <= FUSED_MAX_CTX:
+            call("dsv2_mla_fused", P(ws.qkva), QKVA, B, P(ws.pos), P(ws.base), P(ws.cap), P(packed.kv_norm_weight),
+                 packed.kv_norm_eps, P(cos2), P(sin2), max_pos, P(packed.w_ukt), P(packed.w_uv), P(key_cache),
+                 float(softmax_scale), P(attn2), HID, P(ws.status), st)
+        else:
+            call("dsv2_mla_prepare", P(ws.qkva), QKVA, B, P(ws.pos), P(ws.base), P(ws.cap), P(packed.kv_norm_weight),
+                 packed.kv_norm_eps, P(cos2), P(sin2), max_pos, P(packed.w_ukt), P(key_cache), P(ws.q), P(ws.status),
+                 st)
+            call("dsv2_mla_decode", P(ws.q), P(key_cache), P(ws.base), P(ws.pos), P(ws.cap), B, ws.split, ws.nsplit,
+                 float(softmax_scale), P(ws.part_o), P(ws.part_ml), st)
+            call("dsv2_mla_combine", P(ws.part_o), P(ws.part_ml), P(ws.pos), P(ws.cap), B, ws.split, ws.nsplit,
+                 P(packed.w_uv), P(attn2), HID, st)
+        call("dsv2_gemv_bf16", P(attn2), HID, B, HID, P(packed.w_o), HID, None, 0.0, None, 0, P(out2), HID, 0, st)
+        return ws.out
+    call("dsv2_gemm_bf16", P(x), HID, 0, B, HID, P(packed.w_qkva), 0, QKVA, 1, None, 0, P(ws.qkva), QKVA, 0, 0, st)
+    call("dsv2_mla_prepare", P(ws.qkva), QKVA, B, P(ws.pos), P(ws.base), P(ws.cap), P(packed.kv_norm_weight),
+         packed.kv_norm_eps, P(cos2), P(sin2), max_pos, None, P(key_cache), P(ws.q), P(ws.status), st)
+    call("dsv2_gemm_bf16", P(ws.qkva), QKVA, NOPE + ROPE, B, NOPE, P(packed.w_ukt), LAT * NOPE, LAT, NH, None, 0,
+         P(ws.q), NH * ROW, ROW, 0, st)
+    call("dsv2_mla_decode", P(ws.q), P(key_cache), P(ws.base), P(ws.pos), P(ws.cap), B, ws.split, ws.nsplit,
+         float(softmax_scale), P(ws.part_o), P(ws.part_ml), st)
+    call("dsv2_mla_combine", P(ws.part_o), P(ws.part_ml), P(ws.pos), P(ws.cap), B, ws.split, ws.nsplit, None,
+         P(ws.olat), NH * LAT, st)
+    call("dsv2_gemm_bf16", P(ws.olat), NH * LAT, LAT, B, LAT, P(packed.w_uv), VD * LAT, VD, NH, None, 0, P(attn2),
+         HID, VD, 0, st)
+    call("dsv2_gemm_bf16", P(attn2), HID, 0, B, HID, P(packed.w_o), 0, HID, 1, None, 0, P(out2), HID, 0, 0, st)
+    return ws.out
+
+
+def batched_attention_decode_q1_triton(query_states: torch.Tensor, key_states: torch.Tensor,
+                                       value_states: torch.Tensor, cache_position: torch.Tensor,
+                                       softmax_scale: float) -> torch.Tensor:
+    """q_len=1 attention over an expanded per-head cache: query [B, H, 1, Dq], keys
+    [B, H, L, Dq], values [B, H, L, Dv] (bf16, last dim contiguous) -> [B, H, 1, Dv]:
+    softmax over positions 0..cache_position of scale * q.k, times v, fp32 math.  Positions
+    at or past L are not read (the reference reads them unchecked); the call then attends
+    the L rows and the overflow is reported by check_expanded_status.
+    Reference: attention_decode_batch.py:345-401."""
+    require_cuda("batched_attention_decode_q1_triton", query_states, key_states, value_states, cache_position)
+    if query_states.dtype != torch.bfloat16 or key_states.dtype != torch.bfloat16 or \
+            value_states.dtype != torch.bfloat16:
+        raise NotImplementedError("batched_attention_decode_q1_triton supports bf16 only")
+    if query_states.ndim != 4 or key_states.ndim != 4 or value_states.ndim != 4:
+        raise ValueError("query/key/value states must be rank-4 tensors")
+    if query_states.shape[2] != 1:
+        raise ValueError("batched_attention_decode_q1_triton only supports q_len=1")
+    if cache_position.numel() != 1 or cache_position.dtype != torch.long:
+        raise ValueError("cache_position must be CUDA int64 tensor with one element")
+    B, H, _, Dq = query_states.shape
+    Dv = value_states.shape[3]
+    L = key_states.shape[2]
+    if key_states.shape[:2] != (B, H) or value_states.shape[:3] != (B, H, L) or key_states.shape[3] != Dq:
+        raise ValueError("key/value states must be [B, H, L, Dq] / [B, H, L, Dv] matching the query")
+    for t in (query_states, key_states, value_states):
+        if t.stride(3) != 1:
+            raise NotImplementedError("batched_attention_decode_q1_triton needs a contiguous last dimension")
+    out = torch.empty((B, H, 1, Dv), device=query_states.device, dtype=query_states.dtype)
+    if B == 0 or L == 0:
+        return out
+    q, k, v = query_states, key_states, value_states
+    _hip.call("dsv2_attention_decode_expanded", q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0),
+              k.stride(1), k.stride(2), v.data_ptr(), v.stride(0), v.stride(1), v.stride(2), out.data_ptr(),
+              out.stride(0), out.stride(1), B, H, Dq, Dv, L, cache_position.data_ptr(), float(softmax_scale),
+              _expanded_status(q.device).data_ptr(), _hip.stream_ptr(q.device))
+    return out
+
+
+_EXPANDED_STATUS: dict = {}
+
+
+def _expanded_status(dev: torch.device) -> torch.Tensor:
+    k = dev.index if dev.index is not None else 0
+    if k not in _EXPANDED_STATUS:
+        _EXPANDED_STATUS[k] = torch.zeros(1, dtype=torch.int32, device=dev)
+    return _EXPANDED_STATUS[k]
+
+
+def check_expanded_status(device: torch.device | str = "cuda") -> None:
+    """Raise if a batched_attention_decode_q1_triton call on `device` had cache_position
+    outside [0, L) (synchronises)."""
+    st = _expanded_status(torch.device(device))
+    if int(st.item()) & 1:  # DSV2_DEVERR_CACHE_FULL
+        st.zero_()
+        raise RuntimeError("batched_attention_decode_q1_triton: cache_position outside the cache")
 
 
 def attention_decode_triton(hidden_states, cos, sin, position_ids, cache_position, key_cache, value_cache, packed,

@@ -1,12 +1,15 @@
-"""Absorbed-MLA decode attention, small family: GEMV projections, fused
-prepare (RoPE + cache write + W_UK absorption) and fused combine + W_UV
-(reference: triton_kernels/attention_decode_small.py:553-674, 932-1070).
-Same compressed-cache deviation as attention_decode_batch."""
+"""Absorbed-MLA decode attention, small family: GEMV q/kv_a and o projections around
+the one-launch fused MLA kernel (W_UK absorption, kv-norm + RoPE + cache write,
+softmax over the cached rows, W_UV) while the cache is at most 2048 tokens, else
+prepare + split-KV decode + combine with W_UV
+(reference: triton_kernels/attention_decode_small.py:553-674, 782-840, 932-1070).
+Same compressed-cache deviation as attention_decode_batch; batched_attention_decode_q1_triton
+(the expanded-cache attention) is shared with it."""
 
 from __future__ import annotations
 
 from .attention_decode_batch import (AttentionPackedWeights, _attention_decode,  # noqa: F401
-                                     pack_attention_weights)
+                                     batched_attention_decode_q1_triton, check_cache_status, pack_attention_weights)
 
 
 def attention_decode_only_triton(hidden_states, cos, sin, position_ids, cache_position, key_cache, value_cache,

@@ -125,6 +125,15 @@ def batched_grouped_routed_moe(x, topk_ids, topk_weight, packed, output_dtype=No
     return batched_grouped_routed_moe_grouped_triton(x, topk_ids, topk_weight, packed, output_dtype)
 
 
+def packed_routed_moe_eager(x: torch.Tensor, topk_ids: torch.Tensor, topk_weight: torch.Tensor,
+                            packed: PackedRoutedExperts) -> torch.Tensor:
+    """The reference's per-expert loop (moe_batch.py:366-387): fp32 weighted sum of the
+    bf16 expert outputs, one cast to x.dtype.  Kept as a name for its callers; there is no
+    eager path here, it runs the same HIP grouped kernels as packed_routed_moe (same math:
+    SwiGLU, bf16 expert output, fp32 slot-order sum)."""
+    return batched_grouped_routed_moe(x, topk_ids, topk_weight, packed)
+
+
 def packed_routed_moe(x: torch.Tensor, topk_ids: torch.Tensor, topk_weight: torch.Tensor,
                       packed: PackedRoutedExperts, output_dtype: torch.dtype | None = None) -> torch.Tensor:
     return batched_grouped_routed_moe(x, topk_ids, topk_weight, packed, output_dtype=output_dtype)

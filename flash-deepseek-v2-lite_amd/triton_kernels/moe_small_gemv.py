@@ -7,7 +7,7 @@ from __future__ import annotations
 import torch
 
 from . import _hip
-from .moe_batch import PackedRoutedExperts, _check, pack_routed_experts  # noqa: F401
+from .moe_batch import PackedRoutedExperts, _check, pack_routed_experts, packed_routed_moe_eager  # noqa: F401
 
 
 def batched_grouped_routed_moe_route_gemv(x: torch.Tensor, topk_ids: torch.Tensor, topk_weight: torch.Tensor,

@@ -27,13 +27,16 @@
 extern "C" {
 #endif
 
-#define DSV2_ABI_VERSION 1
+#define DSV2_ABI_VERSION 2
 
 #define DSV2_OK 0
 #define DSV2_E_NULL (-1)      /* a required pointer is null            */
 #define DSV2_E_SHAPE (-2)     /* a size is out of the supported range  */
 #define DSV2_E_ALIGN (-3)     /* a pointer/stride is not 16B-aligned   */
 #define DSV2_E_FLAGS (-4)     /* unsupported flag combination          */
+
+/* bits a kernel ORs into the caller's device status word (int32, optional) */
+#define DSV2_DEVERR_CACHE_FULL 1  /* a cache write at or past a row's capacity was skipped */
 
 /* flags of dsv2_gemv_bf16 / dsv2_gemm_bf16 */
 #define DSV2_LINEAR_SWIGLU 1  /* W holds [gate; up] (2N rows): y = bf16(silu(bf16 g)) * bf16 u */
@@ -53,24 +56,34 @@ int dsv2_rmsnorm_bf16(const void* x, int64_t x_stride, const void* w, void* y, i
  * (triton_kernels/attention_prepost.py:191-223).  n % 8 == 0. */
 int dsv2_residual_add_bf16(const void* a, const void* b, void* out, int64_t n, void* stream);
 
+/* fp16 form of dsv2_residual_add_bf16: out = fp16(fp32(a) + fp32(b)), the fp16 inputs
+ * residual_add_triton also accepts (triton_kernels/attention_prepost.py:196). */
+int dsv2_residual_add_f16(const void* a, const void* b, void* out, int64_t n, void* stream);
+
 /* out = bf16(g * sigmoid(g) * u) in fp32.  Replaces silu_mul_triton
  * (triton_kernels/mlp_elementwise.py:24-45).  n % 8 == 0. */
 int dsv2_silu_mul_bf16(const void* gate, const void* up, void* out, int64_t n, void* stream);
 
-/* mask[b,j] = (j <= pos), position_ids[b] = pos with pos = cache_position[0], int64.
+/* mask[b,j] = (index[j] <= pos), position_ids[b] = pos with pos = cache_position[0], int64
+ * (index = attention_mask_index [max_len]; NULL means index[j] = j).
  * Replaces prepare_decode_inputs_triton (triton_kernels/attention_prepost.py:152-188). */
-int dsv2_prepare_decode_inputs(const int64_t* cache_position, int64_t* attention_mask,
-                               int64_t* position_ids, int batch, int max_len, void* stream);
+int dsv2_prepare_decode_inputs(const int64_t* cache_position, const int64_t* attention_mask_index,
+                               int64_t* attention_mask, int64_t* position_ids, int batch, int max_len, void* stream);
 
 /* dst[b, pos, :] = src[b, :] for b < batch, pos = cache_position[0]; row_bytes % 16 == 0.
  * dst row b starts at dst + b*dst_batch_stride bytes, token rows are row_bytes apart.
- * Replaces copy_single_token_to_cache (triton_kernels/attention_prepost.py:113-149). */
+ * A pos outside [0, max_tokens) writes nothing and ORs DSV2_DEVERR_CACHE_FULL into *status
+ * (when status != NULL).  Replaces copy_single_token_to_cache
+ * (triton_kernels/attention_prepost.py:113-149); the reference's GraphCache raises on
+ * overflow instead (src/run.py:131-134). */
 int dsv2_copy_token_rows(const void* src, int64_t src_batch_stride, void* dst, int64_t dst_batch_stride,
-                         int64_t row_bytes, const int64_t* cache_position, int batch, void* stream);
+                         int64_t row_bytes, const int64_t* cache_position, int64_t max_tokens, int batch,
+                         int32_t* status, void* stream);
 
-/* pos32[b] = cache_position[0]; base[b] = b * per_row_capacity (int64).  Turns the
- * reference's shared scalar cache_position (src/run.py:196-202) into per-row arrays. */
-int dsv2_fill_positions(const int64_t* cache_position, int32_t* pos, int64_t* base,
+/* pos32[b] = cache_position[0]; base[b] = b * per_row_capacity (int64, if base != NULL);
+ * cap[b] = per_row_capacity (int32, if cap != NULL).  Turns the reference's shared scalar
+ * cache_position (src/run.py:196-202) into the per-row arrays of the MLA entry points. */
+int dsv2_fill_positions(const int64_t* cache_position, int32_t* pos, int64_t* base, int32_t* cap,
                         int64_t per_row_capacity, int batch, void* stream);
 
 /* out[r,:] = table[ids[r], :] (bf16 rows of `hidden`).  The embed_tokens gather of the
@@ -119,7 +132,14 @@ int dsv2_gemm_bf16(const void* x, int64_t x_stride, int64_t x_gstride, int rows,
 
 /* ---- absorbed MLA -------------------------------------------------------- */
 
-/* Per row r (new token at cache slot base[r] + pos[r]):
+/* Per-row cache bounds (every MLA entry point): row r owns cache rows
+ * [base[r], base[r] + cap[r]) (int32 cap).  The new token of row r is stored only when
+ * 0 <= pos[r] < cap[r]; otherwise nothing is written, DSV2_DEVERR_CACHE_FULL is ORed into
+ * *status (when status != NULL) and the row attends its cap[r] cached rows, so no launch
+ * reads or writes outside the row's own slots.  The reference raises on overflow
+ * (GraphCacheLayer.update, src/run.py:131-134); here the host reads status after the step.
+ *
+ * Per row r (new token at cache slot base[r] + pos[r]):
  *   c = RMSNorm(qkva[r, 3072:3584]; kv_norm_w) -> cache[slot, 0:512]
  *   k_pe = RoPE(qkva[r, 3584:3648], pos)      -> cache[slot, 512:576]
  *   q_out[r, h, 512:576] = RoPE(q_pe_h);  q_out[r, h, 0:512] = W_UK_h^T q_nope_h
@@ -129,26 +149,26 @@ int dsv2_gemm_bf16(const void* x, int64_t x_stride, int64_t x_gstride, int rows,
  * Replaces kv-norm + _batched_build_qkv_rope_kernel + _cache_write_q1_dual_kernel
  * (attention_decode_batch.py:719-813; attention_decode_small.py:141-339). */
 int dsv2_mla_prepare(const void* qkva, int64_t qkva_stride, int rows, const int32_t* pos,
-                     const int64_t* base, const void* kv_norm_w, float eps, const void* rope_cos,
+                     const int64_t* base, const int32_t* cap, const void* kv_norm_w, float eps, const void* rope_cos,
                      const void* rope_sin, int max_pos, const void* w_ukt, void* cache, void* q_out,
-                     void* stream);
+                     int32_t* status, void* stream);
 
 /* Split-KV absorbed-MLA decode over the compressed cache [*, 576] bf16.
- * Row r attends cache rows base[r] .. base[r]+pos[r] (inclusive); split s covers
+ * Row r attends cache rows base[r] .. base[r]+min(pos[r], cap[r]-1) (inclusive); split s covers
  * tokens [s*split_tokens, (s+1)*split_tokens).  Writes unnormalised partial
  * o_lat [rows, max_splits, 16, 512] fp32 and (m, l) [rows, max_splits, 16, 2]
  * (m in log2 units).  split_tokens % 32 == 0.  Replaces _batched_decode_attention_q1_kernel
  * (attention_decode_batch.py:241-342) / _decode_attention_q1_kernel (attention_decode_small.py:343-423). */
-int dsv2_mla_decode(const void* q, const void* cache, const int64_t* base, const int32_t* pos, int rows,
-                    int split_tokens, int max_splits, float softmax_scale, float* part_o, float* part_ml,
+int dsv2_mla_decode(const void* q, const void* cache, const int64_t* base, const int32_t* pos, const int32_t* cap,
+                    int rows, int split_tokens, int max_splits, float softmax_scale, float* part_o, float* part_ml,
                     void* stream);
 
-/* Merge the splits of dsv2_mla_decode.  With w_uv != NULL: out[r, h*128 + i] =
+/* Merge the splits of dsv2_mla_decode (same pos / cap).  With w_uv != NULL: out[r, h*128 + i] =
  * bf16(sum_j W_UV[h, i, j] o_lat[r, h, j]) (bf16 [rows, 2048], row stride out_stride);
  * with w_uv == NULL: out = bf16 o_lat [rows, 16, 512] for a grouped GEMM.
  * Together with dsv2_mla_decode this replaces the attention core + v-combine
  * (attention_decode_batch.py:240-401). */
-int dsv2_mla_combine(const float* part_o, const float* part_ml, const int32_t* pos, int rows,
+int dsv2_mla_combine(const float* part_o, const float* part_ml, const int32_t* pos, const int32_t* cap, int rows,
                      int split_tokens, int max_splits, const void* w_uv, void* out, int64_t out_stride,
                      void* stream);
 
@@ -160,9 +180,24 @@ int dsv2_mla_combine(const float* part_o, const float* part_ml, const int32_t* p
  * o projections this replaces attention_decode_only_triton / attention_decode_small_batch_triton
  * (triton_kernels/attention_decode_small.py:553-674, :932-1070) for the small family. */
 int dsv2_mla_fused(const void* qkva, int64_t qkva_stride, int rows, const int32_t* pos, const int64_t* base,
-                   const void* kv_norm_w, float eps, const void* rope_cos, const void* rope_sin, int max_pos,
-                   const void* w_ukt, const void* w_uv, void* cache, float softmax_scale, void* out,
-                   int64_t out_stride, void* stream);
+                   const int32_t* cap, const void* kv_norm_w, float eps, const void* rope_cos, const void* rope_sin,
+                   int max_pos, const void* w_ukt, const void* w_uv, void* cache, float softmax_scale, void* out,
+                   int64_t out_stride, int32_t* status, void* stream);
+
+/* q_len = 1 attention over an EXPANDED per-head cache (keys [B, H, L, q_dim], values
+ * [B, H, L, v_dim], bf16, last dim contiguous, element strides as given):
+ *   out[b, h, :] = bf16( softmax_n(scale * k[b,h,n,:] . q[b,h,:]) . v[b,h,n,:] ),  n = 0..pos
+ * with pos = cache_position[0] (int64, device).  pos outside [0, seq_len) attends
+ * min(max(pos, 0), seq_len - 1) + 1 rows and ORs DSV2_DEVERR_CACHE_FULL into *status.
+ * q_dim, v_dim <= 256 and % 8.  Replaces batched_attention_decode_q1_triton
+ * (triton_kernels/attention_decode_batch.py:345-401, attention_decode_small.py:782-840);
+ * the decode step itself reads the compressed cache instead. */
+int dsv2_attention_decode_expanded(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k,
+                                   int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_s, const void* v,
+                                   int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_s, void* out,
+                                   int64_t out_stride_b, int64_t out_stride_h, int batch, int heads, int q_dim,
+                                   int v_dim, int seq_len, const int64_t* cache_position, float softmax_scale,
+                                   int32_t* status, void* stream);
 
 /* ---- MoE ------------------------------------------------------------------ */
 

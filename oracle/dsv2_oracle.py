@@ -339,11 +339,11 @@ class OracleModel:
         return [SeqCache() for _ in range(len(self.w["layers"]))]
 
     def forward(self, ids: torch.Tensor | None, cache: list[SeqCache], start_pos: int,
-                h: torch.Tensor | None = None, trace: list | None = None) -> dict:
+                h: torch.Tensor | None = None, trace: list | None = None, last_logits_only: bool = False) -> dict:
         """Run T tokens of ONE sequence from position ``start_pos``.
 
-        Returns {"hidden": [T,H] final (pre-norm) hidden, "logits": [T,V] fp32,
-        "layer_out": list of [T,H]}.
+        Returns {"hidden": [T,H] final (pre-norm) hidden, "logits": [T,V] fp32 (only the
+        last token's row, [1,V], with last_logits_only), "layer_out": list of [T,H]}.
         """
         if h is None:
             h = self.w["embed"][ids]
@@ -358,7 +358,7 @@ class OracleModel:
                 trace.append(tr)
         res = {"hidden": h, "layer_out": outs}
         if "lm_head" in self.w:
-            xn = rmsnorm(h, self.w["norm"], self.d.eps, self.rb)
+            xn = rmsnorm(h[-1:] if last_logits_only else h, self.w["norm"], self.d.eps, self.rb)
             res["logits"] = linear(xn, self.w["lm_head"], self.rb).to(torch.float32)
         return res
 

@@ -40,7 +40,11 @@ def test_abi_rejects_bad_arguments_without_launching():
     with pytest.raises(_hip.HipKernelError, match="bad shape"):
         _hip.call("dsv2_gemv_bf16", 16, 2048, 1, 2047, 16, 64, None, 0.0, None, 0, 16, 64, 0, None)
     with pytest.raises(_hip.HipKernelError, match="max_splits"):
-        _hip.call("dsv2_mla_decode", 16, 16, 16, 16, 1, 32, 65, 0.1, 16, 16, None)
+        _hip.call("dsv2_mla_decode", 16, 16, 16, 16, 16, 1, 32, 65, 0.1, 16, 16, None)
+    with pytest.raises(_hip.HipKernelError, match="null pointer"):  # the per-row capacity is required
+        _hip.call("dsv2_mla_decode", 16, 16, 16, 16, None, 1, 32, 4, 0.1, 16, 16, None)
+    with pytest.raises(_hip.HipKernelError, match="null pointer"):
+        _hip.call("dsv2_mla_prepare", 16, 3648, 1, 16, 16, None, 16, 1e-6, 16, 16, 64, None, 16, 16, None, None)
     with pytest.raises(_hip.HipKernelError, match="rows\\*6"):
         _hip.call("dsv2_moe_bucket", 16, 2000, 32, 16, 16, 16, 16, None)
 
@@ -218,3 +222,35 @@ def test_bench_refuses_more_than_one_gpu():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True, text=True,
                        timeout=120)
     assert r.returncode == 2 and "one GPU" in r.stderr and r.stdout == ""
+
+
+def test_run_cli_config3_draws_one_prompt_per_row():
+    """--config 3 (bsz=256 x 2048) gives every row its own random prompt, like bench.py's
+    C3; the reference workload (no --config, fixed --prompt-len) replicates one prompt."""
+    from src import run as R
+
+    a = R.parse_args(["--config", "3"])
+    ps = R.make_prompts(a, 4, 102400)
+    assert all(p.numel() == 2048 for p in ps)
+    assert len({tuple(p[:16].tolist()) for p in ps}) == 4
+    b = R.parse_args(["--batch-size", "3", "--prompt-len", "24"])
+    qs = R.make_prompts(b, 3, 102400)
+    assert all(torch.equal(q, qs[0]) for q in qs)
+
+
+def test_engine_capacity_check_is_per_row():
+    """A row whose next position reaches its own capacity stops the step even when another
+    row still has room (capacities [n+2, n+64]: the first row fills after 2 steps)."""
+    from types import SimpleNamespace
+
+    from dsv2lite.engine import DecodeEngine
+
+    eng = object.__new__(DecodeEngine)
+    eng.cache = SimpleNamespace(capacities=[12, 74])
+    eng._host_pos = [10, 10]
+    eng._check_room()  # slot 10 < 12 for row 0
+    eng._host_pos = [11, 11]
+    eng._check_room()  # slot 11, the last of row 0
+    eng._host_pos = [12, 12]
+    with pytest.raises(RuntimeError, match="rows \\[0\\]"):
+        eng._check_room()

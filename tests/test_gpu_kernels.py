@@ -39,7 +39,7 @@ def rb(t):
 
 
 def test_abi_loaded():
-    assert _hip.lib.dsv2_abi_version() == 1
+    assert _hip.lib.dsv2_abi_version() == _hip.ABI_VERSION == 2
     print("native library:", _hip.LIB_PATH, flush=True)
 
 
@@ -511,19 +511,20 @@ def test_mla_decode_combine_vs_fp32(B, lo, hi, seed, split):
     po = torch.empty(B, ns, 16, 512, device=DEV)
     pm = torch.empty(B, ns, 16, 2, device=DEV)
     base_d = base.to(DEV)  # keep device copies alive until the kernels have run
-    call("dsv2_mla_decode", q.data_ptr(), cache.data_ptr(), base_d.data_ptr(), pos.data_ptr(), B, split, ns,
-         scale, po.data_ptr(), pm.data_ptr(), st())
+    cap_d = torch.tensor(cap, dtype=torch.int32, device=DEV)
+    call("dsv2_mla_decode", q.data_ptr(), cache.data_ptr(), base_d.data_ptr(), pos.data_ptr(), cap_d.data_ptr(), B,
+         split, ns, scale, po.data_ptr(), pm.data_ptr(), st())
     olat = torch.empty(B, 16, 512, dtype=BF, device=DEV)
-    call("dsv2_mla_combine", po.data_ptr(), pm.data_ptr(), pos.data_ptr(), B, split, ns, None, olat.data_ptr(),
-         16 * 512, st())
+    call("dsv2_mla_combine", po.data_ptr(), pm.data_ptr(), pos.data_ptr(), cap_d.data_ptr(), B, split, ns, None,
+         olat.data_ptr(), 16 * 512, st())
     rows = [cache[int(base[b]):int(base[b]) + lens[b]] for b in range(B)]
     ref = _mla_reference(q, rows, lens, scale)
     assert rel_err(olat.float(), ref) < 1e-2
     # fused W_UV variant
     w_uv = rnd(16, 128, 512, std=0.05, seed=seed + 100)
     out = torch.empty(B, 2048, dtype=BF, device=DEV)
-    call("dsv2_mla_combine", po.data_ptr(), pm.data_ptr(), pos.data_ptr(), B, split, ns, w_uv.data_ptr(),
-         out.data_ptr(), 2048, st())
+    call("dsv2_mla_combine", po.data_ptr(), pm.data_ptr(), pos.data_ptr(), cap_d.data_ptr(), B, split, ns,
+         w_uv.data_ptr(), out.data_ptr(), 2048, st())
     ref2 = torch.einsum("hij,bhj->bhi", w_uv.float(), ref).reshape(B, 2048)
     assert rel_err(out.float(), ref2) < 1e-2
 
@@ -536,13 +537,14 @@ def test_mla_constant_cache_returns_value():
     base = torch.tensor([0, 800], dtype=torch.int64, device=DEV)
     pos = torch.tensor([L - 1, 31], dtype=torch.int32, device=DEV)
     q = rnd(B, 16, 576, seed=60)
+    cap = torch.tensor([800, 800], dtype=torch.int32, device=DEV)
     po = torch.empty(B, 4, 16, 512, device=DEV)
     pm = torch.empty(B, 4, 16, 2, device=DEV)
-    call("dsv2_mla_decode", q.data_ptr(), cache.data_ptr(), base.data_ptr(), pos.data_ptr(), B, 224, 4, 0.1147,
-         po.data_ptr(), pm.data_ptr(), st())
+    call("dsv2_mla_decode", q.data_ptr(), cache.data_ptr(), base.data_ptr(), pos.data_ptr(), cap.data_ptr(), B, 224, 4,
+         0.1147, po.data_ptr(), pm.data_ptr(), st())
     olat = torch.empty(B, 16, 512, dtype=BF, device=DEV)
-    call("dsv2_mla_combine", po.data_ptr(), pm.data_ptr(), pos.data_ptr(), B, 224, 4, None, olat.data_ptr(), 16 * 512,
-         st())
+    call("dsv2_mla_combine", po.data_ptr(), pm.data_ptr(), pos.data_ptr(), cap.data_ptr(), B, 224, 4, None,
+         olat.data_ptr(), 16 * 512, st())
     assert torch.allclose(olat.float().cpu(), row[:512].float().expand(B, 16, 512), rtol=1e-2, atol=1e-3)
 
 
@@ -562,8 +564,12 @@ def test_mla_prepare_vs_oracle(B):
     cache = torch.zeros(12000, 576, dtype=BF, device=DEV)
     q = torch.zeros(B, 16, 576, dtype=BF, device=DEV)
     w_ukt = w_uk.transpose(1, 2).contiguous()
-    call("dsv2_mla_prepare", qkva.data_ptr(), 3648, B, pos.data_ptr(), base.data_ptr(), kvw.data_ptr(), 1e-6,
-         cos.data_ptr(), sin.data_ptr(), 4096, w_ukt.data_ptr(), cache.data_ptr(), q.data_ptr(), st())
+    cap = torch.full((B,), 4096, dtype=torch.int32, device=DEV)
+    status = torch.zeros(1, dtype=torch.int32, device=DEV)
+    call("dsv2_mla_prepare", qkva.data_ptr(), 3648, B, pos.data_ptr(), base.data_ptr(), cap.data_ptr(), kvw.data_ptr(),
+         1e-6, cos.data_ptr(), sin.data_ptr(), 4096, w_ukt.data_ptr(), cache.data_ptr(), q.data_ptr(),
+         status.data_ptr(), st())
+    assert status.item() == 0
     ocos, osin = O.yarn_cos_sin(O.Dims(), 4096, mode="bf16")
     assert torch.equal(cos.float().cpu(), ocos) and torch.equal(sin.float().cpu(), osin)
     x = qkva.float().cpu()
@@ -630,9 +636,12 @@ def test_mla_fused_small_family_vs_fp32(lens):
     before = cache.clone()
     scale = cfg.softmax_scale
     pos_d, base_d, w_ukt = pos.to(DEV), base.to(DEV), w_uk.transpose(1, 2).contiguous()  # alive across the launch
-    call("dsv2_mla_fused", qkva.data_ptr(), 3648, B, pos_d.data_ptr(), base_d.data_ptr(), kvw.data_ptr(),
-         1e-6, cos.data_ptr(), sin.data_ptr(), 512, w_ukt.data_ptr(), w_uv.data_ptr(),
-         cache.data_ptr(), scale, out.data_ptr(), 2048, st())
+    cap_d = torch.tensor(cap, dtype=torch.int32, device=DEV)
+    status = torch.zeros(1, dtype=torch.int32, device=DEV)
+    call("dsv2_mla_fused", qkva.data_ptr(), 3648, B, pos_d.data_ptr(), base_d.data_ptr(), cap_d.data_ptr(),
+         kvw.data_ptr(), 1e-6, cos.data_ptr(), sin.data_ptr(), 512, w_ukt.data_ptr(), w_uv.data_ptr(),
+         cache.data_ptr(), scale, out.data_ptr(), 2048, status.data_ptr(), st())
+    assert status.item() == 0
     # reference: same prepare math (oracle pieces), fp32 attention over the updated rows
     x = qkva.float().cpu()
     ocos, osin = O.yarn_cos_sin(O.Dims(), 512, mode="bf16")
