@@ -2,6 +2,8 @@
 // once with 16-byte loads, fp32 accumulation, fused RMSNorm prologue, SwiGLU /
 // residual / fp32-logit epilogues.  One wave owns RPW output rows at a time (RPW gate +
 // RPW up rows for SwiGLU); lanes split K in 8-element chunks.
+#include <mutex>
+
 #include "common.h"
 
 // K <= 2048: one batch of chunks per row (lane l owns chunks l, l+64, l+128, l+192).
@@ -493,19 +495,10 @@ extern "C" int64_t dsv2_lm_head_argmax_workspace_size(int rows) {
   return rows < 0 ? -1 : (int64_t)rows * 1024 * 4 * 8;
 }
 
-extern "C" int dsv2_lm_head_argmax_bf16(const void* x, int64_t x_stride, int rows, const void* W, int vocab,
-                                        const void* norm_w, float eps, float* logits, void* partials,
-                                        int64_t partials_bytes, int64_t* next_ids, int32_t* pos, void* stream) {
-  DSV2_REQUIRE(x && W && norm_w && logits && partials && next_ids, DSV2_E_NULL, "lm_head_argmax: null pointer");
-  DSV2_REQUIRE(rows >= 1 && rows <= 8 && vocab > 0 && vocab % 2 == 0, DSV2_E_SHAPE,
-               "lm_head_argmax: 1 <= rows <= 8 and an even vocabulary required (rows %d, vocab %d)", rows, vocab);
-  DSV2_REQUIRE(partials_bytes >= dsv2_lm_head_argmax_workspace_size(rows), DSV2_E_SHAPE,
-               "lm_head_argmax: partials buffer too small");
-  DSV2_REQUIRE(dsv2_aligned16(x) && dsv2_aligned16(W) && dsv2_aligned16(norm_w) && x_stride % 8 == 0, DSV2_E_ALIGN,
-               "lm_head_argmax: alignment");
-  hipStream_t st = (hipStream_t)stream;
+static int lm_head_argmax_launch(const void* x, int64_t x_stride, int rows, const void* W, int vocab,
+                                 const void* norm_w, float eps, float* logits, float* amax, int64_t* next_ids,
+                                 int32_t* pos, hipStream_t st) {
   const bf16_t* xb = (const bf16_t*)x;
-  float* amax = (float*)partials;
   constexpr int RPW = 2;
   if (rows == 1)
     launch_k2048<1, RPW, false>(xb, x_stride, rows, 2048, (const bf16_t*)W, vocab, (const bf16_t*)norm_w, eps,
@@ -521,7 +514,78 @@ extern "C" int dsv2_lm_head_argmax_bf16(const void* x, int64_t x_stride, int row
                                 nullptr, 0, logits, vocab, true, st, amax);
   int rc = dsv2_launch_status("lm_head_argmax");
   if (rc) return rc;
+  // every wave of the GEMV writes its (max, index) partial of every row, so the partials
+  // need no clearing between calls
   hipLaunchKernelGGL(argmax_partials_kernel, dim3(rows), dim3(256), 0, st, amax, k2048_grid(vocab, RPW) * 4, next_ids,
                      pos);
   return dsv2_launch_status("lm_head_argmax");
+}
+
+#define DSV2_LM_HEAD_ARGS_OK(fn)                                                                                     \
+  DSV2_REQUIRE(x && W && norm_w && logits && next_ids, DSV2_E_NULL, fn ": null pointer");                           \
+  DSV2_REQUIRE(rows >= 1 && rows <= 8 && vocab > 0 && vocab % 2 == 0, DSV2_E_SHAPE,                                  \
+               fn ": 1 <= rows <= 8 and an even vocabulary required (rows %d, vocab %d)", rows, vocab);              \
+  DSV2_REQUIRE(dsv2_aligned16(x) && dsv2_aligned16(W) && dsv2_aligned16(norm_w) && x_stride % 8 == 0, DSV2_E_ALIGN, \
+               fn ": alignment")
+
+extern "C" int dsv2_lm_head_argmax_bf16(const void* x, int64_t x_stride, int rows, const void* W, int vocab,
+                                        const void* norm_w, float eps, float* logits, void* partials,
+                                        int64_t partials_bytes, int64_t* next_ids, int32_t* pos, void* stream) {
+  DSV2_LM_HEAD_ARGS_OK("lm_head_argmax");
+  DSV2_REQUIRE(partials, DSV2_E_NULL, "lm_head_argmax: null pointer");
+  DSV2_REQUIRE(partials_bytes >= dsv2_lm_head_argmax_workspace_size(rows), DSV2_E_SHAPE,
+               "lm_head_argmax: partials buffer too small");
+  return lm_head_argmax_launch(x, x_stride, rows, W, vocab, norm_w, eps, logits, (float*)partials, next_ids, pos,
+                               (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------
+// The same, for callers that cannot allocate (code under graph capture, serving loops
+// that forbid hipMalloc): the argmax partials live in `scratch`, a file-scope device array
+// of the library -- one copy per GPU, held until the process ends, sized for the largest
+// call (8 rows x 4096 waves x (max, index) = 256 KiB).  Host code never passes the array's
+// name to a kernel (on the host it is only a stand-in): each device's address comes from
+// hipGetSymbolAddress, taken once per device on the first call made with that device
+// current, and kept in g_scratch_dev.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr int kScratchRows = 8;
+constexpr int64_t kScratchBytes = (int64_t)kScratchRows * 4096 * 8;
+constexpr int kMaxDevices = 64;
+void* g_scratch_dev[kMaxDevices] = {};
+std::mutex g_scratch_mu;
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+static int scratch_on_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  DSV2_REQUIRE(e == hipSuccess, (int)e, "lm_head_argmax_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+  DSV2_REQUIRE(dev >= 0 && dev < kMaxDevices, DSV2_E_SHAPE, "lm_head_argmax_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    DSV2_REQUIRE(e == hipSuccess && p, e == hipSuccess ? DSV2_E_NULL : (int)e,
+                 "lm_head_argmax_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                 hipGetErrorString(e));
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return DSV2_OK;
+}
+
+extern "C" int dsv2_lm_head_argmax_bf16_noalloc(const void* x, int64_t x_stride, int rows, const void* W, int vocab,
+                                                const void* norm_w, float eps, float* logits, int64_t* next_ids,
+                                                int32_t* pos, void* stream) {
+  DSV2_LM_HEAD_ARGS_OK("lm_head_argmax_noalloc");
+  DSV2_REQUIRE(dsv2_lm_head_argmax_workspace_size(rows) <= kScratchBytes, DSV2_E_SHAPE,
+               "lm_head_argmax_noalloc: %d rows need more than the %lld-byte device scratch", rows,
+               (long long)kScratchBytes);
+  void* dev_scratch = nullptr;
+  const int rc = scratch_on_current_device(&dev_scratch);
+  if (rc) return rc;
+  return lm_head_argmax_launch(x, x_stride, rows, W, vocab, norm_w, eps, logits, (float*)dev_scratch, next_ids, pos,
+                               (hipStream_t)stream);
 }

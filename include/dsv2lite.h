@@ -120,6 +120,19 @@ int dsv2_lm_head_argmax_bf16(const void* x, int64_t x_stride, int rows, const vo
                              float eps, float* logits, void* partials, int64_t partials_bytes, int64_t* next_ids,
                              int32_t* pos, void* stream);
 
+/* dsv2_lm_head_argmax_bf16 without the caller's workspace, for callers that cannot
+ * allocate (code under hipGraph capture, serving loops that forbid hipMalloc).  No
+ * counterpart in the reference.  The argmax partials live in a library-owned device array
+ * (one per GPU, 256 KiB, kept until the process ends): rows <= 8 (larger requests are
+ * rejected with DSV2_E_SHAPE).  Nothing is allocated; the array's per-device address is
+ * looked up (hipGetSymbolAddress) on the first call made with that device current, so make
+ * that first call outside graph capture.  Every call on one GPU shares the array: calls
+ * that overlap in time on one GPU (other streams, other threads) race and must be ordered
+ * by the caller.  The partials need no clearing: each call writes every one it reads. */
+int dsv2_lm_head_argmax_bf16_noalloc(const void* x, int64_t x_stride, int rows, const void* W, int vocab,
+                                     const void* norm_w, float eps, float* logits, int64_t* next_ids, int32_t* pos,
+                                     void* stream);
+
 /* Grouped bf16 MFMA GEMM (v_mfma_f32_16x16x32_bf16), fp32 accumulation:
  *   for group g < n_groups, row r < rows:
  *     Y[g*y_gstride + r*y_stride + n] = x[g*x_gstride + r*x_stride, :] . W[g*w_gstride + n*K, :]
