@@ -1,22 +1,28 @@
 """Decode-throughput benchmark of the HIP DeepSeek-V2-Lite decode step on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1|2|3|4|r64|r256] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config all|1|2|3|4|r64|r256] [--no-cpu-baseline]
 
-Default workload (benchmark config 1): full 27-layer random-init DeepSeek-V2-Lite
-bf16 (N(0,0.02), seed 0), bsz=1, a 128-token prompt of uniform random ids (seed
-1), eager prefill, then K greedy decode steps with the small kernel family, the
-whole step replayed as one hipGraph.  Prints ONE JSON line.  --config 2|3 are the
-bsz=64/256 random-prompt workloads; r64|r256 the reference's own published workload (one
-24-token prompt replicated over the batch), whose vs_baseline is value / the published A100
-batch-family TPS for it.  --config 4 is the isolated absorbed-MLA decode microbenchmark
-(bsz=128, KV lengths U[256,8192]); its value is compressed-cache GB/s.
+Every config: full 27-layer random-init DeepSeek-V2-Lite bf16 (N(0,0.02), seed 0), eager
+prefill of uniform random prompt ids, then K greedy decode steps, the whole step replayed
+as one hipGraph.  Prints ONE JSON line.
+
+Default (--config all): the line's value is benchmark config 1 (bsz=1, a 128-token prompt
+from seed 1, small kernel family); the metric's other two batch sizes ride along under
+"configs" -- C2 (bsz=64, prompt lengths U[256,1024], batch family) and C3 (bsz=256, 2048-
+token prompts, batch family) -- timed in the same run on the same weights, each with its
+tok/s, ms/step, step roofline and dominant-kernel roofline.  --config N runs one config
+alone; r64|r256 are the reference's own published workload (one 24-token prompt replicated
+over the batch), whose vs_baseline is value / the published A100 batch-family TPS for it.
+--config 4 is the isolated absorbed-MLA decode microbenchmark (bsz=128, KV lengths
+U[256,8192]); its value is compressed-cache GB/s.
 
 Extra fields:
   roofline      -- dominant kernel of the step: algorithmic bytes per launch /
                    average launch time (HIP events around a graph of repeated
                    launches on the engine's stream) vs 8 TB/s; traffic = HBM bytes
                    per launch from the committed PMC summary profiles/traffic_c<N>.json
-                   (see --pmc-traffic), null when absent.
+                   (see --pmc-traffic), null when absent or when it was measured on other
+                   source of the kernel; traffic_source says which.
   step_roofline -- algorithmic bytes per step (weights of the experts actually hit,
                    counted from the router output, + compressed KV read) / step time.
   cpu_baseline  -- the CPU oracle (PyTorch eager restatement of the HF math) timed on
@@ -118,15 +124,24 @@ def time_dominant_kernel(eng, family: str, reps: int = 4) -> dict:
             def launch(L):
                 call("dsv2_moe_grouped_gateup", ptr(b.xn), ptr(b.sorted), ptr(b.tiles), ptr(b.ntiles), b.max_tiles,
                      b.tile_tokens, ptr(L.w_gu), c.moe_inter, ptr(b.hs), stream_ptr())
+    avg_s = time_graph(launch, moe_layers, reps)
+    ach = bytes_per / avg_s
+    return {"kernel": name, "bound": "hbm", "achieved": ach / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+            "frac": ach / HBM_PEAK, "traffic": None, "bytes_per_launch": bytes_per, "avg_us": avg_s * 1e6}
+
+
+def time_graph(launch, layers, reps: int = 4) -> float:
+    """Average seconds per launch of `launch(L)` over a graph with one launch per entry of
+    `layers`, replayed once untimed and `reps` times between HIP events on the current
+    stream."""
     s = torch.cuda.Stream()
     with torch.cuda.stream(s):
-        launch(moe_layers[0])
+        launch(layers[0])
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        for L in moe_layers:
+        for L in layers:
             launch(L)
-    n_launch = len(moe_layers)
     g.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -135,25 +150,111 @@ def time_dominant_kernel(eng, family: str, reps: int = 4) -> dict:
         g.replay()
     e1.record()
     torch.cuda.synchronize()
-    avg_s = e0.elapsed_time(e1) / 1e3 / (n_launch * reps)
-    ach = bytes_per / avg_s
-    return {"kernel": name, "bound": "hbm", "achieved": ach / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-            "frac": ach / HBM_PEAK, "traffic": None, "bytes_per_launch": bytes_per, "avg_us": avg_s * 1e6}
+    return e0.elapsed_time(e1) / 1e3 / (len(layers) * reps)
 
 
-def measured_traffic(config: int, kernel: str):
+def time_other_kernels(eng, family: str, ctx_rows: list[int]) -> dict:
+    """The step's next-largest kernels, each timed like the dominant one (a graph of one
+    launch per MoE layer on that layer's weights / cache, after the dominant kernel's graph,
+    so their dispatches are the last of their symbol in a profiled run): achieved GB/s of
+    the algorithmic bytes.  ctx_rows: cached tokens each row attends (pos + 1)."""
+    from dsv2lite.engine import shared_in_grouped
+    from triton_kernels._hip import call, ptr, stream_ptr
+
+    c, b, B = eng.cfg, eng.buf, eng.B
+    moe = [i for i, L in enumerate(eng.w.layers) if L.moe]
+    out = {}
+
+    def entry(name, launch, layers, nbytes):
+        t = time_graph(launch, layers)
+        out[name] = {"kernel": name, "avg_us": t * 1e6, "bytes_per_launch": nbytes,
+                     "achieved_GBps": nbytes / t / 1e9, "frac": nbytes / t / HBM_PEAK}
+
+    kv = sum(ctx_rows) * 1152
+    if family == "small":
+        def fused(li):
+            L = eng.w.layers[li]
+            call("dsv2_mla_fused", ptr(b.qkva), c.qkva_dim, B, ptr(eng.cache.pos), ptr(eng.cache.base),
+                 ptr(eng.cache.cap), ptr(L.kv_norm), c.eps, ptr(eng.cos), ptr(eng.sin), eng.max_pos, ptr(L.w_ukt),
+                 ptr(L.w_uv), ptr(eng.cache.layer(li)), eng.scale, ptr(b.attn), c.hidden, None, stream_ptr())
+        if eng.fused_mla:
+            entry("mla_fused_kernel (W_UK absorption + attention + W_UV, one workgroup per head)", fused, moe,
+                  2 * 2 * 16 * 128 * 512 + kv + B * 2048 * 2)
+
+        def down(li):
+            L = eng.w.layers[li]
+            call("dsv2_moe_route_down", ptr(b.hbuf), B, ptr(b.ids32), ptr(b.wts), ptr(L.w_down), ptr(L.sh_down),
+                 c.moe_inter, c.top_k + 2, None, ptr(b.h), ptr(b.attn), stream_ptr())
+        entry("route_down_kernel (6 routed + 2 shared-half down projections + combine)", down, moe,
+              B * 8 * 2048 * 1408 * 2)
+        return out
+    n_exp = int(torch.unique(b.ids32[:B]).numel())
+    R = B * c.top_k
+    shared = shared_in_grouped(B, b.tile_tokens)
+
+    def down(li):
+        L = eng.w.layers[li]
+        if shared:
+            call("dsv2_moe_grouped_down_shared", ptr(b.hs), B, ptr(b.tiles), ptr(b.ntiles), b.max_tiles,
+                 b.tile_tokens, ptr(L.w_down), ptr(b.shmid), ptr(L.sh_down), c.moe_inter, ptr(b.ys), ptr(b.shparts),
+                 stream_ptr())
+        else:
+            call("dsv2_moe_grouped_down", ptr(b.hs), ptr(b.tiles), ptr(b.ntiles), b.max_tiles, b.tile_tokens,
+                 ptr(L.w_down), c.moe_inter, ptr(b.ys), stream_ptr())
+    nb = n_exp * 2048 * 1408 * 2 + R * 1408 * 2 + R * 2048 * 2
+    if shared:
+        nb += 2048 * c.shared_inter * 2 + B * c.shared_inter * 2 + 2 * B * 2048 * 4
+    entry("expert-grouped down" + (" + the 2 shared-expert halves" if shared else "")
+          + f" ({b.tile_tokens}-token tiles)", down, moe, nb)
+
+    def decode(li):
+        call("dsv2_mla_decode", ptr(b.q), ptr(eng.cache.layer(li)), ptr(eng.cache.base), ptr(eng.cache.pos),
+             ptr(eng.cache.cap), B, b.split_tokens, b.max_splits, eng.scale, ptr(b.part_o), ptr(b.part_ml),
+             stream_ptr())
+    entry(f"mla_decode_kernel (split-KV, {b.split_tokens}-token splits)", decode, moe,
+          kv + B * 16 * 576 * 2 + B * b.max_splits * 16 * 514 * 4)
+    return out
+
+
+CSRC = os.path.join(PKG, "csrc")
+
+
+def kernel_source_sha(kernel: str) -> str | None:
+    """sha256 (16 hex) of the csrc file that defines `kernel` (symbol before any template
+    arguments) together with csrc/common.h: a PMC traffic figure measured on other source
+    is stale."""
+    import hashlib
+    import re
+
+    name = kernel.split("<")[0].split(" ")[0]
+    pat = re.compile(r"__global__[^;{]*\b" + re.escape(name) + r"\s*\(")
+    for fn in sorted(os.listdir(CSRC)):
+        if fn.endswith(".hip"):
+            txt = open(os.path.join(CSRC, fn), "rb").read()
+            if pat.search(txt.decode(errors="replace")):
+                h = hashlib.sha256(txt + open(os.path.join(CSRC, "common.h"), "rb").read())
+                return h.hexdigest()[:16]
+    return None
+
+
+def measured_traffic(config, kernel: str) -> tuple[float | None, dict]:
     """HBM bytes per launch of the dominant kernel from the committed PMC summary
-    (profiles/traffic_c<config>.json, written by --pmc-traffic), or None when that summary
-    is missing or covers another kernel."""
-    path = os.path.join(ROOT, "profiles", f"traffic_c{config}.json")
+    profiles/traffic_c<config>.json (written by --pmc-traffic from two rocprofv3 --pmc runs),
+    and where that figure comes from.  None when the summary is missing, covers another
+    kernel, or was measured on a different source of the kernel (its recorded source sha
+    differs from the current file's)."""
+    rel = os.path.join("profiles", f"traffic_c{config}.json")
+    src = {"profile": rel, "source_sha": kernel_source_sha(kernel)}
     try:
-        with open(path) as f:
+        with open(os.path.join(ROOT, rel)) as f:
             t = json.load(f)
     except (OSError, ValueError):
-        return None
+        return None, dict(src, status="missing")
     if not kernel.startswith(t.get("kernel_symbol", "\0")):
-        return None
-    return t.get("traffic_bytes_per_dispatch")
+        return None, dict(src, status="other kernel")
+    if t.get("source_sha") != src["source_sha"]:
+        return None, dict(src, status="stale", profiled_source_sha=t.get("source_sha"))
+    return t.get("traffic_bytes_per_dispatch"), dict(src, status="measured on this source")
 
 
 def _csv_rows(path: str):
@@ -190,7 +291,8 @@ def pmc_traffic(fetch_csv: str, write_csv: str, kernel: str, copy_bytes: int, ou
     f_kib, n_f, f_copy = per_kernel(fetch_csv)
     w_kib, n_w, w_copy = per_kernel(write_csv)
     f_scale, w_scale = copy_bytes / (f_copy * 1024), copy_bytes / (w_copy * 1024)
-    res = {"kernel_symbol": kernel, "command": command, "dispatches": [n_f, n_w],
+    res = {"kernel_symbol": kernel, "source_sha": kernel_source_sha(kernel), "command": command,
+           "dispatches": [n_f, n_w],
            "fetch_kib_per_dispatch": f_kib, "write_kib_per_dispatch": w_kib,
            "copy_calibration": {"bytes": copy_bytes, "fetch_kib": f_copy, "write_kib": w_copy,
                                 "fetch_scale": f_scale, "write_scale": w_scale},
@@ -199,6 +301,59 @@ def pmc_traffic(fetch_csv: str, write_csv: str, kernel: str, copy_bytes: int, ou
         json.dump(res, f, indent=1)
         f.write("\n")
     return res
+
+
+def mfma_summary(counter_csv: str, stats_csv: str, out: str, title: str, command: str, top: int = 12,
+                 tail: int | None = None) -> None:
+    """rocprofv3 --pmc MfmaUtil SQ_INSTS_VALU_MFMA_MOPS_BF16 counter CSV (one row per dispatch
+    and counter) + the kernel_stats.csv of a kernel-trace run of the same command without
+    counters -> markdown: per kernel symbol, the MFMA-busy share of the SIMDs (MfmaUtil), the
+    bf16 MFMA flops per dispatch (MOPS x 512) and, with the counter-free average duration,
+    the achieved TFLOP/s against the 2.5 PFLOP/s dense bf16 peak.  Only the last `tail`
+    dispatches of each symbol count (default DOMINANT_DISPATCHES: the bench's timing graph of
+    that kernel, after the prefill's dispatches of the same symbol)."""
+    import collections
+
+    tail = DOMINANT_DISPATCHES if tail is None else tail
+    per = collections.defaultdict(dict)  # name -> dispatch id -> {counter: value}
+    for r in _csv_rows(counter_csv):
+        name = r["Kernel_Name"].replace("void ", "").split("(")[0]
+        per[name].setdefault(int(r["Dispatch_Id"]), {})[r["Counter_Name"]] = float(r["Counter_Value"])
+    avg_ns, spans = {}, collections.defaultdict(list)
+    for r in _csv_rows(stats_csv):
+        if "AverageNs" in r:  # kernel_stats.csv: the average over all dispatches
+            avg_ns[r["Name"].replace("void ", "").split("(")[0]] = float(r["AverageNs"])
+        else:  # kernel_trace.csv: the last `tail` dispatches, like the counters
+            spans[r["Kernel_Name"].replace("void ", "").split("(")[0]].append(
+                (int(r["Dispatch_Id"]), int(r["End_Timestamp"]) - int(r["Start_Timestamp"])))
+    for name, v in spans.items():
+        v = sorted(v)[-tail:]
+        avg_ns[name] = sum(d for _, d in v) / len(v)
+    rows = []
+    for name, disp in per.items():
+        last = [disp[d] for d in sorted(disp)[-tail:]]
+        mops = [x["SQ_INSTS_VALU_MFMA_MOPS_BF16"] for x in last if "SQ_INSTS_VALU_MFMA_MOPS_BF16" in x]
+        util = [x["MfmaUtil"] for x in last if "MfmaUtil" in x]
+        f = sum(mops) / len(mops) * 512 if mops else 0.0
+        u = sum(util) / len(util) if util else float("nan")
+        rows.append((f, name, len(last), u, avg_ns.get(name)))
+    rows.sort(reverse=True)
+    L = [f"# {title}", "", "Commands (from the repo root, on one MI355X):", "", "```", command, "```", "",
+         f"Per kernel symbol, the last {tail} dispatches of the counter run (the bench's timing graph of that "
+         "kernel: 1 + 5 x 26 launches on the decode step's own activations, after the prefill's dispatches).  "
+         "MfmaUtil = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x SIMDs): the share of SIMD cycles the MFMA "
+         "unit was busy during the dispatch.  bf16 flops = SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512.  Durations: the "
+         f"same last {tail} dispatches of the symbol in the counter-free kernel-trace run.", "",
+         "| kernel | dispatches | MfmaUtil % | bf16 MFMA GFLOP / dispatch | avg us | TFLOP/s | % of 2.5 PF |",
+         "|---|---:|---:|---:|---:|---:|---:|"]
+    for f, name, n, u, ns in rows[:top]:
+        if f <= 0:
+            continue
+        tf = f / (ns * 1e-9) / 1e12 if ns else float("nan")
+        L.append(f"| `{name[:70]}` | {n} | {u:.1f} | {f / 1e9:.3f} | "
+                 f"{(ns or float('nan')) / 1e3:.1f} | {tf:.1f} | {100 * tf / 2500:.1f} |")
+    with open(out, "w") as fh:
+        fh.write("\n".join(L) + "\n")
 
 
 def summarize_trace(db: str, out: str, title: str, command: str, marker: str = "embed_gather") -> None:
@@ -325,7 +480,8 @@ def bench_mla_micro(args) -> dict:
     avg = e0.elapsed_time(e1) / 1e3 / (26 * 4)
     roof = {"kernel": "mla_decode_kernel (split-KV absorbed-MLA decode, MFMA)", "bound": "hbm",
             "achieved": kb / avg / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": kb / avg / HBM_PEAK,
-            "traffic": measured_traffic(4, "mla_decode_kernel"), "bytes_per_launch": kb, "avg_us": avg * 1e6}
+            "traffic": None, "bytes_per_launch": kb, "avg_us": avg * 1e6}
+    roof["traffic"], roof["traffic_source"] = measured_traffic(4, "mla_decode_kernel")
     value = kb * args.steps / dt / 1e9
     out = {
         "metric": "absorbed-MLA decode kernel: compressed-cache GB/s (benchmark config 4)", "value": round(value, 1),
@@ -420,12 +576,81 @@ def _log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def run_config(key, w, args, cfg, dev) -> dict:
+    """Prefill + K timed graph replays of one benchmark config on already-initialised weights:
+    tok/s, ms/step, the step's byte roofline and the dominant kernel's roofline."""
+    import dsv2lite
+
+    spec = CONFIGS[key]
+    family = args.family or spec["family"]
+    g = torch.Generator().manual_seed(spec["seed"])
+    lens = spec["prompt"](g)
+    if spec.get("replicate"):
+        prompts = [torch.randint(0, cfg.vocab, (lens[0],), generator=g)] * len(lens)
+    else:
+        prompts = [torch.randint(0, cfg.vocab, (n,), generator=g) for n in lens]
+    steps, warm = args.steps, args.warmup
+    caps = [n + steps + warm + 8 for n in lens]
+    eng = dsv2lite.DecodeEngine(w, caps, family=family, mla_path=args.mla_path)
+    t0 = time.perf_counter()
+    eng.prefill([p.to(dev) for p in prompts])
+    torch.cuda.synchronize()
+    t_prefill = time.perf_counter() - t0
+    _log(f"config {key}: prefill of {sum(lens)} tokens done ({t_prefill:.2f}s)")
+    snap = eng.snapshot()
+    # one recorded eager step: distinct experts per layer (router output) for the byte model
+    rec = []
+    eng.step(record=rec)
+    torch.cuda.synchronize()
+    n_exp = [int(torch.unique(r[2]).numel()) for r in rec if r[0] == "router"]
+    del rec
+    eng.restore(snap)
+    for _ in range(warm):
+        eng.step()
+    torch.cuda.synchronize()
+    eng.restore(snap)
+    eng.capture()
+    eng.restore(snap)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        eng.replay()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    eng.check_errors()
+    B = eng.B
+    value = B * steps / dt
+    ms = dt / steps * 1e3
+    # KV rows read per layer per step, averaged over the timed steps (ctx = pos + 1)
+    ctx_avg = sum(n + 1 + (steps - 1) / 2 for n in lens)
+    sb = step_bytes(cfg, n_exp, ctx_avg, B)
+    _log(f"config {key}: timed {steps} graph replays: {ms:.3f} ms/step, {value:.1f} tok/s")
+    roof = time_dominant_kernel(eng, family)
+    roof["traffic"], roof["traffic_source"] = measured_traffic(key, roof["kernel"])
+    pos_now = eng.cache.pos.cpu().tolist()
+    others = time_other_kernels(eng, family, [p + 1 for p in pos_now])
+    res = {"workload": spec["workload"], "global_batch": B, "seq_len": max(lens), "kernel_family": family,
+           "mla_path": args.mla_path if family == "small" else "split", "prompt_tokens": sum(lens),
+           "tok_s": value, "ms_per_step": ms, "steps": steps, "warmup": warm, "roofline": roof,
+           "other_kernels": others,
+           "step_roofline": {"bytes_per_step": sb, "achieved_GBps": sb / (ms / 1e3) / 1e9,
+                             "frac_of_8TBps": sb / (ms / 1e3) / HBM_PEAK, "distinct_experts_per_layer": n_exp},
+           "setup_s": {"prefill": round(t_prefill, 3)}}
+    if spec.get("published"):
+        res["vs_published_a100"] = round(value / spec["published"], 3)
+    del eng
+    torch.cuda.empty_cache()
+    return res
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=99)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="1", choices=[str(k) for k in CONFIGS] + ["4"])
+    ap.add_argument("--config", default="all", choices=["all"] + [str(k) for k in CONFIGS] + ["4"],
+                    help="all (default): config 1 is the line's value, configs 2 and 3 ride along under "
+                         "'configs'; N: that config alone")
     ap.add_argument("--family", choices=("small", "batch"), default=None)
     ap.add_argument("--mla-path", choices=("fused", "split"), default="fused",
                     help="small family: one fused MLA kernel per layer, or prepare + split-KV decode + combine")
@@ -438,6 +663,9 @@ def main() -> None:
     ap.add_argument("--pmc-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="no GPU: HBM bytes per dispatch of --kernel from two --pmc runs (FETCH_SIZE, WRITE_SIZE) "
                          "scaled by the run's calibration copies; written to --out")
+    ap.add_argument("--mfma-summary", nargs=2, metavar=("COUNTER_CSV", "TRACE_CSV"),
+                    help="no GPU: MFMA utilisation per kernel from a --pmc MfmaUtil SQ_INSTS_VALU_MFMA_MOPS_BF16 run "
+                         "and the kernel_trace.csv of a --kernel-trace run of the same command; markdown to --out")
     ap.add_argument("--mla-split", type=int, default=0, help="config 4: split_tokens override (multiple of 32)")
     ap.add_argument("--kernel", default=None)
     ap.add_argument("--out", default=None)
@@ -446,6 +674,9 @@ def main() -> None:
     args = ap.parse_args()
     if args.summarize_trace:
         summarize_trace(args.summarize_trace[0], args.summarize_trace[1], args.title, args.command)
+        return
+    if args.mfma_summary:
+        mfma_summary(args.mfma_summary[0], args.mfma_summary[1], args.out, args.title, args.command)
         return
     if args.pmc_traffic:
         print(json.dumps(pmc_traffic(args.pmc_traffic[0], args.pmc_traffic[1], args.kernel, 512 * 2**20, args.out,
@@ -462,8 +693,6 @@ def main() -> None:
     if args.config == 4:
         print(json.dumps(bench_mla_micro(args)), flush=True)
         return
-    spec = CONFIGS[args.config]
-    family = args.family or spec["family"]
     cfg = dsv2lite.DSV2Config()
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
@@ -472,63 +701,27 @@ def main() -> None:
     torch.cuda.synchronize()
     t_init = time.perf_counter() - t0
     _log(f"weights ready ({w.nbytes() / 1e9:.1f} GB, {t_init:.1f}s)")
-    g = torch.Generator().manual_seed(spec["seed"])
-    lens = spec["prompt"](g)
-    if spec.get("replicate"):
-        prompts = [torch.randint(0, cfg.vocab, (lens[0],), generator=g)] * len(lens)
-    else:
-        prompts = [torch.randint(0, cfg.vocab, (n,), generator=g) for n in lens]
-    steps, warm = args.steps, args.warmup
-    caps = [n + steps + warm + 8 for n in lens]
-    eng = dsv2lite.DecodeEngine(w, caps, family=family, mla_path=args.mla_path)
-    t0 = time.perf_counter()
-    eng.prefill([p.to(dev) for p in prompts])
-    torch.cuda.synchronize()
-    t_prefill = time.perf_counter() - t0
-    _log(f"prefill of {sum(lens)} tokens done ({t_prefill:.2f}s)")
-    snap = eng.snapshot()
-
-    # one recorded eager step: distinct experts per layer (router output) for the byte model
-    rec = []
-    eng.step(record=rec)
-    torch.cuda.synchronize()
-    n_exp = [int(torch.unique(r[2]).numel()) for r in rec if r[0] == "router"]
-    eng.restore(snap)
-    for _ in range(warm):
-        eng.step()
-    torch.cuda.synchronize()
-    eng.restore(snap)
-    eng.capture()
-    eng.restore(snap)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        eng.replay()
-    torch.cuda.synchronize()
-    dt = time.perf_counter() - t0
-    B = eng.B
-    value = B * steps / dt
-    ms = dt / steps * 1e3
-    # KV rows read per layer per step, averaged over the timed steps (ctx = pos + 1)
-    ctx_avg = sum(n + 1 + (steps - 1) / 2 for n in lens)
-    sb = step_bytes(cfg, n_exp, ctx_avg, B)
-    _log(f"timed {steps} graph replays: {ms:.3f} ms/step, {value:.1f} tok/s")
-    roof = time_dominant_kernel(eng, family)
-    roof["traffic"] = measured_traffic(args.config, roof["kernel"])
+    head = 1 if args.config == "all" else args.config
+    r = run_config(head, w, args, cfg, dev)
+    spec = CONFIGS[head]
     out = {
-        "metric": METRIC, "value": round(value, 2), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warm,
-        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": round(value / spec["published"], 3) if spec.get("published") else None,
+        "metric": METRIC, "value": round(r["tok_s"], 2), "unit": "tokens/s", "n_gpus": 1, "steps": r["steps"],
+        "warmup": r["warmup"], "ms_per_step": round(r["ms_per_step"], 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": r.get("vs_published_a100"),
         "dtype": "bf16", "data": "synthetic: random-init weights N(0,0.02) seed 0, uniform random prompt ids"
                                  + (" (one prompt replicated over the batch)" if spec.get("replicate") else ""),
-        "config": {"workload": spec["workload"], "global_batch": B, "seq_len": max(lens), "kernel_family": family,
-                   "mla_path": args.mla_path if family == "small" else "split",
-                   "prompt_tokens": sum(lens), "parallelism": "none (1 GPU)"},
-        "roofline": roof,
-        "step_roofline": {"bytes_per_step": sb, "achieved_GBps": sb / (ms / 1e3) / 1e9,
-                          "frac_of_8TBps": sb / (ms / 1e3) / HBM_PEAK, "distinct_experts_per_layer": n_exp},
-        "setup_s": {"init_weights": round(t_init, 2), "prefill": round(t_prefill, 3)},
+        "config": {"workload": r["workload"], "global_batch": r["global_batch"], "seq_len": r["seq_len"],
+                   "kernel_family": r["kernel_family"], "mla_path": r["mla_path"],
+                   "prompt_tokens": r["prompt_tokens"], "parallelism": "none (1 GPU)"},
+        "roofline": r["roofline"], "step_roofline": r["step_roofline"], "other_kernels": r["other_kernels"],
+        "setup_s": dict(r["setup_s"], init_weights=round(t_init, 2)),
     }
+    if args.config == "all":
+        # the metric's other two batch sizes, timed in the same run on the same weights
+        out["configs"] = {}
+        for key in (2, 3):
+            rk = run_config(key, w, args, cfg, dev)
+            out["configs"][f"C{key}"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in rk.items()}
     if args.copy_calibration:
         _copy_calibration(out, dev)
     if not args.no_cpu_baseline:

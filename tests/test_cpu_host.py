@@ -254,3 +254,63 @@ def test_engine_capacity_check_is_per_row():
     eng._host_pos = [12, 12]
     with pytest.raises(RuntimeError, match="rows \\[0\\]"):
         eng._check_room()
+
+
+def test_bench_traffic_is_reported_only_for_the_profiled_source(tmp_path, monkeypatch):
+    """A committed PMC traffic figure is used only while the kernel's source file (and
+    common.h) hash to the sha recorded when it was measured; otherwise traffic is null and
+    traffic_source says why."""
+    import importlib
+    import json
+    import sys
+
+    sys.path.insert(0, str(ROOT))
+    bench = importlib.import_module("bench")
+    sha = bench.kernel_source_sha("route_gateup_kernel<2>")
+    assert sha and sha == bench.kernel_source_sha("route_gateup_kernel<1>")
+    assert bench.kernel_source_sha("gemm_dma_kernel<true>") != sha  # defined in another file
+    assert bench.kernel_source_sha("no_such_kernel") is None
+    prof = tmp_path / "profiles"
+    prof.mkdir()
+    monkeypatch.setattr(bench, "ROOT", str(tmp_path))
+    rec = {"kernel_symbol": "route_gateup_kernel<2>", "source_sha": sha, "traffic_bytes_per_dispatch": 123.0}
+    (prof / "traffic_c1.json").write_text(json.dumps(rec))
+    t, src = bench.measured_traffic(1, "route_gateup_kernel<2> (small-family MoE)")
+    assert t == 123.0 and src["status"] == "measured on this source"
+    (prof / "traffic_c1.json").write_text(json.dumps(dict(rec, source_sha="0" * 16)))
+    t, src = bench.measured_traffic(1, "route_gateup_kernel<2> (small-family MoE)")
+    assert t is None and src["status"] == "stale"
+    t, src = bench.measured_traffic(2, "gemm_dma_kernel<true>")
+    assert t is None and src["status"] == "missing"
+
+
+def test_bench_mfma_summary_uses_the_timing_graph_dispatches(tmp_path):
+    """--mfma-summary keeps, per kernel symbol, only the last DOMINANT_DISPATCHES dispatches
+    (the bench's timing graph), both for the counters and for the trace durations."""
+    import csv
+    import importlib
+    import sys
+
+    sys.path.insert(0, str(ROOT))
+    bench = importlib.import_module("bench")
+    n = bench.DOMINANT_DISPATCHES
+    crow, trow, d = [], [], 0
+    for k, (mops, util, dur) in enumerate([(1.0, 90.0, 1000)] * 5 + [(1000.0, 10.0, 2000)] * n):
+        d += 1
+        crow.append({"Dispatch_Id": d, "Kernel_Name": "void kern<1>(int)", "Counter_Name": "MfmaUtil",
+                     "Counter_Value": util})
+        crow.append({"Dispatch_Id": d, "Kernel_Name": "void kern<1>(int)", "Counter_Name": "SQ_INSTS_VALU_MFMA_MOPS_BF16",
+                     "Counter_Value": mops})
+        trow.append({"Dispatch_Id": d, "Kernel_Name": "void kern<1>(int)", "Start_Timestamp": 10 * d,
+                     "End_Timestamp": 10 * d + dur})
+    for path, rows in ((tmp_path / "c.csv", crow), (tmp_path / "t.csv", trow)):
+        with open(path, "w", newline="") as f:
+            w = csv.DictWriter(f, fieldnames=list(rows[0]))
+            w.writeheader()
+            w.writerows(rows)
+    out = tmp_path / "m.md"
+    bench.mfma_summary(str(tmp_path / "c.csv"), str(tmp_path / "t.csv"), str(out), "t", "cmd")
+    line = [ln for ln in out.read_text().splitlines() if ln.startswith("| `kern<1>`")][0]
+    cells = [c.strip() for c in line.strip("|").split("|")]
+    assert cells[1] == str(n) and cells[2] == "10.0"
+    assert float(cells[3]) == round(1000 * 512 / 1e9, 3) and cells[4] == "2.0"

@@ -182,7 +182,8 @@ def test_run_cli_end_to_end(family, bsz):
 
 def test_bench_json_contract():
     """bench.py (the driver's entry point) prints ONE JSON line with the contract's keys, a
-    roofline object for the dominant kernel and (here skipped) no cpu_baseline."""
+    roofline object for the dominant kernel, the bsz=64 / 256 configs under "configs", and
+    (here skipped) no cpu_baseline."""
     import json
     import math
     import os
@@ -204,3 +205,13 @@ def test_bench_json_contract():
     roof = d["roofline"]
     assert roof["bound"] == "hbm" and roof["unit"] == "GB/s" and 0 < roof["frac"] < 1
     assert math.isclose(roof["frac"], roof["achieved"] / roof["peak"], rel_tol=1e-9)
+    assert roof["traffic_source"]["status"] in ("measured on this source", "stale", "missing", "other kernel")
+    # the metric's bsz=64 and bsz=256 ride along, timed in the same run
+    for key, B in (("C2", 64), ("C3", 256)):
+        c = d["configs"][key]
+        assert c["global_batch"] == B and c["kernel_family"] == "batch" and c["steps"] == 3
+        assert math.isclose(c["tok_s"], B * 1e3 / c["ms_per_step"], rel_tol=1e-3)
+        r = c["roofline"]
+        assert 0 < r["frac"] < 1 and math.isclose(r["frac"], r["achieved"] / r["peak"], rel_tol=1e-3)
+        sr = c["step_roofline"]
+        assert math.isclose(sr["frac_of_8TBps"], sr["bytes_per_step"] / (c["ms_per_step"] / 1e3) / 8e12, rel_tol=1e-3)
