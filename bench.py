@@ -71,17 +71,13 @@ CONFIGS = {
 
 
 def step_bytes(cfg, n_exp_per_layer: list[int], ctx_sum_per_layer: float, batch: int) -> float:
-    """Algorithmic HBM bytes of one decode step: every weight read once (attention,
-    router, the experts actually hit, shared experts, dense layer 0, lm_head, norms), the
-    new cache rows written and the compressed KV rows read (1,152 B per token per layer)."""
-    attn_w = 2048 * 3648 + 512 * 4096 + 2048 * 2048  # 13,762,560 elements per layer
-    expert = 3 * 2048 * 1408  # 8,650,752
-    shared = 3 * 2048 * 2816  # 17,301,504
-    dense = 3 * 2048 * 10944  # 67,239,936
-    head = 102400 * 2048
-    elems = cfg.n_layers * attn_w + cfg.n_layers * 4608 + sum(n * expert + shared for n in n_exp_per_layer) \
-        + dense + head + 2048
-    return 2 * elems + 26 * 64 * 2048 * 2 + 4096 * batch + 1152 * ctx_sum_per_layer * cfg.n_layers
+    """Algorithmic HBM bytes of one decode step (dsv2lite.roofline.step_bytes): every weight
+    read once (attention, router, the experts actually hit, shared experts, dense layer 0,
+    lm_head, norms), the embedding rows and the compressed KV rows read (1,152 B per token
+    per layer)."""
+    from dsv2lite.roofline import step_bytes as _sb
+
+    return float(_sb(cfg, n_exp_per_layer, ctx_sum_per_layer, batch))
 
 
 def time_dominant_kernel(eng, family: str, reps: int = 4) -> dict:
@@ -631,7 +627,8 @@ def run_config(key, w, args, cfg, dev) -> dict:
     others = time_other_kernels(eng, family, [p + 1 for p in pos_now])
     res = {"workload": spec["workload"], "global_batch": B, "seq_len": max(lens), "kernel_family": family,
            "mla_path": args.mla_path if family == "small" else "split", "prompt_tokens": sum(lens),
-           "tok_s": value, "ms_per_step": ms, "steps": steps, "warmup": warm, "roofline": roof,
+           "tok_s": value, "ms_per_step": ms, "steps": steps, "warmup": warm, "kernels_per_step": eng.kernels_per_step,
+           "roofline": roof,
            "other_kernels": others,
            "step_roofline": {"bytes_per_step": sb, "achieved_GBps": sb / (ms / 1e3) / 1e9,
                              "frac_of_8TBps": sb / (ms / 1e3) / HBM_PEAK, "distinct_experts_per_layer": n_exp},
@@ -714,6 +711,7 @@ def main() -> None:
                    "kernel_family": r["kernel_family"], "mla_path": r["mla_path"],
                    "prompt_tokens": r["prompt_tokens"], "parallelism": "none (1 GPU)"},
         "roofline": r["roofline"], "step_roofline": r["step_roofline"], "other_kernels": r["other_kernels"],
+        "kernels_per_step": r["kernels_per_step"],
         "setup_s": dict(r["setup_s"], init_weights=round(t_init, 2)),
     }
     if args.config == "all":

@@ -124,6 +124,18 @@ class RowBuffers:
         self.max_tiles = math.ceil(self._routes / tile_tokens) + self._n_experts
 
 
+def _graph_node_count(g: torch.cuda.CUDAGraph) -> int:
+    """Nodes of a captured (kept, not yet instantiated) graph, by hipGraphGetNodes."""
+    import ctypes
+
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    n = ctypes.c_size_t(0)
+    rc = hip.hipGraphGetNodes(ctypes.c_void_p(g.raw_cuda_graph()), None, ctypes.byref(n))
+    if rc != 0:
+        raise RuntimeError(f"hipGraphGetNodes failed with {rc}")
+    return int(n.value)
+
+
 class DecodeEngine:
     def __init__(self, weights: ModelWeights, capacities: list[int], family: str = "small",
                  max_prefill_rows: int = 1024, device="cuda", mla_path: str = "fused"):
@@ -152,6 +164,7 @@ class DecodeEngine:
         self.fused_mla = family == "small" and self.max_pos <= FUSED_MLA_MAX_CTX and mla_path == "fused"
         self.max_prefill_rows = max_prefill_rows
         self.graph = None
+        self.kernels_per_step = 0  # set by capture()
         self._host_pos = [0] * self.B  # host mirror of cache.pos, for capacity checks only
 
     # ------------------------------------------------------------------ layers
@@ -398,14 +411,18 @@ class DecodeEngine:
 
     def capture(self) -> torch.cuda.CUDAGraph:
         """Record one step() into a graph (positions/ids advance on every replay).  The batch
-        family first picks its MoE token tile from one eager step (tune_moe_tiles)."""
+        family first picks its MoE token tile from one eager step (tune_moe_tiles).  Sets
+        kernels_per_step to the number of nodes of the captured graph (every node is a kernel
+        launch: the step records no copies or memsets)."""
         if self.family == "batch" and not getattr(self, "_moe_tiles_tuned", False):
             self.tune_moe_tiles()
         saved = list(self._host_pos)
-        g = torch.cuda.CUDAGraph()
+        g = torch.cuda.CUDAGraph(keep_graph=True)
         with torch.cuda.graph(g):
             self.step()
         self._host_pos = saved
+        self.kernels_per_step = _graph_node_count(g)
+        g.instantiate()
         self.graph = g
         return g
 

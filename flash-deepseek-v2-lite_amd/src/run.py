@@ -2,18 +2,25 @@
 src/run.py; same flags, same JSON report, same TPS definition).
 
     python flash-deepseek-v2-lite_amd/src/run.py --kernel-family small|batch \
+        [--model-path DIR [--prompt TEXT]] \
         [--batch-size B | --batch-sizes "1 64 256"] [--max-new-tokens 100] \
         [--prompt-len 24 | --prompt-len-range LO HI] [--config 1|2|3] \
         [--dump-token-ids] [--dump-step-trace] [--json-out FILE]
 
-Differences from the reference CLI, all forced by this build having no
-checkpoint and no tokenizer (no network, no /data): the model is the seeded
-random-init DeepSeek-V2-Lite (N(0,0.02) bf16, seed --seed), and the prompt is
-``--prompt-len`` uniform random token ids (seed --prompt-seed).  As in the
-reference (run.py:733-741) one prompt is replicated across the batch unless
-``--prompt-len-range`` draws one length (and prompt) per row.  ``--config N``
-selects benchmark config N (1: bsz=1 prompt 128 small; 2: bsz=64 lengths
-U[256,1024] batch; 3: bsz=256 prompt 2048 batch).
+With ``--model-path`` (a local DeepSeek-V2-Lite(-Chat) directory: config.json, safetensors
+shards, tokenizer files) the weights come from the checkpoint and the prompt is ``--prompt``
+through the tokenizer's chat template with the generation prompt, replicated across the
+batch -- the reference's run (run.py:14, 719-741; default prompt "Write me a 500 word
+novel.").  Without it (there is no checkpoint on these machines) the model is the seeded
+random-init DeepSeek-V2-Lite (N(0,0.02) bf16, seed --seed) and the prompt ``--prompt-len``
+uniform random token ids (seed --prompt-seed), one prompt replicated across the batch as in
+the reference unless ``--prompt-len-range`` draws one length (and prompt) per row.
+``--config N`` selects benchmark config N (1: bsz=1 prompt 128 small; 2: bsz=64 lengths
+U[256,1024] batch; 3: bsz=256 prompt 2048 batch, one prompt per row).
+
+Beside the reference's JSON fields the report carries hbm_bytes_per_step (the algorithmic
+bytes of one step, dsv2lite.roofline), roofline_fraction (those bytes / the mean step time /
+8 TB/s) and kernels_per_step (kernel nodes of the captured step).
 
 Flow per batch size (run.py:591-688): prefill -> snapshot -> 3 eager warmup
 steps (each followed by a restore) -> capture one step into a hipGraph ->
@@ -36,6 +43,7 @@ if _PKG not in sys.path:
 import torch  # noqa: E402
 
 DEFAULT_MAX_NEW_TOKENS = 100
+DEFAULT_PROMPT = "Write me a 500 word novel."
 DEFAULT_PROMPT_LEN = 24  # length of the reference's chat-templated default prompt
 GRAPH_WARMUP_STEPS = 3
 PATH_NAMES = {"small": "hip_small_gemv_graph", "batch": "hip_batching_graph"}
@@ -59,7 +67,9 @@ def set_kernel_family(kernel_family: str) -> str:
 def parse_args(argv: list[str] | None = None) -> argparse.Namespace:
     p = argparse.ArgumentParser(description="DeepSeek-V2-Lite decode using a selectable HIP kernel family.")
     p.add_argument("--model-path", type=str, default=None,
-                   help="not supported: this build has no checkpoint loader (random-init weights only)")
+                   help="local checkpoint directory (config.json, *.safetensors, tokenizer); random-init weights "
+                        "without it")
+    p.add_argument("--prompt", type=str, default=DEFAULT_PROMPT, help="user prompt (with --model-path)")
     p.add_argument("--max-new-tokens", type=int, default=DEFAULT_MAX_NEW_TOKENS)
     p.add_argument("--batch-size", type=int, default=1)
     p.add_argument("--batch-sizes", type=str, default=None, help='Comma/space separated sweep, e.g. "1 2 4".')
@@ -116,6 +126,7 @@ def make_prompts(args: argparse.Namespace, batch_size: int, vocab: int) -> list[
 def run_graph_decode(weights, prompts: list[torch.Tensor], family: str, max_new_tokens: int, device,
                      dump_token_ids: bool = False, dump_step_trace: bool = False) -> dict:
     import dsv2lite
+    from dsv2lite.roofline import step_bytes
 
     B = len(prompts)
     lens = [int(p.numel()) for p in prompts]
@@ -126,6 +137,11 @@ def run_graph_decode(weights, prompts: list[torch.Tensor], family: str, max_new_
     torch.cuda.synchronize()
     prefill_s = time.perf_counter() - t0
     snap = eng.snapshot()
+    rec: list = []
+    eng.step(record=rec)  # the routed experts each layer hits, for the byte count of a step
+    n_exp = [int(torch.unique(r[2]).numel()) for r in rec if r[0] == "router"]
+    del rec
+    eng.restore(snap)
     collect = dump_token_ids or dump_step_trace
     gen = [[t] for t in first.cpu().tolist()] if collect else None
     trace = []
@@ -151,9 +167,12 @@ def run_graph_decode(weights, prompts: list[torch.Tensor], family: str, max_new_
     decode_s = time.perf_counter() - t0
     eng.check_errors()
     out_ids = gen[0] if (gen is not None and B == 1) else gen
+    steps = max(max_new_tokens - 1, 0)
+    nbytes = step_bytes(eng.cfg, n_exp, sum(n + 1 + (steps - 1) / 2 for n in lens), B)
     return {"batch_size": B, "path": PATH_NAMES[family], "generated_ids": out_ids,
-            "decode_tokens": B * max(max_new_tokens - 1, 0), "prefill_seconds": prefill_s,
-            "decode_seconds": decode_s, "step_trace": trace, "prompt_lens": lens}
+            "decode_tokens": B * steps, "prefill_seconds": prefill_s,
+            "decode_seconds": decode_s, "step_trace": trace, "prompt_lens": lens, "hbm_bytes_per_step": nbytes,
+            "kernels_per_step": eng.kernels_per_step, "steps": steps}
 
 
 def _trace_entry(step: int, ids: list[int], positions: list[int]) -> dict:
@@ -170,7 +189,12 @@ def build_result(run: dict, include_token_ids: bool, include_step_trace: bool) -
     ds, dt = run["decode_seconds"], run["decode_tokens"]
     r = {"batch_size": run["batch_size"], "path": run["path"], "ttft_ms": run["prefill_seconds"] * 1000.0,
          "tps": dt / ds if ds > 0 else 0.0, "decode_tokens": dt,
-         "prompt_lens": run["prompt_lens"] if len(set(run["prompt_lens"])) > 1 else run["prompt_lens"][0]}
+         "prompt_lens": run["prompt_lens"] if len(set(run["prompt_lens"])) > 1 else run["prompt_lens"][0],
+         "hbm_bytes_per_step": run["hbm_bytes_per_step"], "kernels_per_step": run["kernels_per_step"]}
+    if ds > 0 and run["steps"] > 0:
+        from dsv2lite.roofline import roofline_fraction
+
+        r["roofline_fraction"] = roofline_fraction(run["hbm_bytes_per_step"], ds / run["steps"])
     if include_token_ids:
         r["generated_token_ids"] = run["generated_ids"]
     if include_step_trace:
@@ -181,20 +205,27 @@ def build_result(run: dict, include_token_ids: bool, include_step_trace: bool) -
 def main(argv: list[str] | None = None) -> dict:
     args = parse_args(argv)
     family = set_kernel_family(args.kernel_family)
-    if args.model_path is not None:
-        raise NotImplementedError("--model-path: checkpoint loading is not part of this build (random-init only)")
     if not torch.cuda.is_available():
         raise RuntimeError("a ROCm GPU is required for this benchmark")
     sizes = parse_batch_sizes(args)
     import dsv2lite
     from src.hardware_info import collect_hardware_info
 
-    cfg = dsv2lite.DSV2Config() if args.layers is None else dsv2lite.DSV2Config(n_layers=args.layers)
     dev = torch.device(args.device)
-    weights = dsv2lite.init_weights(cfg, device=dev, seed=args.seed)
+    chat_ids = None
+    if args.model_path is not None:
+        from dsv2lite.checkpoint import chat_prompt_ids, load_tokenizer, load_weights
+
+        weights = load_weights(args.model_path, device=dev, n_layers=args.layers)
+        cfg = weights.cfg
+        chat_ids = chat_prompt_ids(load_tokenizer(args.model_path), args.prompt)
+    else:
+        cfg = dsv2lite.DSV2Config() if args.layers is None else dsv2lite.DSV2Config(n_layers=args.layers)
+        weights = dsv2lite.init_weights(cfg, device=dev, seed=args.seed)
     results = []
     for B in sizes:
-        prompts = make_prompts(args, B, cfg.vocab)
+        # the reference replicates the chat-templated prompt across the batch (run.py:739-741)
+        prompts = [chat_ids.clone() for _ in range(B)] if chat_ids is not None else make_prompts(args, B, cfg.vocab)
         run = run_graph_decode(weights, prompts, family, args.max_new_tokens, dev, args.dump_token_ids,
                                args.dump_step_trace)
         results.append(build_result(run, args.dump_token_ids, args.dump_step_trace))

@@ -164,19 +164,23 @@ def test_run_cli_parsing_matches_reference_rules():
     rep = R.make_prompts(R.parse_args(["--prompt-len", "24"]), 3, 1000)
     assert all(torch.equal(rep[0], x) for x in rep) and rep[0].numel() == 24
     r = R.build_result({"batch_size": 2, "path": "hip_batching_graph", "prefill_seconds": 0.5, "decode_seconds": 2.0,
-                        "decode_tokens": 198, "generated_ids": [[1], [2]], "step_trace": [], "prompt_lens": [24, 24]},
+                        "decode_tokens": 198, "generated_ids": [[1], [2]], "step_trace": [], "prompt_lens": [24, 24],
+                        "hbm_bytes_per_step": 8e9, "kernels_per_step": 300, "steps": 99},
                        True, False)
     assert r["tps"] == 99.0 and r["ttft_ms"] == 500.0 and r["prompt_lens"] == 24 and "step_trace" not in r
+    # the run report's roofline fields: bytes per step / mean step time / 8 TB/s
+    assert r["kernels_per_step"] == 300 and math.isclose(r["roofline_fraction"], 8e9 / (2.0 / 99) / 8e12)
 
 
-def test_run_cli_refuses_checkpoint_and_needs_gpu():
+def test_run_cli_needs_gpu():
     from src import run as R
 
-    with pytest.raises(NotImplementedError, match="checkpoint"):
-        R.main(["--model-path", "/data/models/DeepSeek-V2-Lite-Chat"])
     if not torch.cuda.is_available():
         with pytest.raises(RuntimeError, match="GPU is required"):
             R.main([])
+        with pytest.raises(RuntimeError, match="GPU is required"):
+            R.main(["--model-path", "/data/models/DeepSeek-V2-Lite-Chat"])
+    assert R.parse_args([]).prompt == "Write me a 500 word novel."  # the reference's default (run.py:17)
 
 
 def test_bench_pmc_traffic_scaling_and_tail(tmp_path):
