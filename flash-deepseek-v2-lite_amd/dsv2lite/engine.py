@@ -138,7 +138,10 @@ def _graph_node_count(g: torch.cuda.CUDAGraph) -> int:
 
 class DecodeEngine:
     def __init__(self, weights: ModelWeights, capacities: list[int], family: str = "small",
-                 max_prefill_rows: int = 1024, device="cuda", mla_path: str = "fused"):
+                 max_prefill_rows: int = 1024, device="cuda", mla_path: str = "fused", moe_tile: int | None = None):
+        """capacities: cache tokens of each row (slot).  moe_tile (batch family): fix the
+        grouped MoE token tile (16, 32 or 64) instead of choosing it from the routing of one
+        eager step at capture -- for a serving loop whose batch changes under one graph."""
         if family not in FAMILIES:
             raise ValueError(f"Unknown kernel family: {family}")
         if mla_path not in ("split", "fused"):
@@ -157,6 +160,9 @@ class DecodeEngine:
         self.ids = torch.zeros(self.B, dtype=torch.int64, device=device)
         self.logits = torch.empty(self.B, cfg.vocab, dtype=torch.float32, device=device)
         self.buf = RowBuffers(cfg, self.B, family, self.max_pos, device)
+        if family == "batch" and moe_tile is not None:
+            self.buf.set_tile_tokens(moe_tile)
+            self._moe_tiles_tuned = True
         self._amax = torch.empty(max(0, _hip.lib.dsv2_lm_head_argmax_workspace_size(min(self.B, 8))),
                                  dtype=torch.uint8, device=device)
         # small family: one fused workgroup per (row, head) while contexts are short; the
@@ -166,6 +172,7 @@ class DecodeEngine:
         self.graph = None
         self.kernels_per_step = 0  # set by capture()
         self._host_pos = [0] * self.B  # host mirror of cache.pos, for capacity checks only
+        self._free: set[int] = set()  # retired slots (continuous batching)
 
     # ------------------------------------------------------------------ layers
     def _attention(self, L, li: int, b: RowBuffers, R: int, pos, base, cap, family: str, st: int) -> None:
@@ -327,22 +334,63 @@ class DecodeEngine:
         a recorded decode step (row b = sequence b)."""
         if len(prompts) != self.B:
             raise ValueError(f"need {self.B} prompts, got {len(prompts)}")
+        self._free.clear()
+        return self._prefill_slots(list(range(self.B)), prompts, record)
+
+    def insert(self, slot: int, prompt: torch.Tensor) -> int:
+        """Continuous batching: start a new sequence in `slot` (free, or to be overwritten)
+        while the captured graph stays as it is.  The prompt is prefilled into the slot's own
+        cache rows only, its position and next id are set in place (the graph reads them from
+        the same device tensors), and the slot's first greedy token is returned.  The other
+        rows are untouched.  The slot's capacity must hold the prompt plus the tokens it will
+        generate."""
+        if not 0 <= slot < self.B:
+            raise ValueError(f"slot {slot} out of range [0, {self.B})")
+        self._prefill_slots([slot], [prompt])
+        self._free.discard(slot)
+        return int(self.ids[slot].item())
+
+    def retire(self, slot: int) -> None:
+        """Continuous batching: end the sequence in `slot`.  The captured step keeps running
+        every row, so a free slot goes on decoding throw-away tokens inside its own cache rows;
+        its position restarts at 0 now and whenever it would reach its capacity (a device write
+        before the replay), so it never stops the batch.  insert() reuses it."""
+        if not 0 <= slot < self.B:
+            raise ValueError(f"slot {slot} out of range [0, {self.B})")
+        self._free.add(slot)
+        self._reset_slots([slot])
+
+    @property
+    def free_slots(self) -> list[int]:
+        return sorted(self._free)
+
+    def _reset_slots(self, slots: list[int]) -> None:
+        idx = torch.tensor(slots, dtype=torch.int64, device=self.device)
+        self.cache.pos.index_fill_(0, idx, 0)
+        for b in slots:
+            self._host_pos[b] = 0
+
+    def _prefill_slots(self, slots: list[int], prompts: list[torch.Tensor], record: list | None = None) -> torch.Tensor:
         lens = [int(p.numel()) for p in prompts]
-        if min(lens) < 1:
+        if not slots or min(lens) < 1:
             raise ValueError("empty prompt")
-        for b, n in enumerate(lens):
+        if len(set(slots)) != len(slots):
+            raise ValueError(f"slots repeat: {slots}")
+        for b, n in zip(slots, lens):
             if n >= self.cache.capacities[b]:
-                raise ValueError(f"prompt {b} of length {n} does not fit capacity {self.cache.capacities[b]}")
+                raise ValueError(f"prompt of length {n} does not fit slot {b} (capacity {self.cache.capacities[b]})")
         dev = self.device
-        seq = torch.cat([torch.full((n,), b, dtype=torch.int64) for b, n in enumerate(lens)])
+        k = len(slots)
+        seq = torch.cat([torch.full((n,), j, dtype=torch.int64) for j, n in enumerate(lens)])  # prompt index
+        slot_t = torch.tensor(slots, dtype=torch.int64)
         posv = torch.cat([torch.arange(n, dtype=torch.int32) for n in lens])
         ids_all = torch.cat([p.reshape(-1).to(torch.int64).cpu() for p in prompts])
-        base_all = self.cache.base.cpu()[seq]
-        cap_all = self.cache.cap.cpu()[seq]
+        base_all = self.cache.base.cpu()[slot_t[seq]]
+        cap_all = self.cache.cap.cpu()[slot_t[seq]]
         total = seq.numel()
         max_rows = min(self.max_prefill_rows, total)
         pb = RowBuffers(self.cfg, max_rows, "batch", self.max_pos, dev)
-        last_h = torch.empty(self.B, self.cfg.hidden, dtype=BF16, device=dev)
+        last_h = torch.empty(k, self.cfg.hidden, dtype=BF16, device=dev)
         last_xn = torch.empty_like(last_h)
         st = _hip.stream_ptr(dev)
         acc: dict = {}
@@ -364,22 +412,30 @@ class DecodeEngine:
                     key = (r[0], r[1], j)
                     if key not in acc:
                         acc[key] = torch.zeros((self.B,) + tuple(t.shape[1:]), dtype=t.dtype, device=dev)
-                    acc[key].index_copy_(0, which, t)
+                    acc[key].index_copy_(0, slot_t.to(dev)[which], t)
             if rows.numel():
                 last_h.index_copy_(0, which, pb.h[rows_d])
                 last_xn.index_copy_(0, which, pb.xn[rows_d])
         # final norm is fused into the last layer's combine (pb.xn); lm_head + argmax
         c = self.cfg
-        call("dsv2_gemm_bf16", ptr(last_xn), c.hidden, 0, self.B, c.hidden, ptr(self.w.lm_head), 0, c.vocab, 1, None,
-             0, ptr(self.logits), c.vocab, 0, LINEAR_OUT_F32, st)
-        call("dsv2_argmax_f32", ptr(self.logits), self.B, c.vocab, ptr(self.ids), None, st)
-        self.cache.pos.copy_(torch.tensor(lens, dtype=torch.int32))
-        self._host_pos = list(lens)
+        whole = slots == list(range(self.B))
+        logits = self.logits if whole else torch.empty(k, c.vocab, dtype=torch.float32, device=dev)
+        ids = self.ids if whole else torch.empty(k, dtype=torch.int64, device=dev)
+        call("dsv2_gemm_bf16", ptr(last_xn), c.hidden, 0, k, c.hidden, ptr(self.w.lm_head), 0, c.vocab, 1, None,
+             0, ptr(logits), c.vocab, 0, LINEAR_OUT_F32, st)
+        call("dsv2_argmax_f32", ptr(logits), k, c.vocab, ptr(ids), None, st)
+        slot_d = slot_t.to(dev)
+        if not whole:
+            self.logits.index_copy_(0, slot_d, logits)
+            self.ids.index_copy_(0, slot_d, ids)
+        self.cache.pos.index_copy_(0, slot_d, torch.tensor(lens, dtype=torch.int32, device=dev))
+        for b, n in zip(slots, lens):
+            self._host_pos[b] = n
         if record is not None:
-            for (kind, li, j) in sorted(acc, key=lambda k: (k[1], ("attn", "layer", "router").index(k[0]), k[2])):
+            for (kind, li, j) in sorted(acc, key=lambda kk: (kk[1], ("attn", "layer", "router").index(kk[0]), kk[2])):
                 if j == 0:
                     record.append((kind, li) + tuple(acc[(kind, li, jj)] for jj in range(3) if (kind, li, jj) in acc))
-        self.buf.h.copy_(last_h)
+        self.buf.h.index_copy_(0, slot_d, last_h)
         del pb
         return self.ids
 
@@ -434,8 +490,13 @@ class DecodeEngine:
 
     def _check_room(self) -> None:
         """Every row needs a free slot for its next token: pos[b] + 1 <= capacity[b]
-        (the reference raises on overflow, src/run.py:131-134)."""
-        full = [b for b, (p, c) in enumerate(zip(self._host_pos, self.cache.capacities)) if p + 1 > c]
+        (the reference raises on overflow, src/run.py:131-134).  Retired slots restart at 0
+        (outside graph capture: the reset is an eager device write)."""
+        caps = self.cache.capacities
+        wrap = [b for b in self._free if self._host_pos[b] + 1 > caps[b]]
+        if wrap and not torch.cuda.is_current_stream_capturing():
+            self._reset_slots(wrap)
+        full = [b for b, (p, c) in enumerate(zip(self._host_pos, caps)) if p + 1 > c]
         if full:
             raise RuntimeError(f"KV cache capacity exhausted for rows {full[:8]} "
                                f"(positions {[self._host_pos[b] for b in full[:8]]}, "
