@@ -251,6 +251,7 @@ def test_engine_capacity_check_is_per_row():
 
     eng = object.__new__(DecodeEngine)
     eng.cache = SimpleNamespace(capacities=[12, 74])
+    eng._free = set()
     eng._host_pos = [10, 10]
     eng._check_room()  # slot 10 < 12 for row 0
     eng._host_pos = [11, 11]
