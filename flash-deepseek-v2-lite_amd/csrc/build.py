@@ -23,7 +23,7 @@ ROOT = os.path.dirname(PKG)
 INCLUDE = os.path.join(ROOT, "include")
 OUT = os.path.join(PKG, "triton_kernels", "libdsv2lite_hip.so")
 OBJDIR = os.path.join(PKG, "_build")
-SOURCES = ["elementwise.hip", "gemv.hip", "gemm.hip", "mla.hip", "mla_small.hip", "moe.hip", "attention_expanded.hip"]
+SOURCES = ["elementwise.hip", "gemv.hip", "gemm.hip", "mla.hip", "mla_small.hip", "moe.hip", "attention_expanded.hip", "mla_prefill.hip"]
 ARCH = os.environ.get("DSV2_OFFLOAD_ARCH", "gfx950")
 
 CXXFLAGS = [

@@ -1,0 +1,187 @@
+// Prefill attention of DeepSeek-V2's MLA in its expanded form (the prompt's attention, run
+// before the q_len = 1 decode path): per head h, softmax(scale * q . k) v over the causal
+// prefix, with
+//   q = [q_nope (128, from the qkv_a output) | RoPE(q_pe) (64, from mla_prepare)]
+//   k = [k_nope = W_UK_h c (128, expanded) | RoPE(k_pe) (64, the cache row's tail)]
+//   v = W_UV_h c (128, expanded)
+// where c is the kv-normalised latent of the compressed cache.  The expanded form needs
+// 320 multiply-adds per (query, key, head) against 1088 for the absorbed (latent) form the
+// decode step uses, which pays off when every cached token is attended by many queries.
+//
+// One 256-thread workgroup per (tile of <= 64 consecutive query tokens of one sequence,
+// head); wave w owns queries 16w .. 16w + 15 of the tile.  Keys go in 32-token tiles,
+// double-buffered in LDS (the next tile's 16-byte chunks in registers meanwhile):
+//   S^T = K Q^T   two 16-key blocks x 6 k-steps of v_mfma_f32_16x16x32_bf16 (queries = N)
+//   online softmax per query (column), fp32, the causal mask key <= query position
+//   O^T += V^T P^T  8 x 16 value dims; V^T fragments by transposed LDS reads
+//                   (ds_read_b64_tr_b16), P^T packed to bf16 in the order the reads give.
+#include "common.h"
+
+namespace {
+constexpr int kKT = 32;         // keys per tile
+constexpr int kQK = 192;        // q.k dims: 128 nope + 64 rope
+constexpr int kVD = 128;        // value dims
+constexpr int kKRow = kQK + 8;  // padded LDS rows (elements): 400 B
+constexpr int kVRow = kVD + 8;  // 272 B
+constexpr int kHeads = 16;
+constexpr int kCacheRow = 576;
+constexpr int kChunksPerKey = kQK / 8 + kVD / 8;  // 16-byte chunks per key: 16 nope + 8 rope + 16 v = 40
+constexpr int kLoads = kKT * kChunksPerKey / 256;  // per thread per tile: 5
+}  // namespace
+
+__global__ __launch_bounds__(256, 2) void mla_prefill_kernel(
+    const bf16_t* __restrict__ qkva, int64_t qs, const bf16_t* __restrict__ qrope, int64_t qrs,
+    const bf16_t* __restrict__ cache, int64_t cache_rows, const bf16_t* __restrict__ knope,
+    const bf16_t* __restrict__ vexp, int64_t exp_lo, int64_t exp_rows, int rows, const int4* __restrict__ tiles,
+    float scale_log2, bf16_t* __restrict__ out, int64_t os) {
+  __shared__ __attribute__((aligned(16))) bf16_t kt[2][kKT * kKRow];
+  __shared__ __attribute__((aligned(16))) bf16_t vt[2][kKT * kVRow];
+  const int4 tl = tiles[blockIdx.x];
+  const int h = blockIdx.y;
+  // every index derived from the tile table is clamped into the buffers the host described
+  // (a malformed table gives wrong numbers, never an access outside them)
+  const int r0 = min(max(tl.x, 0), rows - 1), nr = min(max(tl.y, 1), min(64, rows - r0)), p0 = max(tl.z, 0);
+  const int64_t sb = tl.w;  // cache row of position 0 of the tile's sequence
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, li = lane & 15, kg = lane >> 4;
+  const int j = wv * 16 + li;                  // this lane's query (column) in the tile
+  const int r = r0 + min(j, nr - 1);           // its row (queries past the tile repeat the last one)
+  const int qp = p0 + j;                       // its position
+  const int nkv = p0 + nr;                     // keys [0, nkv) of the sequence
+  const int ntiles = (nkv + kKT - 1) / kKT;
+
+  bf16x8_t qf[6];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) qf[kk] = as_bf16x8(ldg16(qkva + (int64_t)r * qs + h * 192 + kk * 32 + kg * 8));
+#pragma unroll
+  for (int kk = 4; kk < 6; ++kk)
+    qf[kk] = as_bf16x8(ldg16(qrope + (int64_t)r * qrs + h * kCacheRow + 512 + (kk - 4) * 32 + kg * 8));
+
+  uint4 st[kLoads];
+  auto load_tile = [&](int t0) {
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int c = tid + 256 * i;
+      const int key = c / kChunksPerKey, part = c % kChunksPerKey;
+      const int64_t row = sb + min(t0 + key, nkv - 1);  // past the prefix: the last key (masked)
+      const int64_t crow = min(max(row, (int64_t)0), cache_rows - 1);
+      const int64_t erow = min(max(row - exp_lo, (int64_t)0), exp_rows - 1);
+      const bf16_t* src;
+      if (part < 16)
+        src = knope + erow * (kHeads * kVD) + h * kVD + part * 8;
+      else if (part < 24)
+        src = cache + crow * kCacheRow + 512 + (part - 16) * 8;
+      else
+        src = vexp + erow * (kHeads * kVD) + h * kVD + (part - 24) * 8;
+      st[i] = ldg16(src);
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int c = tid + 256 * i;
+      const int key = c / kChunksPerKey, part = c % kChunksPerKey;
+      bf16_t* dst = part < 24 ? &kt[buf][key * kKRow + part * 8] : &vt[buf][key * kVRow + (part - 24) * 8];
+      *reinterpret_cast<uint4*>(dst) = st[i];
+    }
+  };
+
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+
+  float m_run = -INFINITY, l_run = 0.f;
+  floatx4_t acc[8];
+#pragma unroll
+  for (int mb = 0; mb < 8; ++mb) acc[mb] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+
+  for (int it = 0; it < ntiles; ++it) {
+    const int buf = it & 1;
+    const int t0 = it * kKT;
+    if (it + 1 < ntiles) load_tile(t0 + kKT);
+    // S^T: sc[blk][e] = score(key t0 + blk*16 + 4kg + e, query j)
+    floatx4_t sc[2];
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) {
+      floatx4_t sp = floatx4_t{0.f, 0.f, 0.f, 0.f};
+      const bf16_t* kr = &kt[buf][(blk * 16 + li) * kKRow + kg * 8];
+#pragma unroll
+      for (int kk = 0; kk < 6; ++kk) sp = mfma16x16x32(*reinterpret_cast<const bf16x8_t*>(kr + kk * 32), qf[kk], sp);
+      sc[blk] = sp;
+    }
+    float p[8];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int kp = t0 + blk * 16 + 4 * kg + e;
+        const float v = kp <= qp ? sc[blk][e] * scale_log2 : -INFINITY;
+        p[blk * 4 + e] = v;
+        mx = fmaxf(mx, v);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);  // finite: key 0 is in the first tile of every query
+    const float alpha = exp2f(m_run - m_new);
+    float rsum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      p[i] = exp2f(p[i] - m_new);
+      rsum += p[i];
+    }
+    rsum += __shfl_xor(rsum, 16, 64);
+    rsum += __shfl_xor(rsum, 32, 64);
+    l_run = l_run * alpha + rsum;
+    m_run = m_new;
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) acc[mb] *= alpha;
+    // O^T += V^T P^T: lane (li, kg) addresses key 4kg + li/4 (then 16 + 4kg + li/4), dims
+    // 16mb + 4(li % 4) .. +3, and receives V[4kg + e][16mb + li] (then V[16 + 4kg + e][..]),
+    // the keys of its P^T column in the same order
+    const bf16x8_t pb = as_bf16x8(pack8(p));
+    const bf16_t* vp = &vt[buf][(4 * kg + (li >> 2)) * kVRow + 4 * (li & 3)];
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) {
+      const uint2 lo = lds_read_tr16(vp + mb * 16), hi = lds_read_tr16(vp + mb * 16 + 16 * kVRow);
+      acc[mb] = mfma16x16x32(as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y)), pb, acc[mb]);
+    }
+    // buffer buf ^ 1 was last read in iteration it - 1, which every wave finished before
+    // that iteration's closing barrier
+    if (it + 1 < ntiles) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+  if (j < nr) {
+    const float inv = 1.f / l_run;
+    bf16_t* o = out + (int64_t)(r0 + j) * os + h * kVD + 4 * kg;
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) {
+      uint2 w;
+      w.x = pack2(acc[mb][0] * inv, acc[mb][1] * inv);
+      w.y = pack2(acc[mb][2] * inv, acc[mb][3] * inv);
+      *reinterpret_cast<uint2*>(o + mb * 16) = w;
+    }
+  }
+}
+
+extern "C" int dsv2_mla_prefill_attention(const void* qkva, int64_t qkva_stride, const void* q_rope,
+                                          int64_t q_rope_stride, int rows, const void* cache, int64_t cache_rows,
+                                          const void* k_nope, const void* v, int64_t exp_lo, int64_t exp_rows,
+                                          const int32_t* tiles, int n_tiles, float softmax_scale, void* out,
+                                          int64_t out_stride, void* stream) {
+  DSV2_REQUIRE(qkva && q_rope && cache && k_nope && v && tiles && out, DSV2_E_NULL,
+               "mla_prefill_attention: null pointer");
+  DSV2_REQUIRE(n_tiles >= 0 && n_tiles <= 0x7fffffff && exp_lo >= 0 && qkva_stride >= 3648 &&
+                   q_rope_stride >= kHeads * kCacheRow && out_stride >= kHeads * kVD && rows >= 0 &&
+                   cache_rows > 0 && exp_rows > 0,
+               DSV2_E_SHAPE, "mla_prefill_attention: bad shape");
+  DSV2_REQUIRE(dsv2_aligned16(qkva) && dsv2_aligned16(q_rope) && dsv2_aligned16(cache) && dsv2_aligned16(k_nope) &&
+                   dsv2_aligned16(v) && dsv2_aligned16(tiles) && dsv2_aligned16(out) && qkva_stride % 8 == 0 &&
+                   q_rope_stride % 8 == 0 && out_stride % 4 == 0,
+               DSV2_E_ALIGN, "mla_prefill_attention: alignment");
+  if (n_tiles == 0 || rows == 0) return DSV2_OK;
+  hipLaunchKernelGGL(mla_prefill_kernel, dim3(n_tiles, kHeads), dim3(256), 0, (hipStream_t)stream,
+                     (const bf16_t*)qkva, qkva_stride, (const bf16_t*)q_rope, q_rope_stride, (const bf16_t*)cache,
+                     cache_rows, (const bf16_t*)k_nope, (const bf16_t*)v, exp_lo, exp_rows, rows, (const int4*)tiles,
+                     softmax_scale * 1.4426950408889634f, (bf16_t*)out, out_stride);
+  return dsv2_launch_status("mla_prefill_attention");
+}

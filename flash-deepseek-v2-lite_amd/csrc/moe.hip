@@ -488,41 +488,45 @@ extern "C" int dsv2_moe_route_down(const void* hbuf, int rows, const int32_t* id
 // batch family bucketing: one workgroup of 16 waves.  Routes are processed in
 // 64-route chunks; a route's slot = expert start + routes of the same expert in
 // earlier chunks + earlier lanes of its own chunk, so the order is stable in the
-// route index and the result is deterministic (no atomics).
+// route index and the result is deterministic (no atomics).  Only the per-chunk counts
+// live in LDS (96 KB at the 49,152-route maximum, the prefill's 8192-row chunks); a route's
+// rank inside its chunk is recomputed from the same ballots when it is placed.
 // ---------------------------------------------------------------------------
-constexpr int kMaxRoutes = 8192;
+constexpr int kMaxRoutes = 49152;
 constexpr int kMaxChunks = kMaxRoutes / 64;
+
+// expert of route r (kE when r is past the routes), and its rank among the lanes of its
+// 64-route chunk that hold the same expert; `last` is set on the chunk's last such lane
+__device__ __forceinline__ int route_rank(const int32_t* __restrict__ ids, int r, int R, int lane, int& e,
+                                          bool& last) {
+  e = r < R ? min(max(ids[r], 0), kE - 1) : kE;
+  // lanes holding the same expert: intersect, over the 7 bits of e, the ballots that agree
+  unsigned long long same = ~0ull;
+#pragma unroll
+  for (int bit = 0; bit < 7; ++bit) {
+    const unsigned long long bl = __ballot((e >> bit) & 1);
+    same &= ((e >> bit) & 1) ? bl : ~bl;
+  }
+  const unsigned long long below = (1ull << lane) - 1ull;
+  last = __popcll(same & ~below) == 1;
+  return __popcll(same & below);
+}
 
 __global__ __launch_bounds__(1024) void bucket_kernel(const int32_t* __restrict__ ids, int R, int tile_tokens,
                                                       int32_t* __restrict__ sorted_routes,
                                                       int32_t* __restrict__ route_pos, int32_t* __restrict__ tiles,
                                                       int32_t* __restrict__ num_tiles) {
-  __shared__ uint16_t hist[kMaxChunks][kE];  // 16 KB: per-chunk counts, then exclusive prefix over chunks
-  __shared__ uint8_t rank[kMaxRoutes];
-  __shared__ uint8_t expert[kMaxRoutes];
+  __shared__ uint16_t hist[kMaxChunks][kE];  // per-chunk counts, then exclusive prefix over chunks
   __shared__ int start[kE], tstart[kE], total[kE];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int nchunks = (R + 63) / 64;
   for (int i = tid; i < nchunks * kE; i += 1024) hist[i / kE][i % kE] = 0;
   __syncthreads();
   for (int c = wv; c < nchunks; c += 16) {
-    const int r = c * 64 + lane;
-    const int e = r < R ? min(max(ids[r], 0), kE - 1) : kE;  // kE: no route (matches no expert)
-    // lanes holding the same expert: intersect, over the 7 bits of e, the ballots that agree
-    unsigned long long same = ~0ull;
-#pragma unroll
-    for (int bit = 0; bit < 7; ++bit) {
-      const unsigned long long bl = __ballot((e >> bit) & 1);
-      same &= ((e >> bit) & 1) ? bl : ~bl;
-    }
-    const unsigned long long below = (1ull << lane) - 1ull;
-    const int before = __popcll(same & below);
-    const int after = __popcll(same & ~below) - 1;
-    if (r < R) {
-      rank[r] = (uint8_t)before;
-      expert[r] = (uint8_t)e;
-      if (after == 0) hist[c][e] = (uint16_t)(before + 1);
-    }
+    int e;
+    bool last;
+    const int before = route_rank(ids, c * 64 + lane, R, lane, e, last);
+    if (c * 64 + lane < R && last) hist[c][e] = (uint16_t)(before + 1);
   }
   __syncthreads();
   if (tid < kE) {
@@ -552,11 +556,16 @@ __global__ __launch_bounds__(1024) void bucket_kernel(const int32_t* __restrict_
     if (lane == 63) num_tiles[0] = tincl;
   }
   __syncthreads();
-  for (int r = tid; r < R; r += 1024) {
-    const int e = expert[r];
-    const int p = start[e] + hist[r >> 6][e] + rank[r];
-    sorted_routes[p] = r;
-    route_pos[r] = p;
+  for (int c = wv; c < nchunks; c += 16) {
+    const int r = c * 64 + lane;
+    int e;
+    bool last;
+    const int before = route_rank(ids, r, R, lane, e, last);
+    if (r < R) {
+      const int p = start[e] + hist[c][e] + before;
+      sorted_routes[p] = r;
+      route_pos[r] = p;
+    }
   }
   for (int e = wv; e < kE; e += 16) {
     const int tot = total[e];

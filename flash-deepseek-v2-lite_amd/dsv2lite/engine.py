@@ -14,8 +14,9 @@ Kernel families (``--kernel-family``, src/run.py:53-65):
   batch -- bf16 MFMA grouped GEMM for every projection (heads-batched W_UK /
            W_UV), deterministic expert bucketing, expert-grouped gate_up+SwiGLU
            and down on MFMA, fused combine + shared + residual + next RMSNorm.
-Both use the same split-KV absorbed-MLA decode kernel.  Prefill always uses
-the batch family with one row per prompt token.
+Both use the same split-KV absorbed-MLA decode kernel.  Prefill uses the batch
+family's projections and MoE with one row per prompt token, and MLA in its expanded
+form through a causal flash-attention kernel.
 """
 
 from __future__ import annotations
@@ -76,10 +77,39 @@ def routing_load(ids: torch.Tensor, n_experts: int = 64) -> float:
     return float((c * c).sum() / c.sum().clamp(min=1))
 
 
-class RowBuffers:
-    """Per-row work buffers for `rows` rows of one kernel family."""
+class PrefillPlan:
+    """One prefill chunk's attention work: the query tiles (<= 64 consecutive rows of one
+    sequence each: first row, rows, first position, the sequence's cache base) and the cache
+    rows [exp_lo, exp_lo + exp_rows) whose keys / values the chunk expands."""
 
-    def __init__(self, cfg: DSV2Config, rows: int, family: str, max_ctx: int, device):
+    def __init__(self, tiles: torch.Tensor, exp_lo: int, exp_rows: int, kexp: torch.Tensor, vexp: torch.Tensor):
+        self.tiles, self.n_tiles = tiles, int(tiles.shape[0])
+        self.exp_lo, self.exp_rows = exp_lo, exp_rows
+        self.kexp, self.vexp = kexp, vexp
+
+
+def prefill_tiles(seq: torch.Tensor, posv: torch.Tensor, bases: list[int], tile: int = 64) -> tuple[torch.Tensor, int, int]:
+    """Query tiles of one chunk (seq[r]: sequence of chunk row r, posv[r]: its position;
+    rows of a sequence are consecutive with consecutive positions) and the cache row range
+    its attention reads: from the lowest sequence base to the last position of any row."""
+    vals, counts = torch.unique_consecutive(seq, return_counts=True)
+    out, lo, hi, r = [], None, None, 0
+    for s, cnt in zip(vals.tolist(), counts.tolist()):
+        p_first = int(posv[r])
+        for a in range(0, cnt, tile):
+            out.append((r + a, min(tile, cnt - a), p_first + a, bases[s]))
+        lo = bases[s] if lo is None else min(lo, bases[s])
+        last = bases[s] + p_first + cnt
+        hi = last if hi is None else max(hi, last)
+        r += cnt
+    return torch.tensor(out, dtype=torch.int32).reshape(-1, 4), int(lo), int(hi - lo)
+
+
+class RowBuffers:
+    """Per-row work buffers for `rows` rows of one kernel family (prefill: the batch family
+    without the split-KV decode buffers)."""
+
+    def __init__(self, cfg: DSV2Config, rows: int, family: str, max_ctx: int, device, prefill: bool = False):
         self.rows = rows
         self.family = family
         e = lambda *s, dt=BF16: torch.empty(*s, dtype=dt, device=device)  # noqa: E731
@@ -89,8 +119,9 @@ class RowBuffers:
         self.qkva = e(rows, cfg.qkva_dim)
         self.q = e(rows, cfg.n_heads, cfg.cache_row)
         self.split_tokens, self.max_splits = plan_splits(rows, max_ctx)
-        self.part_o = e(rows, self.max_splits, cfg.n_heads, cfg.kv_rank, dt=torch.float32)
-        self.part_ml = e(rows, self.max_splits, cfg.n_heads, 2, dt=torch.float32)
+        if not prefill:
+            self.part_o = e(rows, self.max_splits, cfg.n_heads, cfg.kv_rank, dt=torch.float32)
+            self.part_ml = e(rows, self.max_splits, cfg.n_heads, 2, dt=torch.float32)
         self.attn = e(rows, H)
         self.ids32 = e(rows, cfg.top_k, dt=torch.int32)
         self.wts = e(rows, cfg.top_k, dt=torch.float32)
@@ -100,7 +131,8 @@ class RowBuffers:
             self.hbuf = e(rows, cfg.top_k + 2, cfg.moe_inter)
         else:
             R = rows * cfg.top_k
-            self.olat = e(rows, cfg.n_heads, cfg.kv_rank)
+            if not prefill:
+                self.olat = e(rows, cfg.n_heads, cfg.kv_rank)
             self._routes, self._n_experts = R, cfg.n_experts
             self.tile_tokens = moe_tile_tokens(rows, cfg.n_experts, cfg.top_k)
             self.max_tiles = math.ceil(R / self.tile_tokens) + cfg.n_experts
@@ -138,7 +170,7 @@ def _graph_node_count(g: torch.cuda.CUDAGraph) -> int:
 
 class DecodeEngine:
     def __init__(self, weights: ModelWeights, capacities: list[int], family: str = "small",
-                 max_prefill_rows: int = 1024, device="cuda", mla_path: str = "fused", moe_tile: int | None = None):
+                 max_prefill_rows: int = 8192, device="cuda", mla_path: str = "fused", moe_tile: int | None = None):
         """capacities: cache tokens of each row (slot).  moe_tile (batch family): fix the
         grouped MoE token tile (16, 32 or 64) instead of choosing it from the routing of one
         eager step at capture -- for a serving loop whose batch changes under one graph."""
@@ -175,9 +207,13 @@ class DecodeEngine:
         self._free: set[int] = set()  # retired slots (continuous batching)
 
     # ------------------------------------------------------------------ layers
-    def _attention(self, L, li: int, b: RowBuffers, R: int, pos, base, cap, family: str, st: int) -> None:
+    def _attention(self, L, li: int, b: RowBuffers, R: int, pos, base, cap, family: str, st: int,
+                   pf: PrefillPlan | None = None) -> None:
         c = self.cfg
         cache = self.cache.layer(li)
+        if pf is not None:
+            self._attention_prefill(L, cache, b, R, pos, base, cap, st, pf)
+            return
         if family == "small" and self.fused_mla and b is self.buf:
             call("dsv2_gemv_bf16", ptr(b.h), c.hidden, R, c.hidden, ptr(L.w_qkva), c.qkva_dim, ptr(L.ln_in), c.eps,
                  None, 0, ptr(b.qkva), c.qkva_dim, 0, st)
@@ -218,6 +254,26 @@ class DecodeEngine:
                  c.v_dim * c.kv_rank, c.v_dim, c.n_heads, None, 0, ptr(b.attn), c.hidden, c.v_dim, 0, st)
             call("dsv2_gemm_bf16", ptr(b.attn), c.hidden, 0, R, c.hidden, ptr(L.w_o), 0, c.hidden, 1, ptr(b.h),
                  c.hidden, ptr(b.h), c.hidden, 0, 0, st)
+
+    def _attention_prefill(self, L, cache, b: RowBuffers, R: int, pos, base, cap, st: int, pf: PrefillPlan) -> None:
+        """A prefill chunk's attention in the expanded form: the chunk's cache rows and
+        RoPE(q_pe) (mla_prepare), k_nope / v of every cache row the chunk attends (W_UK /
+        W_UV over the latent: grouped GEMMs over the heads), causal flash attention per
+        (64-query tile, head), then o_proj with the residual."""
+        c = self.cfg
+        H, nh = c.hidden, c.n_heads
+        call("dsv2_gemm_bf16", ptr(b.xn), H, 0, R, H, ptr(L.w_qkva), 0, c.qkva_dim, 1, None, 0, ptr(b.qkva),
+             c.qkva_dim, 0, 0, st)
+        call("dsv2_mla_prepare", ptr(b.qkva), c.qkva_dim, R, ptr(pos), ptr(base), ptr(cap), ptr(L.kv_norm), c.eps,
+             ptr(self.cos), ptr(self.sin), self.max_pos, None, ptr(cache), ptr(b.q), ptr(self.cache.status), st)
+        crow = cache.data_ptr() + pf.exp_lo * c.cache_row * cache.element_size()
+        for w, out in ((L.w_uk, pf.kexp), (L.w_uv, pf.vexp)):
+            call("dsv2_gemm_bf16", crow, c.cache_row, 0, pf.exp_rows, c.kv_rank, ptr(w), c.qk_nope * c.kv_rank,
+                 c.qk_nope, nh, None, 0, ptr(out), nh * c.qk_nope, c.qk_nope, 0, st)
+        call("dsv2_mla_prefill_attention", ptr(b.qkva), c.qkva_dim, ptr(b.q), nh * c.cache_row, R, ptr(cache),
+             cache.shape[0], ptr(pf.kexp), ptr(pf.vexp), pf.exp_lo, pf.exp_rows, ptr(pf.tiles), pf.n_tiles,
+             self.scale, ptr(b.attn), H, st)
+        call("dsv2_gemm_bf16", ptr(b.attn), H, 0, R, H, ptr(L.w_o), 0, H, 1, ptr(b.h), H, ptr(b.h), H, 0, 0, st)
 
     def _mlp(self, L, li: int, b: RowBuffers, R: int, family: str, next_norm, st: int) -> None:
         c = self.cfg
@@ -277,7 +333,7 @@ class DecodeEngine:
             call("dsv2_rmsnorm_bf16", ptr(b.h), H, ptr(next_norm), ptr(b.xn), H, R, H, c.eps, st)
 
     def _layers(self, b: RowBuffers, R: int, ids: torch.Tensor, pos, base, cap, family: str, st: int,
-                record: list | None = None, rows: torch.Tensor | None = None) -> None:
+                record: list | None = None, rows: torch.Tensor | None = None, pf: PrefillPlan | None = None) -> None:
         """Enqueue the embedding gather and every layer for R kernel rows.  With `record`,
         append per layer ("attn", li, h), ("layer", li, h) and ("router", li, ids, weights)
         copies of the rows `rows` (device index tensor; all R rows when None)."""
@@ -289,7 +345,7 @@ class DecodeEngine:
                  c.hidden, c.eps, st)
         n = len(self.w.layers)
         for li, L in enumerate(self.w.layers):
-            self._attention(L, li, b, R, pos, base, cap, family, st)
+            self._attention(L, li, b, R, pos, base, cap, family, st, pf)
             if record is not None:
                 record.append(("attn", li, sel(b.h)))
             next_norm = self.w.layers[li + 1].ln_in if li + 1 < n else self.w.norm
@@ -326,12 +382,14 @@ class DecodeEngine:
         self._host_pos = [p + 1 for p in self._host_pos]
 
     def prefill(self, prompts: list[torch.Tensor], record: list | None = None) -> torch.Tensor:
-        """Eager prefill of one prompt per row (batch-family kernels, one kernel row per
-        prompt token, chunks of <= max_prefill_rows rows in sequence order).  Writes the
-        compressed cache, sets cache.pos = prompt lengths and self.ids = greedy first
-        tokens (returned).  Mirrors _prefill_once (src/run.py:526-544).  With `record`, it
-        receives the per-layer records of each sequence's LAST prompt token, in the format of
-        a recorded decode step (row b = sequence b)."""
+        """Eager prefill of one prompt per row: chunks of <= max_prefill_rows prompt tokens
+        (one kernel row each, in sequence order) through the batch-family projections and
+        grouped MoE, with the attention in MLA's expanded form (the chunk's cache rows, k_nope
+        / v of the cached prefix by grouped GEMMs, causal MFMA flash attention per 64-query
+        tile and head).  Writes the compressed cache, sets cache.pos = prompt lengths and
+        self.ids = greedy first tokens (returned).  Mirrors _prefill_once (src/run.py:526-544).
+        With `record`, it receives the per-layer records of each sequence's LAST prompt token,
+        in the format of a recorded decode step (row b = sequence b)."""
         if len(prompts) != self.B:
             raise ValueError(f"need {self.B} prompts, got {len(prompts)}")
         self._free.clear()
@@ -389,7 +447,13 @@ class DecodeEngine:
         cap_all = self.cache.cap.cpu()[slot_t[seq]]
         total = seq.numel()
         max_rows = min(self.max_prefill_rows, total)
-        pb = RowBuffers(self.cfg, max_rows, "batch", self.max_pos, dev)
+        pb = RowBuffers(self.cfg, max_rows, "batch", self.max_pos, dev, prefill=True)
+        bases = [int(x) for x in self.cache.base.cpu()[slot_t]]
+        plans = [prefill_tiles(seq[s:s + max_rows], posv[s:s + max_rows], bases) for s in range(0, total, max_rows)]
+        n_exp = max(p[2] for p in plans)
+        nh, dk = self.cfg.n_heads, self.cfg.qk_nope
+        kexp = torch.empty(n_exp, nh, dk, dtype=BF16, device=dev)
+        vexp = torch.empty(n_exp, nh, self.cfg.v_dim, dtype=BF16, device=dev)
         last_h = torch.empty(k, self.cfg.hidden, dtype=BF16, device=dev)
         last_xn = torch.empty_like(last_h)
         st = _hip.stream_ptr(dev)
@@ -406,7 +470,9 @@ class DecodeEngine:
             rows_d = rows.to(dev)
             which = seq[s:e][rows].to(dev)
             crec = [] if record is not None else None
-            self._layers(pb, R, ids_c, pos_c, base_c, cap_c, "batch", st, crec, rows_d)
+            t, lo, n = plans[s // max_rows]
+            pf = PrefillPlan(t.to(dev), lo, n, kexp, vexp)
+            self._layers(pb, R, ids_c, pos_c, base_c, cap_c, "batch", st, crec, rows_d, pf)
             for r in crec or ():
                 for j, t in enumerate(r[2:]):  # scatter the last-token rows to their sequences
                     key = (r[0], r[1], j)

@@ -49,6 +49,8 @@ _SIGS = {
                        _i32),
     "dsv2_attention_decode_expanded": ([_p, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64,
                                         _i32, _i32, _i32, _i32, _i32, _p, _f32, _p, _p], _i32),
+    "dsv2_mla_prefill_attention": ([_p, _i64, _p, _i64, _i32, _p, _i64, _p, _p, _i64, _i64, _p, _i32, _f32, _p, _i64,
+                                    _p], _i32),
     "dsv2_router_logits": ([_p, _i64, _p, _f32, _p, _i32, _p, _p, _p], _i32),
     "dsv2_moe_route_gateup_logits": ([_p, _i32, _p, _f32, _p, _p, _p, _p, _i32, _p, _p], _i32),
     "dsv2_router_topk6": ([_p, _i64, _p, _f32, _p, _f32, _i32, _p, _p, _p, _p, _p], _i32),

@@ -96,8 +96,8 @@ def batched_grouped_routed_moe_grouped_triton(x: torch.Tensor, topk_ids: torch.T
     w = topk_weight.to(torch.float32).contiguous()
     B, I = x.shape[0], packed.intermediate_size
     R = B * 6
-    if R > 8192:
-        raise ValueError("batched_grouped_routed_moe supports at most 1365 tokens per call")
+    if R > 49152:
+        raise ValueError("batched_grouped_routed_moe supports at most 8192 tokens per call")
     dev = x.device
     avg = R / 64
     tile = 16 if avg <= 6 else (32 if avg <= 16 else 64)

@@ -212,6 +212,23 @@ int dsv2_attention_decode_expanded(const void* q, int64_t q_stride_b, int64_t q_
                                    int v_dim, int seq_len, const int64_t* cache_position, float softmax_scale,
                                    int32_t* status, void* stream);
 
+/* Prefill attention (the prompt's tokens, before the decode path) in MLA's expanded form,
+ * per head h and query row r (position p, in the sequence whose position 0 is cache row sb):
+ *   out[r, h*128 + i] = bf16( softmax_{n <= p}(scale * q_rh . k_nh) . v_nh[i] )
+ *   q_rh = [qkva[r, h*192 .. +128] | q_rope[r, h*576 + 512 .. +64]]   (mla_prepare's RoPE(q_pe))
+ *   k_nh = [k_nope[sb + n - exp_lo, h, :128] | cache[sb + n, 512 .. 576]],
+ *   v_nh = v[sb + n - exp_lo, h, :128]
+ * k_nope / v [exp_rows, 16, 128] bf16 are W_UK / W_UV applied to cache rows exp_lo .. (the
+ * kv_b projection of every cached token; dsv2_gemm_bf16 grouped over heads).  tiles [n_tiles]
+ * int32x4 {first row, rows (1..64), position of the first row, sb}: <= 64 consecutive query
+ * rows of one sequence each.  Indices derived from the table are clamped into rows /
+ * cache_rows / exp_rows.  Replaces the prefill attention of the HF model the reference runs
+ * eagerly (src/run.py:526-544; remote DeepseekV2Attention.forward over the expanded K/V). */
+int dsv2_mla_prefill_attention(const void* qkva, int64_t qkva_stride, const void* q_rope, int64_t q_rope_stride,
+                               int rows, const void* cache, int64_t cache_rows, const void* k_nope, const void* v,
+                               int64_t exp_lo, int64_t exp_rows, const int32_t* tiles, int n_tiles,
+                               float softmax_scale, void* out, int64_t out_stride, void* stream);
+
 /* ---- MoE ------------------------------------------------------------------ */
 
 /* Router logits only, spread over 16 workgroups per token: xn = RMSNorm(h) (written by the
@@ -265,7 +282,7 @@ int dsv2_moe_route_down(const void* hbuf, int rows, const int32_t* ids, const fl
 /* Batch family bucketing (one workgroup, deterministic counting sort by expert):
  *   sorted_routes[p] = route index r*6+s in expert order, stable in r;
  *   route_pos[r*6+s] = p;  tiles[t] = {expert, first slot, count<=tile_tokens, 0} (int32x4);
- *   num_tiles[0] = number of tiles (<= rows*6/tile_tokens + 64).  rows*6 <= 8192.
+ *   num_tiles[0] = number of tiles (<= rows*6/tile_tokens + 64).  rows*6 <= 49152 (8192 rows).
  * Replaces _build_route_indices_kernel + _build_route_blocks_kernel (moe_batch.py:95-148). */
 int dsv2_moe_bucket(const int32_t* ids, int rows, int tile_tokens, int32_t* sorted_routes, int32_t* route_pos,
                     int32_t* tiles, int32_t* num_tiles, void* stream);

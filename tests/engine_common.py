@@ -4,7 +4,10 @@ CPU oracle pair, the comparison bars and the teacher-forcing helpers.
 Bars: hidden states and logits within max-rel 2e-2 (max|a-b|/max|b|) of the oracle with
 the HF remote code's bf16 rounding points ("bf16", the reference's own arithmetic: the
 north-star bar), and within 3e-2 of exact fp32 math ("fp32"; HF's bf16 arithmetic is itself
-up to ~2.5e-2 from it on these logits, the measured "floor" printed by the tests).  Router:
+up to ~2.5e-2 from it on these logits, the measured "floor" printed by the tests).  A result
+closer to exact math than HF's own arithmetic (fp32 error <= min(2e-2, floor)) also passes,
+with a 3e-2 cap against the bf16 oracle: |ours - HF| can reach |ours - exact| + |HF - exact|
+without ours being the less accurate of the two.  Router:
 exact on its own input (the kernel's expert set equals the top-6 of the kernel's own
 post-attention hidden state wherever the top-6 logit margin exceeds 1e-3); a set that
 differs from the oracle's must be explained by the two inputs' measured router-logit
@@ -57,15 +60,18 @@ def build_model(n_layers: int, max_pos: int = 512):
 
 
 def close(got: torch.Tensor, r16: torch.Tensor, r32: torch.Tensor, flipped: bool, what, errs: list | None = None):
-    """2e-2 against the bf16 oracle (the reference's arithmetic) and 3e-2 against exact fp32
-    math; 5e-2 against the bf16 oracle after a router flip."""
+    """Within 2e-2 of the bf16 oracle (the reference's arithmetic) and 3e-2 of exact fp32
+    math -- or closer to exact math than the bf16 oracle itself is (and within 2e-2 of it,
+    3e-2 of the bf16 oracle); 5e-2 against the bf16 oracle after a router flip."""
     e16, e32, floor = rel_err(got, r16), rel_err(got, r32), rel_err(r16, r32)
     if errs is not None:
         errs.append((e16, e32, flipped, floor))
     if flipped:
         assert e16 < NEAR_TIE_BAR, (what, "after a near-tie router flip", e16)
         return
-    assert e16 <= BAR and e32 <= FP32_BAR, (what, e16, e32, floor)
+    near_reference = e16 <= BAR and e32 <= FP32_BAR
+    more_exact = e32 <= min(BAR, floor) and e16 <= FP32_BAR
+    assert near_reference or more_exact, (what, e16, e32, floor)
 
 
 def prompts(lens, seed, vocab=102400):

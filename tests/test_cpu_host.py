@@ -46,7 +46,7 @@ def test_abi_rejects_bad_arguments_without_launching():
     with pytest.raises(_hip.HipKernelError, match="null pointer"):
         _hip.call("dsv2_mla_prepare", 16, 3648, 1, 16, 16, None, 16, 1e-6, 16, 16, 64, None, 16, 16, None, None)
     with pytest.raises(_hip.HipKernelError, match="rows\\*6"):
-        _hip.call("dsv2_moe_bucket", 16, 2000, 32, 16, 16, 16, 16, None)
+        _hip.call("dsv2_moe_bucket", 16, 8193, 32, 16, 16, 16, 16, None)
 
 
 def test_wrappers_reject_cpu_tensors_like_the_reference():
@@ -319,3 +319,29 @@ def test_bench_mfma_summary_uses_the_timing_graph_dispatches(tmp_path):
     cells = [c.strip() for c in line.strip("|").split("|")]
     assert cells[1] == str(n) and cells[2] == "10.0"
     assert float(cells[3]) == round(1000 * 512 / 1e9, 3) and cells[4] == "2.0"
+
+
+def test_prefill_tiles_cover_every_row_once():
+    """The prefill attention's query tiles: <= 64 consecutive rows of one sequence each, every
+    chunk row in exactly one tile with its own position and its sequence's cache base; the
+    expanded range spans every key any row attends."""
+    from dsv2lite.engine import prefill_tiles
+
+    lens = [100, 3, 64, 130]
+    bases = [0, 200, 300, 500]
+    seq = torch.cat([torch.full((n,), b, dtype=torch.int64) for b, n in enumerate(lens)])
+    posv = torch.cat([torch.arange(n, dtype=torch.int32) for n in lens])
+    # a chunk that starts inside sequence 0 (positions 40..) and ends inside sequence 3
+    s, e = 40, 100 + 3 + 64 + 70
+    t, lo, n = prefill_tiles(seq[s:e], posv[s:e], bases)
+    seen = torch.zeros(e - s, dtype=torch.int32)
+    for r0, nr, p0, sb in t.tolist():
+        assert 1 <= nr <= 64
+        rows = torch.arange(r0, r0 + nr)
+        assert len(set(seq[s:e][rows].tolist())) == 1
+        b = int(seq[s + r0])
+        assert sb == bases[b] and torch.equal(posv[s:e][rows], torch.arange(p0, p0 + nr, dtype=torch.int32))
+        seen[rows] += 1
+        assert lo <= sb and sb + p0 + nr <= lo + n  # every key of the tile's rows is expanded
+    assert torch.all(seen == 1)
+    assert lo == 0 and lo + n == 500 + 70

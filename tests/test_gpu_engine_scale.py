@@ -1,7 +1,8 @@
 """Engine-level GPU parity at the benchmark batch sizes and context lengths: the decode step
 at bsz=64 with prompts U[256,1024] (benchmark config 2) and bsz=256 with 2048-token prompts
 (config 3), a 256-token prefill followed by 32 decode steps (config 0's shape, one row), and
-a prompt that crosses the 1024-row prefill chunk.  Same 3-layer full-width model and bars
+a prompt that crosses a prefill chunk.  The prefill logits of every sampled row -- the
+chunked flash-attention prefill over 2048-token prompts at bsz=256 -- are checked too.  Same 3-layer full-width model and bars
 as test_gpu_engine.py (engine_common).
 
 At bsz 64 / 256 the step runs the kernels that only those sizes select: the one-workgroup-
@@ -59,12 +60,12 @@ def _graph_equals_eager(eng, snap, steps=2):
     eng.restore(snap)
 
 
-def _parity(model, family, lens, seed, steps=3, rows=None, graph=True, tile=None):
+def _parity(model, family, lens, seed, steps=3, rows=None, graph=True, tile=None, chunk=8192):
     import dsv2lite
 
     cfg, w, om = model
     B = len(lens)
-    eng = dsv2lite.DecodeEngine(w, [n + steps + 8 for n in lens], family=family)
+    eng = dsv2lite.DecodeEngine(w, [n + steps + 8 for n in lens], family=family, max_prefill_rows=chunk)
     P = prompts(lens, seed)
     prec = []
     first = eng.prefill([p.cuda() for p in P], record=prec).cpu().clone()
@@ -138,7 +139,8 @@ def test_c0_shape_prefill256_then_32_steps(model, family):
     _parity(model, family, [256], seed=5, steps=32, rows=[0])
 
 
-def test_prefill_crosses_the_1024_row_chunk(model):
-    """A 1300-token and a 100-token prompt: the prefill runs 1400 rows in two chunks, the
-    first holding the short prompt and the long one's first 924 tokens."""
-    _parity(model, "batch", [100, 1300], seed=6, rows=[0, 1])
+def test_prefill_crosses_a_chunk_boundary(model):
+    """A 1300-token and a 100-token prompt in 1024-row prefill chunks: the first chunk holds
+    the short prompt and the long one's first 924 tokens, the second chunk's queries attend
+    keys the first chunk cached."""
+    _parity(model, "batch", [100, 1300], seed=6, rows=[0, 1], chunk=1024)

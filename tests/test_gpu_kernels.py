@@ -751,3 +751,43 @@ def test_lm_head_argmax_matches_gemv_then_argmax(rows):
     with pytest.raises(_hip.HipKernelError, match="rows"):
         call("dsv2_lm_head_argmax_bf16", x.data_ptr(), 2048, 9, W.data_ptr(), 102400, nw.data_ptr(), 1e-6,
              lg.data_ptr(), part.data_ptr(), part.numel(), ids.data_ptr(), None, st())
+
+
+@pytest.mark.parametrize("lens,start", [([70, 150], 0), ([300, 5, 129], 40)])
+def test_mla_prefill_attention_vs_fp32(lens, start):
+    """Prefill attention (expanded form, causal) against fp32 torch: rows of several
+    sequences (a chunk that may start inside the first sequence: its earlier keys come from
+    the cache), 64-query tiles with partial last tiles."""
+    from dsv2lite.engine import prefill_tiles
+
+    caps = [n + 30 for n in lens]
+    bases = [0]
+    for cp in caps[:-1]:
+        bases.append(bases[-1] + cp)
+    ncache = bases[-1] + caps[-1]
+    seq = torch.cat([torch.full((n,), b, dtype=torch.int64) for b, n in enumerate(lens)])[start:]
+    posv = torch.cat([torch.arange(n, dtype=torch.int32) for n in lens])[start:]
+    R = seq.numel()
+    tiles, lo, nexp = prefill_tiles(seq, posv, bases)
+    cache = rnd(ncache, 576, seed=200)
+    kexp = rnd(nexp, 16, 128, seed=201)
+    vexp = rnd(nexp, 16, 128, seed=202)
+    qkva = rnd(R, 3648, seed=203)
+    qrope = rnd(R, 16, 576, seed=204)
+    out = torch.full((R, 2048), float("nan"), dtype=BF, device=DEV)
+    scale = O.softmax_scale(O.Dims())
+    td = tiles.to(DEV)
+    call("dsv2_mla_prefill_attention", qkva.data_ptr(), 3648, qrope.data_ptr(), 16 * 576, R, cache.data_ptr(), ncache,
+         kexp.data_ptr(), vexp.data_ptr(), lo, nexp, td.data_ptr(), td.shape[0], scale, out.data_ptr(), 2048, st())
+    c = lambda t: t.float().cpu()  # noqa: E731
+    cc, ke, ve, qa, qr = c(cache), c(kexp), c(vexp), c(qkva), c(qrope)
+    ref = torch.empty(R, 16, 128)
+    for r in range(R):
+        b, p = int(seq[r]), int(posv[r])
+        rows = torch.arange(bases[b], bases[b] + p + 1)
+        q = torch.cat([qa[r, :3072].view(16, 192)[:, :128], qr[r, :, 512:]], -1)  # [16, 192]
+        k = torch.cat([ke[rows - lo], cc[rows, 512:][:, None, :].expand(-1, 16, -1)], -1)  # [n, 16, 192]
+        s = torch.einsum("hd,nhd->hn", q, k) * scale
+        ref[r] = torch.einsum("hn,nhd->hd", torch.softmax(s, -1), ve[rows - lo])
+    assert torch.isfinite(c(out)).all()
+    assert rel_err(c(out).view(R, 16, 128), ref) < 1e-2
