@@ -70,14 +70,15 @@ CONFIGS = {
 }
 
 
-def step_bytes(cfg, n_exp_per_layer: list[int], ctx_sum_per_layer: float, batch: int) -> float:
+def step_bytes(cfg, n_exp_per_layer: list[int], ctx_sum_per_layer: float, batch: int,
+               expert_fp8: bool = False) -> float:
     """Algorithmic HBM bytes of one decode step (dsv2lite.roofline.step_bytes): every weight
     read once (attention, router, the experts actually hit, shared experts, dense layer 0,
     lm_head, norms), the embedding rows and the compressed KV rows read (1,152 B per token
     per layer)."""
     from dsv2lite.roofline import step_bytes as _sb
 
-    return float(_sb(cfg, n_exp_per_layer, ctx_sum_per_layer, batch))
+    return float(_sb(cfg, n_exp_per_layer, ctx_sum_per_layer, batch, expert_fp8))
 
 
 def time_dominant_kernel(eng, family: str, reps: int = 4) -> dict:
@@ -90,7 +91,15 @@ def time_dominant_kernel(eng, family: str, reps: int = 4) -> dict:
     c, b = eng.cfg, eng.buf
     moe_layers = [L for L in eng.w.layers if L.moe]
     B = eng.B
-    if family == "small":
+    if family == "small" and eng.expert_dtype == "fp8":
+        name = "route_gateup_fp8_kernel<4> (small-family MoE gate_up+SwiGLU on e4m3 weights, 6 routed + 2 shared halves)"
+        bytes_per = B * 8 * 2 * c.moe_inter * (c.hidden + 4) + B * 8 * c.moe_inter * 2
+
+        def launch(L):
+            call("dsv2_moe_route_gateup_logits_fp8", ptr(b.xn), B, ptr(b.router_logits), c.routed_scaling,
+                 ptr(b.ids32), ptr(b.wts), ptr(L.w_gu8), ptr(L.gu_scale), ptr(L.sh_gu8), ptr(L.sh_gu_scale),
+                 c.moe_inter, ptr(b.hbuf), stream_ptr())
+    elif family == "small":
         name = "route_gateup_kernel<2> (small-family MoE gate_up+SwiGLU, 6 routed + 2 shared halves)"
         bytes_per = B * 8 * 2 * c.moe_inter * c.hidden * 2 + B * 8 * c.moe_inter * 2
 
@@ -181,8 +190,18 @@ def time_other_kernels(eng, family: str, ctx_rows: list[int]) -> dict:
             L = eng.w.layers[li]
             call("dsv2_moe_route_down", ptr(b.hbuf), B, ptr(b.ids32), ptr(b.wts), ptr(L.w_down), ptr(L.sh_down),
                  c.moe_inter, c.top_k + 2, None, ptr(b.h), ptr(b.attn), stream_ptr())
-        entry("route_down_kernel (6 routed + 2 shared-half down projections + combine)", down, moe,
-              B * 8 * 2048 * 1408 * 2)
+
+        def down8(li):
+            L = eng.w.layers[li]
+            call("dsv2_moe_route_down_fp8", ptr(b.hbuf), B, ptr(b.ids32), ptr(b.wts), ptr(L.w_down8),
+                 ptr(L.down_scale), ptr(L.sh_down8), ptr(L.sh_down_scale), c.moe_inter, c.top_k + 2, ptr(b.h),
+                 ptr(b.attn), stream_ptr())
+        if eng.expert_dtype == "fp8":
+            entry("route_down_fp8_kernel (6 routed + 2 shared-half down projections on e4m3 weights + combine)",
+                  down8, moe, B * 8 * 2048 * (1408 + 4))
+        else:
+            entry("route_down_kernel (6 routed + 2 shared-half down projections + combine)", down, moe,
+                  B * 8 * 2048 * 1408 * 2)
         return out
     n_exp = int(torch.unique(b.ids32[:B]).numel())
     R = B * c.top_k
@@ -572,7 +591,7 @@ def _log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def run_config(key, w, args, cfg, dev) -> dict:
+def run_config(key, w, args, cfg, dev, expert_dtype: str = "bf16") -> dict:
     """Prefill + K timed graph replays of one benchmark config on already-initialised weights:
     tok/s, ms/step, the step's byte roofline and the dominant kernel's roofline."""
     import dsv2lite
@@ -587,7 +606,7 @@ def run_config(key, w, args, cfg, dev) -> dict:
         prompts = [torch.randint(0, cfg.vocab, (n,), generator=g) for n in lens]
     steps, warm = args.steps, args.warmup
     caps = [n + steps + warm + 8 for n in lens]
-    eng = dsv2lite.DecodeEngine(w, caps, family=family, mla_path=args.mla_path)
+    eng = dsv2lite.DecodeEngine(w, caps, family=family, mla_path=args.mla_path, expert_dtype=expert_dtype)
     t0 = time.perf_counter()
     eng.prefill([p.to(dev) for p in prompts])
     torch.cuda.synchronize()
@@ -619,13 +638,14 @@ def run_config(key, w, args, cfg, dev) -> dict:
     ms = dt / steps * 1e3
     # KV rows read per layer per step, averaged over the timed steps (ctx = pos + 1)
     ctx_avg = sum(n + 1 + (steps - 1) / 2 for n in lens)
-    sb = step_bytes(cfg, n_exp, ctx_avg, B)
+    sb = step_bytes(cfg, n_exp, ctx_avg, B, expert_dtype == "fp8")
     _log(f"config {key}: timed {steps} graph replays: {ms:.3f} ms/step, {value:.1f} tok/s")
     roof = time_dominant_kernel(eng, family)
     roof["traffic"], roof["traffic_source"] = measured_traffic(key, roof["kernel"])
     pos_now = eng.cache.pos.cpu().tolist()
     others = time_other_kernels(eng, family, [p + 1 for p in pos_now])
-    res = {"workload": spec["workload"], "global_batch": B, "seq_len": max(lens), "kernel_family": family,
+    res = {"workload": spec["workload"] + (", e4m3 expert weights" if expert_dtype == "fp8" else ""),
+           "expert_dtype": expert_dtype, "global_batch": B, "seq_len": max(lens), "kernel_family": family,
            "mla_path": args.mla_path if family == "small" else "split", "prompt_tokens": sum(lens),
            "tok_s": value, "ms_per_step": ms, "steps": steps, "warmup": warm, "kernels_per_step": eng.kernels_per_step,
            "roofline": roof,
@@ -649,6 +669,8 @@ def main() -> None:
                     help="all (default): config 1 is the line's value, configs 2 and 3 ride along under "
                          "'configs'; N: that config alone")
     ap.add_argument("--family", choices=("small", "batch"), default=None)
+    ap.add_argument("--expert-dtype", choices=("bf16", "fp8"), default="bf16",
+                    help="one config: MoE expert weights in bf16 or e4m3 (small family); 'all' runs C1 both ways")
     ap.add_argument("--mla-path", choices=("fused", "split"), default="fused",
                     help="small family: one fused MLA kernel per layer, or prepare + split-KV decode + combine")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -699,13 +721,16 @@ def main() -> None:
     t_init = time.perf_counter() - t0
     _log(f"weights ready ({w.nbytes() / 1e9:.1f} GB, {t_init:.1f}s)")
     head = 1 if args.config == "all" else args.config
-    r = run_config(head, w, args, cfg, dev)
+    head_dtype = "bf16" if args.config == "all" else args.expert_dtype
+    if head_dtype == "fp8":
+        dsv2lite.quantize_experts_fp8(w)
+    r = run_config(head, w, args, cfg, dev, expert_dtype=head_dtype)
     spec = CONFIGS[head]
     out = {
         "metric": METRIC, "value": round(r["tok_s"], 2), "unit": "tokens/s", "n_gpus": 1, "steps": r["steps"],
         "warmup": r["warmup"], "ms_per_step": round(r["ms_per_step"], 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": r.get("vs_published_a100"),
-        "dtype": "bf16", "data": "synthetic: random-init weights N(0,0.02) seed 0, uniform random prompt ids"
+        "dtype": "bf16" if head_dtype == "bf16" else "bf16 activations, e4m3 expert weights", "data": "synthetic: random-init weights N(0,0.02) seed 0, uniform random prompt ids"
                                  + (" (one prompt replicated over the batch)" if spec.get("replicate") else ""),
         "config": {"workload": r["workload"], "global_batch": r["global_batch"], "seq_len": r["seq_len"],
                    "kernel_family": r["kernel_family"], "mla_path": r["mla_path"],
@@ -720,6 +745,12 @@ def main() -> None:
         for key in (2, 3):
             rk = run_config(key, w, args, cfg, dev)
             out["configs"][f"C{key}"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in rk.items()}
+        # config 1 again with the MoE expert weights in e4m3 (per-row power-of-two scales);
+        # quantizing rewrites the bf16 experts with their dequantized values, so it runs last
+        _log("quantizing expert weights to e4m3")
+        dsv2lite.quantize_experts_fp8(w)
+        rk = run_config(1, w, args, cfg, dev, expert_dtype="fp8")
+        out["configs"]["C1_fp8"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in rk.items()}
     if args.copy_calibration:
         _copy_calibration(out, dev)
     if not args.no_cpu_baseline:

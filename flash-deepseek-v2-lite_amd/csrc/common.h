@@ -100,6 +100,30 @@ __device__ __forceinline__ uint4 keep_if(bool ok, const uint4& v) {
 // wait here covers only the loads issued before it.
 __device__ __forceinline__ void pin(uint32_t v) { asm volatile("" ::"v"(v)); }
 
+// 16 fp8 (OCP e4m3, the format of gfx950's v_cvt_pk_f32_fp8) -> fp32, two per instruction
+__device__ __forceinline__ void unpack16_fp8(const uint4& v, float* f) {
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const f32x2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w[i]), false);
+    const f32x2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w[i]), true);
+    f[4 * i] = lo[0];
+    f[4 * i + 1] = lo[1];
+    f[4 * i + 2] = hi[0];
+    f[4 * i + 3] = hi[1];
+  }
+}
+
+__device__ __forceinline__ float dot16_fp8(const uint4& w, const float* x) {
+  float f[16];
+  unpack16_fp8(w, f);
+  float s = f[0] * x[0];
+#pragma unroll
+  for (int i = 1; i < 16; ++i) s = __builtin_fmaf(f[i], x[i], s);
+  return s;
+}
+
 __device__ __forceinline__ float dot8(const uint4& w, const float* x) {
   float f[8];
   unpack8(w, f);

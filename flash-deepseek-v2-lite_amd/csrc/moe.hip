@@ -186,7 +186,14 @@ struct RouteGateupArgs {
   const bf16_t* wgu;
   const bf16_t* shgu;
   bf16_t* hbuf;
+  // fp8 weights (route_gateup_fp8_kernel): e4m3 rows and one fp32 scale per row
+  const uint8_t* wgu8;
+  const float* sgu;     // [64, 2*inter]
+  const uint8_t* shgu8;
+  const float* sshgu;   // [2*2*inter]
 };
+
+
 
 // Expert of routed slot s < 6 from the row's 64 fp32 router logits (lane j holds logit j):
 // the lane whose rank -- the number of lanes with a larger logit, or an equal one at a lower
@@ -209,6 +216,34 @@ __device__ __forceinline__ int routed_expert(float x, int s) {
   return __ffsll(__ballot(rank == s)) - 1;
 }
 
+// Expert of routed slot s of row b (wave 0 of the route's workgroups): from the row's ids, or
+// ranked from its fp32 router logits (the route's first workgroup then publishes the row's
+// ids and softmax weights).  Slots s >= 6 (shared halves) return 0.
+__device__ __forceinline__ int route_expert(const RouteGateupArgs& a, int b, int s, int bx, int lane) {
+  int e = 0;
+  if (s < kTopK && a.logits) {
+    const float x = a.logits[(int64_t)b * kE + lane];
+    e = routed_expert(x, s);
+    if (bx == 0 && s == 0) {
+      int rank = 0;
+      for (int j = 0; j < kE; ++j) {
+        const float xj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), j));
+        rank += (xj > x || (xj == x && j < lane)) ? 1 : 0;
+      }
+      const float mx = wave_max(x);
+      const float ex = expf(x - mx);
+      const float sm = wave_sum(ex);
+      if (rank < kTopK) {
+        a.ids[b * kTopK + rank] = lane;
+        a.wts[b * kTopK + rank] = ex / sm * a.scaling;
+      }
+    }
+  } else if (s < kTopK) {
+    e = min(max(a.ids[b * kTopK + s], 0), kE - 1);
+  }
+  return e;
+}
+
 // 6 waves per SIMD: all 1408 workgroups of a bsz=1 launch (8 routes x 176) resident together
 template <int RPW>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) void route_gateup_kernel(
@@ -222,29 +257,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) voi
   // x first (it does not depend on the routing), then the logits
   const uint4 x4 = ldg16(a.xn + (int64_t)b * kH + tid * 8);
   if (wv == 0) {
-    int e = 0;
-    if (s < kTopK && a.logits) {
-      // one wave per workgroup ranks the logits; the route's first workgroup also
-      // publishes the row's ids and softmax weights
-      const float x = a.logits[(int64_t)b * kE + lane];
-      e = routed_expert(x, s);
-      if (bx == 0 && s == 0) {
-        int rank = 0;
-        for (int j = 0; j < kE; ++j) {
-          const float xj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), j));
-          rank += (xj > x || (xj == x && j < lane)) ? 1 : 0;
-        }
-        const float mx = wave_max(x);
-        const float ex = expf(x - mx);
-        const float sm = wave_sum(ex);
-        if (rank < kTopK) {
-          a.ids[b * kTopK + rank] = lane;
-          a.wts[b * kTopK + rank] = ex / sm * a.scaling;
-        }
-      }
-    } else if (s < kTopK) {
-      e = min(max(a.ids[b * kTopK + s], 0), kE - 1);
-    }
+    // one wave per workgroup ranks the logits
+    const int e = route_expert(a, b, s, bx, lane);
     if (lane == 0) eid = e;
   }
   {
@@ -299,6 +313,88 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) voi
 #pragma unroll
     for (int r = 0; r < RPW; ++r)
       a.hbuf[((int64_t)b * a.hbuf_routes + s) * a.inter + i0 + r] = f2bf(swiglu_bf(ag[r], au[r]));
+  }
+}
+
+// fp8 weights: the same work per route with every weight row in e4m3 (16 per 16-byte load,
+// 2 loads per lane per row, 4 rows of gate and 4 of up per wave) and the row's fp32 scale
+// applied to the fp32 dot product before the SwiGLU.
+template <int RPW>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) void route_gateup_fp8_kernel(
+    const RouteGateupArgs a) {
+  __shared__ float xs[kH];
+  __shared__ int eid;
+  const int bx = blockIdx.x % a.gu_blocks, route = blockIdx.x / a.gu_blocks;
+  const int b = route / a.nr, s = route % a.nr;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int i0 = (bx * 4 + wv) * RPW;
+  const uint4 x4 = ldg16(a.xn + (int64_t)b * kH + tid * 8);
+  if (wv == 0) {
+    const int e = route_expert(a, b, s, bx, lane);
+    if (lane == 0) eid = e;
+  }
+  {
+    float f[8];
+    unpack8(x4, f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xs[tid * 8 + i] = f[i];
+  }
+  __syncthreads();
+  const int e = eid;
+  if (i0 >= a.inter) return;  // inter % RPW == 0: a live wave owns RPW whole rows
+  const uint8_t *gp, *up;
+  const float *gs, *us;
+  if (s < kTopK) {
+    gp = a.wgu8 + (int64_t)e * 2 * a.inter * kH;
+    up = gp + (int64_t)a.inter * kH;
+    gs = a.sgu + (int64_t)e * 2 * a.inter;
+    us = gs + a.inter;
+  } else {
+    const int half = s - kTopK;
+    gp = a.shgu8 + (int64_t)half * a.inter * kH;
+    up = a.shgu8 + (int64_t)(2 * a.inter + half * a.inter) * kH;
+    gs = a.sshgu + half * a.inter;
+    us = a.sshgu + 2 * a.inter + half * a.inter;
+  }
+  float sg[RPW], su[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    sg[r] = gs[i0 + r];
+    su[r] = us[i0 + r];
+  }
+  gp += (int64_t)i0 * kH;
+  up += (int64_t)i0 * kH;
+  uint4 wg[RPW][2], wu[RPW][2];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      wg[r][j] = ldg16_nt(gp + (int64_t)r * kH + (lane + 64 * j) * 16);
+      wu[r][j] = ldg16_nt(up + (int64_t)r * kH + (lane + 64 * j) * 16);
+    }
+  float ag[RPW], au[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) ag[r] = au[r] = 0.f;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const float* xl = &xs[(lane + 64 * j) * 16];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      ag[r] += dot16_fp8(wg[r][j], xl);
+      au[r] += dot16_fp8(wu[r][j], xl);
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1)
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      ag[r] += __shfl_xor(ag[r], off, 64);
+      au[r] += __shfl_xor(au[r], off, 64);
+    }
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+      a.hbuf[((int64_t)b * a.hbuf_routes + s) * a.inter + i0 + r] = f2bf(swiglu_bf(ag[r] * sg[r], au[r] * su[r]));
   }
 }
 
@@ -357,6 +453,41 @@ extern "C" int dsv2_moe_route_gateup_logits(const void* xn, int rows, const floa
   a.shgu = (const bf16_t*)sh_gate_up;
   a.hbuf = (bf16_t*)hbuf;
   return launch_route_gateup(a, rows, (hipStream_t)stream, "moe_route_gateup_logits");
+}
+
+extern "C" int dsv2_moe_route_gateup_logits_fp8(const void* xn, int rows, const float* logits, float scaling,
+                                                int32_t* ids, float* weights, const uint8_t* w_gate_up,
+                                                const float* gate_up_scale, const uint8_t* sh_gate_up,
+                                                const float* sh_gate_up_scale, int inter, void* hbuf, void* stream) {
+  constexpr int RPW = 4;
+  DSV2_REQUIRE(xn && logits && ids && weights && w_gate_up && gate_up_scale && hbuf, DSV2_E_NULL,
+               "moe_route_gateup_logits_fp8: null pointer");
+  DSV2_REQUIRE(!sh_gate_up == !sh_gate_up_scale, DSV2_E_NULL,
+               "moe_route_gateup_logits_fp8: shared weights and their scales go together");
+  const int nr = sh_gate_up ? kTopK + 2 : kTopK;
+  DSV2_REQUIRE(rows >= 0 && (int64_t)rows * nr <= 65535 && inter > 0 && inter % RPW == 0, DSV2_E_SHAPE,
+               "moe_route_gateup_logits_fp8: bad shape (inter %% 4 == 0)");
+  DSV2_REQUIRE(dsv2_aligned16(xn) && dsv2_aligned16(w_gate_up) && (!sh_gate_up || dsv2_aligned16(sh_gate_up)),
+               DSV2_E_ALIGN, "moe_route_gateup_logits_fp8: alignment");
+  if (rows == 0) return DSV2_OK;
+  RouteGateupArgs a{};
+  a.nr = nr;
+  a.hbuf_routes = kTopK + 2;
+  a.inter = inter;
+  a.xn = (const bf16_t*)xn;
+  a.ids = ids;
+  a.logits = logits;
+  a.scaling = scaling;
+  a.wts = weights;
+  a.wgu8 = w_gate_up;
+  a.sgu = gate_up_scale;
+  a.shgu8 = sh_gate_up;
+  a.sshgu = sh_gate_up_scale;
+  a.hbuf = (bf16_t*)hbuf;
+  a.gu_blocks = (inter + 4 * RPW - 1) / (4 * RPW);
+  const int64_t grid = (int64_t)rows * nr * a.gu_blocks;
+  hipLaunchKernelGGL(route_gateup_fp8_kernel<RPW>, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, a);
+  return dsv2_launch_status("moe_route_gateup_logits_fp8");
 }
 
 // ---------------------------------------------------------------------------
@@ -458,6 +589,131 @@ __global__ __launch_bounds__(256) void route_down_kernel(const bf16_t* __restric
     if (res) y = rbf(rv + y);
     out[(int64_t)b * kH + j0 + r] = f2bf(y);
   }
+}
+
+// fp8 weights: the same work with every down row in e4m3 (16 weights and 16 hbuf values per
+// lane chunk, at most 2 chunks per lane) and the row's fp32 scale on the fp32 dot product.
+template <int NR>
+__global__ __launch_bounds__(256) void route_down_fp8_kernel(const bf16_t* __restrict__ hbuf,
+                                                             const int32_t* __restrict__ ids,
+                                                             const float* __restrict__ wts,
+                                                             const uint8_t* __restrict__ wd,
+                                                             const float* __restrict__ sd,
+                                                             const uint8_t* __restrict__ shd,
+                                                             const float* __restrict__ ssh, int inter,
+                                                             int hbuf_routes, const bf16_t* __restrict__ res,
+                                                             bf16_t* __restrict__ out) {
+  __shared__ float part[8][2];
+  const int b = blockIdx.y;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int j0 = blockIdx.x * 2;
+  const int nch = inter >> 4;
+  constexpr int kMaxCh = 2;  // chunks of 16 per lane: ceil(88 / 64) for inter = 1408
+  int eid[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) eid[q] = ids[b * kTopK + min(2 * wv + q, kTopK - 1)];
+  const int jr = j0 + (threadIdx.x & 1);
+  bf16_t resb = (res ? res : hbuf)[res ? (int64_t)b * kH + jr : 0];
+  if (2 * wv < NR) {
+    const uint8_t* wrow[2];
+    int64_t wstride[2];
+    float sc[2][2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int s = 2 * wv + q;
+      if (s < kTopK) {
+        const int e = min(max(eid[q], 0), kE - 1);
+        wrow[q] = wd + (int64_t)e * kH * inter + (int64_t)j0 * inter;
+        wstride[q] = inter;
+        sc[q][0] = sd[(int64_t)e * kH + j0];
+        sc[q][1] = sd[(int64_t)e * kH + j0 + 1];
+      } else {
+        wrow[q] = shd + (int64_t)(s - kTopK) * inter + (int64_t)j0 * 2 * inter;
+        wstride[q] = 2 * inter;
+        sc[q][0] = ssh[j0];
+        sc[q][1] = ssh[j0 + 1];
+      }
+    }
+    uint4 w[2][2][kMaxCh], x[2][kMaxCh][2];
+#pragma unroll
+    for (int k = 0; k < kMaxCh; ++k) {
+      const int c = min(lane + 64 * k, nch - 1);
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const bf16_t* hx = hbuf + ((int64_t)b * hbuf_routes + 2 * wv + q) * inter + c * 16;
+        x[q][k][0] = ldg16(hx);
+        x[q][k][1] = ldg16(hx + 8);
+#pragma unroll
+        for (int r = 0; r < 2; ++r) w[q][r][k] = ldg16_nt(wrow[q] + r * wstride[q] + c * 16);
+      }
+    }
+    pin(resb);
+    float acc[2][2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        float a = 0.f;
+#pragma unroll
+        for (int k = 0; k < kMaxCh; ++k) {
+          float hx[16];
+          unpack8(x[q][k][0], hx);
+          unpack8(x[q][k][1], hx + 8);
+          const float d = dot16_fp8(w[q][r][k], hx);
+          a += lane + 64 * k < nch ? d : 0.f;
+        }
+        acc[q][r] = a;
+      }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1)
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int r = 0; r < 2; ++r) acc[q][r] += __shfl_xor(acc[q][r], off, 64);
+    if (lane == 0) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int r = 0; r < 2; ++r) part[2 * wv + q][r] = acc[q][r] * sc[q][r];
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < 2) {
+    const int r = threadIdx.x;
+    float routed = 0.f;
+    const float rv = res ? bf2f(resb) : 0.f;
+#pragma unroll
+    for (int s = 0; s < kTopK; ++s) routed += wts[b * kTopK + s] * rbf(part[s][r]);
+    float y = rbf(routed);
+    if (NR > kTopK) y = rbf(y + rbf(part[kTopK][r] + part[kTopK + 1][r]));
+    if (res) y = rbf(rv + y);
+    out[(int64_t)b * kH + j0 + r] = f2bf(y);
+  }
+}
+
+extern "C" int dsv2_moe_route_down_fp8(const void* hbuf, int rows, const int32_t* ids, const float* weights,
+                                       const uint8_t* w_down, const float* down_scale, const uint8_t* sh_down,
+                                       const float* sh_down_scale, int inter, int hbuf_routes, const void* residual,
+                                       void* out, void* stream) {
+  DSV2_REQUIRE(hbuf && ids && weights && w_down && down_scale && out, DSV2_E_NULL, "moe_route_down_fp8: null pointer");
+  DSV2_REQUIRE(!sh_down == !sh_down_scale, DSV2_E_NULL, "moe_route_down_fp8: shared weights and their scales go together");
+  DSV2_REQUIRE(rows >= 0 && rows <= 65535 && inter > 0 && inter % 16 == 0 && inter <= 2 * 64 * 16, DSV2_E_SHAPE,
+               "moe_route_down_fp8: bad shape (inter %% 16 == 0, inter <= 2048)");
+  DSV2_REQUIRE(dsv2_aligned16(hbuf) && dsv2_aligned16(w_down) && (!sh_down || dsv2_aligned16(sh_down)),
+               DSV2_E_ALIGN, "moe_route_down_fp8: alignment");
+  DSV2_REQUIRE(hbuf_routes >= (sh_down ? kTopK + 2 : kTopK) && hbuf_routes <= kTopK + 2, DSV2_E_SHAPE,
+               "moe_route_down_fp8: hbuf_routes must cover the routes read");
+  if (rows == 0) return DSV2_OK;
+  const dim3 grid(kH / 2, rows);
+  if (sh_down)
+    hipLaunchKernelGGL((route_down_fp8_kernel<kTopK + 2>), grid, dim3(256), 0, (hipStream_t)stream,
+                       (const bf16_t*)hbuf, ids, weights, w_down, down_scale, sh_down, sh_down_scale, inter,
+                       hbuf_routes, (const bf16_t*)residual, (bf16_t*)out);
+  else
+    hipLaunchKernelGGL((route_down_fp8_kernel<kTopK>), grid, dim3(256), 0, (hipStream_t)stream, (const bf16_t*)hbuf,
+                       ids, weights, w_down, down_scale, nullptr, nullptr, inter, hbuf_routes,
+                       (const bf16_t*)residual, (bf16_t*)out);
+  return dsv2_launch_status("moe_route_down_fp8");
 }
 
 extern "C" int dsv2_moe_route_down(const void* hbuf, int rows, const int32_t* ids, const float* weights,

@@ -170,19 +170,29 @@ def _graph_node_count(g: torch.cuda.CUDAGraph) -> int:
 
 class DecodeEngine:
     def __init__(self, weights: ModelWeights, capacities: list[int], family: str = "small",
-                 max_prefill_rows: int = 8192, device="cuda", mla_path: str = "fused", moe_tile: int | None = None):
+                 max_prefill_rows: int = 8192, device="cuda", mla_path: str = "fused", moe_tile: int | None = None,
+                 expert_dtype: str = "bf16"):
         """capacities: cache tokens of each row (slot).  moe_tile (batch family): fix the
         grouped MoE token tile (16, 32 or 64) instead of choosing it from the routing of one
-        eager step at capture -- for a serving loop whose batch changes under one graph."""
+        eager step at capture -- for a serving loop whose batch changes under one graph.
+        expert_dtype "fp8" (small family): the decode step reads the e4m3 expert weights of
+        quantize_experts_fp8 (prefill keeps the bf16 kernels on the dequantized weights)."""
         if family not in FAMILIES:
             raise ValueError(f"Unknown kernel family: {family}")
         if mla_path not in ("split", "fused"):
             raise ValueError(f"Unknown MLA path: {mla_path}")
+        if expert_dtype not in ("bf16", "fp8"):
+            raise ValueError(f"Unknown expert dtype: {expert_dtype}")
+        if expert_dtype == "fp8" and family != "small":
+            raise NotImplementedError("fp8 expert weights: small kernel family only")
+        if expert_dtype == "fp8" and not weights.fp8_experts:
+            raise ValueError("fp8 expert weights: run dsv2lite.quantize_experts_fp8(weights) first")
         cfg = weights.cfg
         cfg.check_kernel_dims()
         self.cfg = cfg
         self.w = weights
         self.family = family
+        self.expert_dtype = expert_dtype
         self.device = torch.device(device)
         self.B = len(capacities)
         self.cache = CompressedKVCache(cfg.n_layers, capacities, device=device, row=cfg.cache_row)
@@ -282,6 +292,14 @@ class DecodeEngine:
             if L.moe:
                 call("dsv2_router_logits", ptr(b.h), H, ptr(L.ln_post), c.eps, ptr(L.w_router), R, ptr(b.xn),
                      ptr(b.router_logits), st)
+                if self.expert_dtype == "fp8" and b is self.buf:
+                    call("dsv2_moe_route_gateup_logits_fp8", ptr(b.xn), R, ptr(b.router_logits), c.routed_scaling,
+                         ptr(b.ids32), ptr(b.wts), ptr(L.w_gu8), ptr(L.gu_scale), ptr(L.sh_gu8), ptr(L.sh_gu_scale),
+                         c.moe_inter, ptr(b.hbuf), st)
+                    call("dsv2_moe_route_down_fp8", ptr(b.hbuf), R, ptr(b.ids32), ptr(b.wts), ptr(L.w_down8),
+                         ptr(L.down_scale), ptr(L.sh_down8), ptr(L.sh_down_scale), c.moe_inter, c.top_k + 2, ptr(b.h),
+                         ptr(b.h), st)
+                    return
                 call("dsv2_moe_route_gateup_logits", ptr(b.xn), R, ptr(b.router_logits), c.routed_scaling,
                      ptr(b.ids32), ptr(b.wts), ptr(L.w_gu), ptr(L.sh_gu), c.moe_inter, ptr(b.hbuf), st)
                 call("dsv2_moe_route_down", ptr(b.hbuf), R, ptr(b.ids32), ptr(b.wts), ptr(L.w_down), ptr(L.sh_down),

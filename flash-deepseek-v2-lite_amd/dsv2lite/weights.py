@@ -16,6 +16,10 @@ Packed layouts (HBM):
   w_down[E, H, I]
   sh_gu [2*2816, 2048]  = cat(shared gate_proj, shared up_proj); sh_down [2048, 2816]
   dense w_gu [2*10944, 2048], w_down [2048, 10944]
+
+FP8 expert weights (quantize_experts_fp8): the same four MoE layouts in OCP e4m3 bytes
+(w_gu8, w_down8, sh_gu8, sh_down8) with one fp32 power-of-two scale per output row
+(gu_scale [E, 2I], down_scale [E, H], sh_gu_scale [2*2816], sh_down_scale [2048]).
 """
 
 from __future__ import annotations
@@ -45,6 +49,15 @@ class LayerWeights:
     w_router: torch.Tensor | None = None
     sh_gu: torch.Tensor | None = None
     sh_down: torch.Tensor | None = None
+    # fp8 (e4m3) copies of the MoE weights and their per-row scales, set by quantize_experts_fp8
+    w_gu8: torch.Tensor | None = None
+    gu_scale: torch.Tensor | None = None
+    w_down8: torch.Tensor | None = None
+    down_scale: torch.Tensor | None = None
+    sh_gu8: torch.Tensor | None = None
+    sh_gu_scale: torch.Tensor | None = None
+    sh_down8: torch.Tensor | None = None
+    sh_down_scale: torch.Tensor | None = None
 
 
 @dataclass
@@ -54,6 +67,7 @@ class ModelWeights:
     norm: torch.Tensor
     lm_head: torch.Tensor
     layers: list[LayerWeights] = field(default_factory=list)
+    fp8_experts: bool = False  # quantize_experts_fp8 has run
 
     def hf_layer(self, i: int) -> dict:
         """HF-named views of layer i (shared storage; kv_b rebuilt) for checkers."""
@@ -156,3 +170,59 @@ def pack_hf_layer(cfg: DSV2Config, hf: dict, device="cuda") -> LayerWeights:
                             sh_down=t(hf["sh_down"]))
     return LayerWeights(**common, moe=False, w_gu=torch.cat((t(hf["gate_proj"]), t(hf["up_proj"]))),
                         w_down=t(hf["down_proj"]))
+
+
+E4M3_MAX = 448.0  # largest finite OCP e4m3 (float8_e4m3fn) value
+
+
+def fp8_row_scales(w: torch.Tensor) -> torch.Tensor:
+    """Per-row power-of-two scales s (fp32, shape w.shape[:-1]) with max|w| / s <= 448: the
+    smallest such power of two, 1 for an all-zero row.  A power of two keeps w / s exact and
+    makes e4m3 * s exactly a bf16 value."""
+    amax = w.abs().amax(dim=-1).float()
+    m, e = torch.frexp(amax / E4M3_MAX)  # amax / 448 = m * 2**e, m in [0.5, 1)
+    e = torch.where(m == 0.5, e - 1, e)  # an exact power of two needs no step up
+    s = torch.ldexp(torch.ones_like(amax), e)
+    return torch.where(amax > 0, s, torch.ones_like(amax))
+
+
+def quantize_rows_fp8(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """(e4m3 bytes as uint8, fp32 row scales) of a bf16 matrix stack [..., K]: each weight
+    rounded to the nearest e4m3 value of w / s (ties to even), s from fp8_row_scales."""
+    s = fp8_row_scales(w)
+    q = (w.float() / s.unsqueeze(-1)).to(torch.float8_e4m3fn)
+    return q.view(torch.uint8), s
+
+
+def dequantize_rows_fp8(q: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
+    """bf16 value of every e4m3 weight times its row scale (exact: 4 significant bits)."""
+    return (q.view(torch.float8_e4m3fn).float() * s.unsqueeze(-1)).to(BF16)
+
+
+def quantize_experts_fp8(w: ModelWeights) -> ModelWeights:
+    """Quantize every MoE layer's routed and shared expert weights to e4m3 with per-row
+    power-of-two scales (in place).  The bf16 tensors are overwritten with the dequantized
+    values, so the bf16 kernels (prefill, batch family) and any checker see exactly the
+    weights the fp8 kernels read.  Returns w."""
+    if w.fp8_experts:
+        return w
+    for L in w.layers:
+        if not L.moe:
+            continue
+        E = L.w_gu.shape[0]
+        L.w_gu8 = torch.empty(L.w_gu.shape, dtype=torch.uint8, device=L.w_gu.device)
+        L.w_down8 = torch.empty(L.w_down.shape, dtype=torch.uint8, device=L.w_down.device)
+        L.gu_scale = torch.empty(L.w_gu.shape[:2], dtype=torch.float32, device=L.w_gu.device)
+        L.down_scale = torch.empty(L.w_down.shape[:2], dtype=torch.float32, device=L.w_down.device)
+        for e in range(E):  # one expert at a time keeps the fp32 temporaries small
+            for src, q8, sc in ((L.w_gu, L.w_gu8, L.gu_scale), (L.w_down, L.w_down8, L.down_scale)):
+                q, s = quantize_rows_fp8(src[e])
+                q8[e].copy_(q)
+                sc[e].copy_(s)
+                src[e].copy_(dequantize_rows_fp8(q, s))
+        L.sh_gu8, L.sh_gu_scale = quantize_rows_fp8(L.sh_gu)
+        L.sh_gu.copy_(dequantize_rows_fp8(L.sh_gu8, L.sh_gu_scale))
+        L.sh_down8, L.sh_down_scale = quantize_rows_fp8(L.sh_down)
+        L.sh_down.copy_(dequantize_rows_fp8(L.sh_down8, L.sh_down_scale))
+    w.fp8_experts = True
+    return w

@@ -279,6 +279,23 @@ int dsv2_moe_route_down(const void* hbuf, int rows, const int32_t* ids, const fl
                         const void* w_down, const void* sh_down, int inter, int hbuf_routes, const void* shared_y,
                         const void* residual, void* out, void* stream);
 
+/* FP8 expert weights (small family): dsv2_moe_route_gateup_logits / dsv2_moe_route_down with
+ * every routed and shared expert row in OCP e4m3 (1 byte per weight, same row layouts) and one
+ * fp32 scale per row: weight = e4m3 value * scale (gate_up_scale [64, 2*inter], sh_gate_up_scale
+ * [2*2*inter], down_scale [64, 2048], sh_down_scale [2048]).  Each row's dot product is taken
+ * in fp32 over the e4m3 values (converted by v_cvt_pk_f32_fp8) and multiplied by the row's
+ * scale; the rounding points are those of the bf16 entry points.  No counterpart in the
+ * reference (bf16 only): the low-precision weights of the build's next steps.  inter % 4 == 0
+ * (gate_up), inter % 16 == 0 and <= 2048 (down). */
+int dsv2_moe_route_gateup_logits_fp8(const void* xn, int rows, const float* logits, float scaling, int32_t* ids,
+                                     float* weights, const uint8_t* w_gate_up, const float* gate_up_scale,
+                                     const uint8_t* sh_gate_up, const float* sh_gate_up_scale, int inter, void* hbuf,
+                                     void* stream);
+int dsv2_moe_route_down_fp8(const void* hbuf, int rows, const int32_t* ids, const float* weights,
+                            const uint8_t* w_down, const float* down_scale, const uint8_t* sh_down,
+                            const float* sh_down_scale, int inter, int hbuf_routes, const void* residual, void* out,
+                            void* stream);
+
 /* Batch family bucketing (one workgroup, deterministic counting sort by expert):
  *   sorted_routes[p] = route index r*6+s in expert order, stable in r;
  *   route_pos[r*6+s] = p;  tiles[t] = {expert, first slot, count<=tile_tokens, 0} (int32x4);

@@ -45,13 +45,16 @@ class Pair:
         return r16
 
 
-def build_model(n_layers: int, max_pos: int = 512):
+def build_model(n_layers: int, max_pos: int = 512, fp8: bool = False):
     """Full-width random-init DeepSeek-V2-Lite with n_layers layers (layer 0 dense) on the
-    GPU, and the oracle pair on fp32 host copies of the same weights."""
+    GPU, and the oracle pair on fp32 host copies of the same weights.  fp8: the expert
+    weights quantized to e4m3 first, so the oracle holds their dequantized values."""
     import dsv2lite
 
     cfg = dsv2lite.DSV2Config(n_layers=n_layers)
     w = dsv2lite.init_weights(cfg, device="cuda", seed=0)
+    if fp8:
+        dsv2lite.quantize_experts_fp8(w)
     ow = {"layers": [{k: v.float().cpu() for k, v in w.hf_layer(i).items()} for i in range(n_layers)],
           "embed": w.embed.float().cpu(), "norm": w.norm.float().cpu(), "lm_head": w.lm_head.float().cpu()}
     om = O.OracleModel(O.Dims(n_layers=n_layers), ow, mode="bf16", max_pos=max_pos)
