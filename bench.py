@@ -186,6 +186,22 @@ def time_other_kernels(eng, family: str, ctx_rows: list[int]) -> dict:
             entry("mla_fused_kernel (W_UK absorption + attention + W_UV, one workgroup per head)", fused, moe,
                   2 * 2 * 16 * 128 * 512 + kv + B * 2048 * 2)
 
+        def prepare(li):
+            L = eng.w.layers[li]
+            call("dsv2_mla_prepare", ptr(b.qkva), c.qkva_dim, B, ptr(eng.cache.pos), ptr(eng.cache.base),
+                 ptr(eng.cache.cap), ptr(L.kv_norm), c.eps, ptr(eng.cos), ptr(eng.sin), eng.max_pos, ptr(L.w_ukt),
+                 ptr(eng.cache.layer(li)), ptr(b.q), None, stream_ptr())
+
+        def attend(li):
+            L = eng.w.layers[li]
+            call("dsv2_mla_attend", ptr(b.q), ptr(eng.cache.layer(li)), ptr(eng.cache.base), ptr(eng.cache.pos),
+                 ptr(eng.cache.cap), B, ptr(L.w_uv), eng.scale, ptr(b.attn), c.hidden, stream_ptr())
+        if eng.spread_mla:
+            entry("mla_prepare_kernel<true> (W_UK absorption over 128 workgroups + new cache row + RoPE)", prepare,
+                  moe, 2 * 16 * 128 * 512 + B * 3648 * 2 + B * 16 * 576 * 2)
+            entry("mla_attend_kernel (attention + W_UV over heads x W_UV quarters)", attend, moe,
+                  2 * 16 * 128 * 512 + kv + B * 16 * 576 * 2 + B * 2048 * 2)
+
         def down(li):
             L = eng.w.layers[li]
             call("dsv2_moe_route_down", ptr(b.hbuf), B, ptr(b.ids32), ptr(b.wts), ptr(L.w_down), ptr(L.sh_down),
@@ -671,8 +687,9 @@ def main() -> None:
     ap.add_argument("--family", choices=("small", "batch"), default=None)
     ap.add_argument("--expert-dtype", choices=("bf16", "fp8"), default="bf16",
                     help="one config: MoE expert weights in bf16 or e4m3 (small family); 'all' runs C1 both ways")
-    ap.add_argument("--mla-path", choices=("fused", "split"), default="fused",
-                    help="small family: one fused MLA kernel per layer, or prepare + split-KV decode + combine")
+    ap.add_argument("--mla-path", choices=("fused", "spread", "split"), default="spread",
+                    help="small family: prepare + spread attention (two launches), one fused MLA kernel per "
+                         "layer, or prepare + split-KV decode + combine")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 3 plain 512 MiB device copies (the reference kernel for scaling the "

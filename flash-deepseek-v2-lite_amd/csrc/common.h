@@ -140,6 +140,24 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Wave64 sum on the VALU: DPP within each 16-lane row (quad_perm xor 1, xor 2, then
+// row_half_mirror and row_mirror leave the row's sum in all 16 lanes), then the four row
+// sums read into scalars.  Uniform result; a different (fixed) summation order from
+// wave_sum, with no LDS traffic and a short dependency chain.
+#define DSV2_DPP(v, ctrl) \
+  __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, (v)), (ctrl), 0xF, 0xF, false))
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += DSV2_DPP(v, 0xB1);   // quad_perm [1,0,3,2]
+  v += DSV2_DPP(v, 0x4E);   // quad_perm [2,3,0,1]
+  v += DSV2_DPP(v, 0x141);  // row_half_mirror
+  v += DSV2_DPP(v, 0x140);  // row_mirror
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, DSV2_WAVE));

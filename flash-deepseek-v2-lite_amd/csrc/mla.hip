@@ -28,10 +28,12 @@ __device__ __forceinline__ void rope_pair(const bf16_t* x, const bf16_t* cs, con
   out[32 + t] = f2bf(o * bf2f(cs[32 + t]) + e * bf2f(sn[32 + t]));
 }
 
-// Workgroup (x, y) handles rows y*RB .. y*RB+RB-1.  With w_ukt != null every workgroup
-// computes 64 of the 16*512 absorbed outputs (rows of W_UK_h^T, K = 128 split over 16
-// lanes, weights requested first); workgroup x == 0 also writes the new cache rows
-// (kv-norm + RoPE(k_pe)) and RoPE(q_pe) of its rows.
+// Workgroup (x, y) handles rows y*RB .. y*RB+RB-1.  With w_ukt != null workgroups x < 128
+// each compute 64 of the 16*512 absorbed outputs (rows of W_UK_h^T, K = 128 split over 16
+// lanes, weights requested first) and workgroup x == 128 writes the new cache rows
+// (kv-norm + RoPE(k_pe)) and RoPE(q_pe) of its rows; without w_ukt workgroup 0 does the
+// latter.  w_uv_pf != null (the spread small-batch path): the absorbing workgroups also
+// bring mla_attend_kernel's W_UV rows into the L2 of the XCD that will read them.
 template <bool ABSORB>
 __global__ __launch_bounds__(256) void mla_prepare_kernel(const bf16_t* __restrict__ qkva, int64_t qs, int rows,
                                                           const int32_t* __restrict__ pos,
@@ -41,18 +43,56 @@ __global__ __launch_bounds__(256) void mla_prepare_kernel(const bf16_t* __restri
                                                           const bf16_t* __restrict__ cosT,
                                                           const bf16_t* __restrict__ sinT, int max_pos,
                                                           const bf16_t* __restrict__ w_ukt, bf16_t* __restrict__ cache,
-                                                          bf16_t* __restrict__ qout, int32_t* __restrict__ status) {
+                                                          bf16_t* __restrict__ qout, int32_t* __restrict__ status,
+                                                          const bf16_t* __restrict__ w_uv_pf) {
   constexpr int RB = ABSORB ? 8 : 1;  // RoPE/cache only: one row per workgroup
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int b0 = blockIdx.y * RB;
   const int nr = min(RB, rows - b0);
-  if (ABSORB) {
+  if (ABSORB && blockIdx.x < 128) {
     const int gi = tid >> 4, k = tid & 15;
     const int row0 = blockIdx.x * 64 + gi * 4;  // 4 consecutive rows of one head
     const int h = row0 / kLat, j0 = row0 % kLat;
     uint4 wr[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) wr[q] = ldg16(w_ukt + (int64_t)(row0 + q) * 128 + k * 8);
+    // Prefetch of the cached tokens of the block's first two rows for the attention launch
+    // that follows (each head's workgroups re-read every cached row there): the 16
+    // workgroups that share an XCD (block ids equal mod 8) each request every 16th token row
+    // of the first 256, so each XCD's L2 holds them when the attention starts.  The values
+    // only feed an empty asm after the absorption.
+    constexpr int kPf = (16 * (kRow / 8) + 255) / 256;  // 16 rows of 72 chunks over 256 threads
+    uint4 pf[2][kPf];
+    const int slot = blockIdx.x >> 3;
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      const int b = b0 + min(rr, nr - 1);
+      const int n = min(min(max(pos[b], 0), cap[b]), 256);  // rows [0, n) are already cached
+      const int nt = n > slot ? (n - 1 - slot) / 16 + 1 : 0;  // tokens slot, slot + 16, ... < n
+      const bf16_t* crow0 = cache + base[b] * kRow;
+#pragma unroll
+      for (int i = 0; i < kPf; ++i) {
+        const int c = tid + 256 * i;
+        const bool live = rr < nr && c < nt * (kRow / 8);
+        const int t = live ? slot + 16 * (c / (kRow / 8)) : 0;
+        pf[rr][i] = ldg16(crow0 + (int64_t)t * kRow + (live ? c % (kRow / 8) : 0) * 8);
+      }
+    }
+    // W_UV: the attention workgroup bid = 4h + qq (on XCD bid % 8) reads rows h*128 + qq*32
+    // .. +31; the 16 workgroups of this XCD take 16 rows each of its 8 such workgroups
+    uint4 pu[4];
+    if (w_uv_pf) {
+      const int abid = (blockIdx.x & 7) + 8 * (slot >> 1);
+      const int64_t row = (int64_t)(abid >> 2) * 128 + (abid & 3) * 32 + (slot & 1) * 16;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int c = tid + 256 * i;  // 16 rows x 64 chunks of 16 bytes
+        pu[i] = ldg16(w_uv_pf + (row + (c >> 6)) * kLat + (c & 63) * 8);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pu[i] = make_uint4(0u, 0u, 0u, 0u);
+    }
     for (int r = 0; r < nr; ++r) {
       float qn[8];
       unpack8(ldg16(qkva + (b0 + r) * qs + h * 192 + k * 8), qn);
@@ -70,8 +110,16 @@ __global__ __launch_bounds__(256) void mla_prepare_kernel(const bf16_t* __restri
         *reinterpret_cast<uint2*>(qout + ((int64_t)(b0 + r) * kHeads + h) * kRow + j0) = o;
       }
     }
+    uint32_t acc = 0;
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr)
+#pragma unroll
+      for (int i = 0; i < kPf; ++i) acc ^= pf[rr][i].x;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc ^= pu[i].x;
+    asm volatile("" ::"v"(acc));
+    return;
   }
-  if (blockIdx.x != 0) return;
   for (int r = 0; r < nr; ++r) {
     const int b = b0 + r;
     int p = pos[b];
@@ -107,6 +155,17 @@ __global__ __launch_bounds__(256) void mla_prepare_kernel(const bf16_t* __restri
   }
 }
 
+// mla_prepare with absorption and the W_UV prefetch for mla_attend_kernel (dsv2_mla_spread)
+void mla_prepare_absorb_launch(const void* qkva, int64_t qkva_stride, int rows, const int32_t* pos,
+                              const int64_t* base, const int32_t* cap, const void* kv_norm_w, float eps,
+                              const void* rope_cos, const void* rope_sin, int max_pos, const void* w_ukt,
+                              const void* w_uv, void* cache, void* q_out, int32_t* status, hipStream_t stream) {
+  hipLaunchKernelGGL(mla_prepare_kernel<true>, dim3(kHeads * kLat / 64 + 1, (rows + 7) / 8), dim3(256), 0, stream,
+                     (const bf16_t*)qkva, qkva_stride, rows, pos, base, cap, (const bf16_t*)kv_norm_w, eps,
+                     (const bf16_t*)rope_cos, (const bf16_t*)rope_sin, max_pos, (const bf16_t*)w_ukt, (bf16_t*)cache,
+                     (bf16_t*)q_out, status, (const bf16_t*)w_uv);
+}
+
 extern "C" int dsv2_mla_prepare(const void* qkva, int64_t qkva_stride, int rows, const int32_t* pos,
                                 const int64_t* base, const int32_t* cap, const void* kv_norm_w, float eps,
                                 const void* rope_cos, const void* rope_sin, int max_pos, const void* w_ukt,
@@ -119,15 +178,17 @@ extern "C" int dsv2_mla_prepare(const void* qkva, int64_t qkva_stride, int rows,
                    dsv2_aligned16(q_out) && (!w_ukt || dsv2_aligned16(w_ukt)),
                DSV2_E_ALIGN, "mla_prepare: alignment");
   if (rows == 0) return DSV2_OK;
-  const dim3 grid(w_ukt ? kHeads * kLat / 64 : 1, w_ukt ? (rows + 7) / 8 : rows);
+  const dim3 grid(w_ukt ? kHeads * kLat / 64 + 1 : 1, w_ukt ? (rows + 7) / 8 : rows);
   if (w_ukt)
     hipLaunchKernelGGL(mla_prepare_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, (const bf16_t*)qkva,
                        qkva_stride, rows, pos, base, cap, (const bf16_t*)kv_norm_w, eps, (const bf16_t*)rope_cos,
-                       (const bf16_t*)rope_sin, max_pos, (const bf16_t*)w_ukt, (bf16_t*)cache, (bf16_t*)q_out, status);
+                       (const bf16_t*)rope_sin, max_pos, (const bf16_t*)w_ukt, (bf16_t*)cache, (bf16_t*)q_out, status,
+                       nullptr);
   else
     hipLaunchKernelGGL(mla_prepare_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, (const bf16_t*)qkva,
                        qkva_stride, rows, pos, base, cap, (const bf16_t*)kv_norm_w, eps, (const bf16_t*)rope_cos,
-                       (const bf16_t*)rope_sin, max_pos, nullptr, (bf16_t*)cache, (bf16_t*)q_out, status);
+                       (const bf16_t*)rope_sin, max_pos, nullptr, (bf16_t*)cache, (bf16_t*)q_out, status,
+                       nullptr);
   return dsv2_launch_status("mla_prepare");
 }
 

@@ -197,6 +197,24 @@ int dsv2_mla_fused(const void* qkva, int64_t qkva_stride, int rows, const int32_
                    int max_pos, const void* w_ukt, const void* w_uv, void* cache, float softmax_scale, void* out,
                    int64_t out_stride, int32_t* status, void* stream);
 
+/* The same result as dsv2_mla_fused after dsv2_mla_prepare(..., w_ukt, ...) has written the
+ * absorbed, rotated q [rows, 16, 576] and the new cache rows: per row 64 workgroups, one per
+ * (head, quarter of W_UV_h's 128 outputs), each attending the row's min(pos+1, cap) cached
+ * tokens and applying its 32 W_UV rows:
+ *   out[r, h*128 + i] = bf16(W_UV_h softmax(scale * q_h . C^T) C[:, :512])   (row stride out_stride).
+ * Same reference functions as dsv2_mla_fused (attention_decode_small.py:553-674, :932-1070). */
+int dsv2_mla_attend(const void* q, const void* cache, const int64_t* base, const int32_t* pos, const int32_t* cap,
+                    int rows, const void* w_uv, float softmax_scale, void* out, int64_t out_stride, void* stream);
+
+/* dsv2_mla_prepare (with W_UK absorption into q_buf [rows, 16, 576] bf16, a caller-owned
+ * buffer) followed by dsv2_mla_attend, as two launches: the same inputs and result as
+ * dsv2_mla_fused.  The absorbing workgroups also bring the attention's W_UV rows and the
+ * first 256 cached rows into L2 ahead of it.  Same reference functions as dsv2_mla_fused. */
+int dsv2_mla_spread(const void* qkva, int64_t qkva_stride, int rows, const int32_t* pos, const int64_t* base,
+                    const int32_t* cap, const void* kv_norm_w, float eps, const void* rope_cos, const void* rope_sin,
+                    int max_pos, const void* w_ukt, const void* w_uv, void* cache, void* q_buf, float softmax_scale,
+                    void* out, int64_t out_stride, int32_t* status, void* stream);
+
 /* q_len = 1 attention over an EXPANDED per-head cache (keys [B, H, L, q_dim], values
  * [B, H, L, v_dim], bf16, last dim contiguous, element strides as given):
  *   out[b, h, :] = bf16( softmax_n(scale * k[b,h,n,:] . q[b,h,:]) . v[b,h,n,:] ),  n = 0..pos

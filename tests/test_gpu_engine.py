@@ -31,6 +31,7 @@ def model():
 
 
 @pytest.mark.parametrize("family,lens,mla", [("small", [16], "split"), ("small", [16], "fused"), ("batch", [16], "split"),
+                                             ("small", [16], "spread"), ("small", [5, 11], "spread"),
                                              ("small", [5, 11], "split"), ("small", [5, 11], "fused"),
                                              ("batch", [5, 16, 9, 1], "split")])
 def test_engine_decode_vs_oracle(model, family, lens, mla):
@@ -81,13 +82,14 @@ def test_engine_decode_vs_oracle(model, family, lens, mla):
     print(f"{family} {lens}: greedy agreement {agree}/{total}", flush=True)
 
 
-@pytest.mark.parametrize("family", ["small", "batch"])
-def test_graph_replay_equals_eager_bitwise(model, family):
+@pytest.mark.parametrize("family,mla", [("small", "fused"), ("small", "spread"), ("batch", "split")])
+def test_graph_replay_equals_eager_bitwise(model, family, mla):
     import dsv2lite
 
     cfg, w, _ = model
     lens = [12, 7, 20]
-    eng = dsv2lite.DecodeEngine(w, [n + 16 for n in lens], family=family)
+    eng = dsv2lite.DecodeEngine(w, [n + 16 for n in lens], family=family, mla_path=mla)
+    assert eng.mla_path == mla
     eng.prefill([p.cuda() for p in _prompts(lens, seed=3)])
     snap = eng.snapshot()
     eager = []

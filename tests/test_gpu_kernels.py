@@ -665,6 +665,66 @@ def test_mla_fused_small_family_vs_fp32(lens):
     assert rel_err(out.float().cpu(), ref) < 1e-2
 
 
+@pytest.mark.parametrize("lens", [[1], [2, 3], [231], [40, 7, 300], [700]])
+def test_mla_attend_matches_fused_and_fp32(lens):
+    """prepare (absorption) + the spread attend kernel against the fused kernel on the same
+    inputs (same cache rows written, outputs within 1e-2) and the fp32 reference, at two
+    consecutive positions; the two-launch entry point equals the two calls bit for bit."""
+    from dsv2lite.config import DSV2Config
+    from dsv2lite.rope import cos_sin_tables
+
+    cfg = DSV2Config()
+    B = len(lens)
+    g = torch.Generator().manual_seed(7 * sum(lens))
+    cap = [L + 5 for L in lens]
+    base = torch.tensor([0] + list(torch.cumsum(torch.tensor(cap), 0)[:-1].tolist()), dtype=torch.int64)
+    cache0 = (torch.randn(sum(cap), 576, generator=g) * 0.5).to(BF).to(DEV)
+    qkva = rnd(B, 3648, seed=190)
+    kvw = (rnd(512, seed=191, std=0.1) + 1).to(BF)
+    w_uk = rnd(16, 128, 512, std=0.05, seed=192)
+    w_uv = rnd(16, 128, 512, std=0.05, seed=193)
+    w_ukt = w_uk.transpose(1, 2).contiguous()
+    cos, sin = cos_sin_tables(cfg, 1024, device=DEV)
+    scale = cfg.softmax_scale
+    base_d = base.to(DEV)
+    cap_d = torch.tensor(cap, dtype=torch.int32, device=DEV)
+    status = torch.zeros(1, dtype=torch.int32, device=DEV)
+    q = torch.empty(B, 16, 576, dtype=BF, device=DEV)
+    for step in range(2):
+        pos = torch.tensor([L - 1 + step for L in lens], dtype=torch.int32)
+        pos_d = pos.to(DEV)
+        c_f, c_s = cache0.clone(), cache0.clone()
+        out_f = torch.empty(B, 2048, dtype=BF, device=DEV)
+        out_s = torch.empty(B, 2048, dtype=BF, device=DEV)
+        call("dsv2_mla_fused", qkva.data_ptr(), 3648, B, pos_d.data_ptr(), base_d.data_ptr(), cap_d.data_ptr(),
+             kvw.data_ptr(), 1e-6, cos.data_ptr(), sin.data_ptr(), 1024, w_ukt.data_ptr(), w_uv.data_ptr(),
+             c_f.data_ptr(), scale, out_f.data_ptr(), 2048, status.data_ptr(), st())
+        call("dsv2_mla_prepare", qkva.data_ptr(), 3648, B, pos_d.data_ptr(), base_d.data_ptr(), cap_d.data_ptr(),
+             kvw.data_ptr(), 1e-6, cos.data_ptr(), sin.data_ptr(), 1024, w_ukt.data_ptr(), c_s.data_ptr(),
+             q.data_ptr(), status.data_ptr(), st())
+        call("dsv2_mla_attend", q.data_ptr(), c_s.data_ptr(), base_d.data_ptr(), pos_d.data_ptr(), cap_d.data_ptr(),
+             B, w_uv.data_ptr(), scale, out_s.data_ptr(), 2048, st())
+        torch.cuda.synchronize()
+        assert status.item() == 0
+        assert torch.equal(c_f, c_s), step  # the same new rows, nothing else written
+        # the attend kernel rounds the softmax weights to bf16 before p.v (as the reference
+        # does), the fused kernel keeps them in fp32: both within 1e-2 of fp32 math
+        assert rel_err(out_s.float().cpu(), out_f.float().cpu()) < 1e-2, step
+        q_full = q.float().cpu()
+        n = [L + step for L in lens]
+        rows = [c_s.float().cpu()[int(base[b]):int(base[b]) + n[b]] for b in range(B)]
+        olat = _mla_reference(q_full, rows, n, scale)
+        ref = torch.einsum("hij,bhj->bhi", w_uv.float().cpu(), olat).reshape(B, 2048)
+        assert rel_err(out_s.float().cpu(), ref) < 1e-2, step
+        # the two-launch entry point: identical cache rows and output
+        c_2, out_2, q2 = cache0.clone(), torch.empty_like(out_s), torch.empty_like(q)
+        call("dsv2_mla_spread", qkva.data_ptr(), 3648, B, pos_d.data_ptr(), base_d.data_ptr(), cap_d.data_ptr(),
+             kvw.data_ptr(), 1e-6, cos.data_ptr(), sin.data_ptr(), 1024, w_ukt.data_ptr(), w_uv.data_ptr(),
+             c_2.data_ptr(), q2.data_ptr(), scale, out_2.data_ptr(), 2048, status.data_ptr(), st())
+        torch.cuda.synchronize()
+        assert torch.equal(c_2, c_s) and torch.equal(q2, q) and torch.equal(out_2, out_s), step
+
+
 @pytest.mark.parametrize("rows", [1, 3])
 def test_router_logits_split_and_gateup_topk(rows):
     h, nw, wr = _router_case(rows, 95)
