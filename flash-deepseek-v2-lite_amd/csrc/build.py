@@ -50,6 +50,19 @@ def _compile(src: str) -> str:
     return obj
 
 
+def _check_no_missing_stubs(lib: str) -> None:
+    """A kernel whose host launch stub the compiler left undefined links into a library that
+    only fails when it is loaded; refuse it at build time."""
+    nm = shutil.which("nm")
+    if not nm:
+        return
+    r = subprocess.run([nm, "-D", "--undefined-only", lib], capture_output=True, text=True)
+    missing = [ln.split()[-1] for ln in r.stdout.splitlines() if "__device_stub__" in ln]
+    if missing:
+        os.remove(lib)
+        raise RuntimeError(f"undefined kernel launch stubs in the linked library: {missing}")
+
+
 def build(jobs: int | None = None, verbose: bool = False) -> str:
     os.makedirs(OBJDIR, exist_ok=True)
     jobs = jobs or min(len(SOURCES), os.cpu_count() or 4, 8)
@@ -60,6 +73,7 @@ def build(jobs: int | None = None, verbose: bool = False) -> str:
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    _check_no_missing_stubs(tmp)
     os.replace(tmp, OUT)
     if verbose:
         print(f"built {OUT}", file=sys.stderr)
