@@ -183,7 +183,8 @@ def time_other_kernels(eng, family: str, ctx_rows: list[int]) -> dict:
                  ptr(eng.cache.cap), ptr(L.kv_norm), c.eps, ptr(eng.cos), ptr(eng.sin), eng.max_pos, ptr(L.w_ukt),
                  ptr(L.w_uv), ptr(eng.cache.layer(li)), eng.scale, ptr(b.attn), c.hidden, None, stream_ptr())
         if eng.fused_mla:
-            entry("mla_fused_kernel (W_UK absorption + attention + W_UV, one workgroup per head)", fused, moe,
+            entry("mla_quad_kernel (one launch: absorption + new row + attention + W_UV, 64 workgroups per row)",
+                  fused, moe,
                   2 * 2 * 16 * 128 * 512 + kv + B * 2048 * 2)
 
         def prepare(li):

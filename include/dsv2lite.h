@@ -185,9 +185,11 @@ int dsv2_mla_combine(const float* part_o, const float* part_ml, const int32_t* p
                      int split_tokens, int max_splits, const void* w_uv, void* out, int64_t out_stride,
                      void* stream);
 
-/* Fused absorbed-MLA decode for a few rows: one workgroup per (row, head) does the W_UK
- * absorption, kv-norm + RoPE of the new token (stored to cache[base+pos] by the h == 0
- * workgroup), RoPE(q_pe), softmax over the row's pos+1 cached tokens and W_UV:
+/* Absorbed-MLA decode for a few rows in one launch: per row 64 workgroups, one per (head,
+ * quarter of W_UV_h's 128 outputs); each absorbs q_h = W_UK_h^T q_nope_h itself, builds the
+ * new token's kv-norm + RoPE(k_pe) row (stored to cache[base+pos] by one workgroup), applies
+ * RoPE(q_pe), attends the row's pos cached tokens plus the new one and applies its 32 W_UV
+ * rows:
  *   out[r, h*128 + i] = bf16(W_UV_h softmax(scale * q_h . C^T) C[:, :512]).
  * w_ukt is W_UK transposed [16, 512, 128].  Together with dsv2_gemv_bf16 for the q/kv and
  * o projections this replaces attention_decode_only_triton / attention_decode_small_batch_triton
