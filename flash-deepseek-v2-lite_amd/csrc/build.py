@@ -69,7 +69,10 @@ def build(jobs: int | None = None, verbose: bool = False) -> str:
     with cf.ThreadPoolExecutor(jobs) as ex:
         objs = list(ex.map(_compile, SOURCES))
     tmp = OUT + ".tmp"
-    cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp]
+    # -Bsymbolic: the library's launches bind to its own kernel handles, never to a same-named
+    # kernel of a library loaded before it with RTLD_GLOBAL (which would run that kernel on
+    # this library's argument layout)
+    cmd = [hipcc(), "-shared", "-fPIC", "-Wl,-Bsymbolic", f"--offload-arch={ARCH}", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")

@@ -213,7 +213,7 @@ __device__ __forceinline__ int routed_expert(float x, int s) {
     const float xj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), j));
     rank += (xj > x || (xj == x && j < lane)) ? 1 : 0;
   }
-  return __ffsll(__ballot(rank == s)) - 1;
+  return max(__ffsll(__ballot(rank == s)) - 1, 0);  // no lane holds rank s only when logits are NaN
 }
 
 // Expert of routed slot s of row b (wave 0 of the route's workgroups): from the row's ids, or
