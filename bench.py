@@ -239,11 +239,19 @@ def time_other_kernels(eng, family: str, ctx_rows: list[int]) -> dict:
     entry("expert-grouped down" + (" + the 2 shared-expert halves" if shared else "")
           + f" ({b.tile_tokens}-token tiles)", down, moe, nb)
 
+    if b.max_splits == 1:
+        def decode(li):
+            call("dsv2_mla_decode_rows", ptr(b.q), ptr(eng.cache.layer(li)), ptr(eng.cache.base), ptr(eng.cache.pos),
+                 ptr(eng.cache.cap), B, eng.scale, ptr(b.olat), 16 * 512, stream_ptr())
+        entry("mla_decode_kernel<true> (one workgroup per row, normalised o_lat out)", decode, moe,
+              kv + B * 16 * 576 * 2 + B * 16 * 512 * 2)
+        return out
+
     def decode(li):
         call("dsv2_mla_decode", ptr(b.q), ptr(eng.cache.layer(li)), ptr(eng.cache.base), ptr(eng.cache.pos),
              ptr(eng.cache.cap), B, b.split_tokens, b.max_splits, eng.scale, ptr(b.part_o), ptr(b.part_ml),
              stream_ptr())
-    entry(f"mla_decode_kernel (split-KV, {b.split_tokens}-token splits)", decode, moe,
+    entry(f"mla_decode_kernel<false> (split-KV, {b.split_tokens}-token splits)", decode, moe,
           kv + B * 16 * 576 * 2 + B * b.max_splits * 16 * 514 * 4)
     return out
 

@@ -195,23 +195,34 @@ extern "C" int dsv2_mla_prepare(const void* qkva, int64_t qkva_stride, int rows,
 // ---------------------------------------------------------------------------
 // split-KV decode
 // ---------------------------------------------------------------------------
+// DIRECT (one split per row, split_tokens covering every row): the workgroup's softmax is
+// the row's, so it writes o_lat = O / l as bf16 (out [rows, 16 * 512], row stride os) --
+// the value dsv2_mla_combine computes from a single split, bit for bit -- and no partials.
+template <bool DIRECT>
 __global__ __launch_bounds__(256, 2) void mla_decode_kernel(const bf16_t* __restrict__ q,
                                                             const bf16_t* __restrict__ cache,
                                                             const int64_t* __restrict__ base,
                                                             const int32_t* __restrict__ pos,
                                                             const int32_t* __restrict__ cap, int split_tokens,
                                                             int max_splits, float scale_log2,
-                                                            float* __restrict__ part_o, float* __restrict__ part_ml) {
+                                                            float* __restrict__ part_o, float* __restrict__ part_ml,
+                                                            bf16_t* __restrict__ out, int64_t os) {
   __shared__ __attribute__((aligned(16))) bf16_t lds[2][kTile * kLdsRow];
   __shared__ floatx4_t spart[4][64];  // per-wave partial S^T (one 16-token block, half of K)
   const int s = blockIdx.x, b = blockIdx.y;
   const int len = min(pos[b] + 1, cap[b]);  // never past the row's own slots
   const int t_begin = s * split_tokens;
-  if (t_begin >= len) return;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, li = lane & 15, kg = lane >> 4;
+  if (t_begin >= len) {
+    if (DIRECT) {  // a row with no cached token (capacity 0): zeros, as the combine writes
+#pragma unroll
+      for (int j = 0; j < 4; ++j) *reinterpret_cast<uint4*>(out + b * os + tid * 32 + j * 8) = make_uint4(0, 0, 0, 0);
+    }
+    return;
+  }
   const int t_end = min(len, t_begin + split_tokens);
   const int ntiles = (t_end - t_begin + kTile - 1) / kTile;
   const bf16_t* crow = cache + base[b] * kRow;
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, li = lane & 15, kg = lane >> 4;
 
   // S^T = K Q^T is split over the waves: wave w scores 16-token block w >> 1 of every tile
   // over k steps [9*(w & 1), 9*(w & 1) + 9) of the 18; the pair's partials meet in LDS.
@@ -332,6 +343,18 @@ __global__ __launch_bounds__(256, 2) void mla_decode_kernel(const bf16_t* __rest
     if (it + 2 >= ntiles) break;
   }
   // O^T layout: lane holds head li, dims wv*128 + mb*16 + 4kg + e
+  if (DIRECT) {
+    const float inv = 1.0f / l_run;  // the combine's weight of a lone split: exp2(0) / l
+    bf16_t* ob = out + b * os + li * kLat + wv * 128 + 4 * kg;
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) {
+      uint2 v;
+      v.x = pack2(__builtin_fmaf(inv, acc[mb][0], 0.f), __builtin_fmaf(inv, acc[mb][1], 0.f));
+      v.y = pack2(__builtin_fmaf(inv, acc[mb][2], 0.f), __builtin_fmaf(inv, acc[mb][3], 0.f));
+      *reinterpret_cast<uint2*>(ob + mb * 16) = v;
+    }
+    return;
+  }
   float* po = part_o + (((int64_t)b * max_splits + s) * kHeads + li) * kLat + wv * 128 + 4 * kg;
 #pragma unroll
   for (int mb = 0; mb < 8; ++mb)
@@ -354,10 +377,27 @@ extern "C" int dsv2_mla_decode(const void* q, const void* cache, const int64_t* 
                "mla_decode: alignment");
   if (rows == 0) return DSV2_OK;
   const float scale_log2 = softmax_scale * 1.4426950408889634f;
-  hipLaunchKernelGGL(mla_decode_kernel, dim3(max_splits, rows), dim3(256), 0, (hipStream_t)stream,
+  hipLaunchKernelGGL(mla_decode_kernel<false>, dim3(max_splits, rows), dim3(256), 0, (hipStream_t)stream,
                      (const bf16_t*)q, (const bf16_t*)cache, base, pos, cap, split_tokens, max_splits, scale_log2, part_o,
-                     part_ml);
+                     part_ml, nullptr, 0);
   return dsv2_launch_status("mla_decode");
+}
+
+extern "C" int dsv2_mla_decode_rows(const void* q, const void* cache, const int64_t* base, const int32_t* pos,
+                                    const int32_t* cap, int rows, float softmax_scale, void* olat, int64_t olat_stride,
+                                    void* stream) {
+  DSV2_REQUIRE(q && cache && base && pos && cap && olat, DSV2_E_NULL, "mla_decode_rows: null pointer");
+  DSV2_REQUIRE(rows >= 0 && rows <= 65535, DSV2_E_SHAPE, "mla_decode_rows: bad rows");
+  DSV2_REQUIRE(dsv2_aligned16(q) && dsv2_aligned16(cache) && dsv2_aligned16(olat) && olat_stride % 8 == 0 &&
+                   olat_stride >= kHeads * kLat,
+               DSV2_E_ALIGN, "mla_decode_rows: alignment (16-byte o_lat rows of >= 8192 elements)");
+  if (rows == 0) return DSV2_OK;
+  const float scale_log2 = softmax_scale * 1.4426950408889634f;
+  // one split per row covering all of it (2^30 tokens would be 1.2 TB of one row's cache)
+  hipLaunchKernelGGL(mla_decode_kernel<true>, dim3(1, rows), dim3(256), 0, (hipStream_t)stream, (const bf16_t*)q,
+                     (const bf16_t*)cache, base, pos, cap, 1 << 30, 1, scale_log2, nullptr, nullptr, (bf16_t*)olat,
+                     olat_stride);
+  return dsv2_launch_status("mla_decode_rows");
 }
 
 // ---------------------------------------------------------------------------
@@ -383,11 +423,13 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(const float* __restric
     for (int r = 0; r < 8; ++r) wr[r] = ldg16(wp + (int64_t)r * kLat);
   }
   // the first 8 splits' partial outputs are requested before the (m, l) merge; further
-  // splits come 8 loads at a time (split indices clamped, masked where used)
+  // splits come 8 loads at a time (split indices clamped into [0, ns), masked where used; a
+  // row with nothing cached, ns = 0, reads its first split's slot and writes zeros)
   const float* po = part_o + ((int64_t)b * max_splits * kHeads + h) * kLat + 2 * tid;
   float2 pv[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) pv[j] = *reinterpret_cast<const float2*>(po + (int64_t)min(j, ns - 1) * kHeads * kLat);
+  for (int j = 0; j < 8; ++j)
+    pv[j] = *reinterpret_cast<const float2*>(po + (int64_t)max(min(j, ns - 1), 0) * kHeads * kLat);
   if (wv == 0) {
     const float* pm = part_ml + ((int64_t)b * max_splits * kHeads + h) * 2;
     const float m = lane < ns ? pm[(int64_t)lane * kHeads * 2] : -INFINITY;

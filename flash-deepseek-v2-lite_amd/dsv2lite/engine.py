@@ -262,6 +262,15 @@ class DecodeEngine:
             call("dsv2_gemm_bf16", ptr(b.qkva), c.qkva_dim, c.q_head, R, c.qk_nope, ptr(L.w_ukt),
                  c.kv_rank * c.qk_nope, c.kv_rank, c.n_heads, None, 0, ptr(b.q), c.n_heads * c.cache_row,
                  c.cache_row, 0, st)
+        if family == "batch" and b.max_splits == 1:
+            # one split per row (~256+ rows fill the GPU): normalised o_lat straight from the decode
+            call("dsv2_mla_decode_rows", ptr(b.q), ptr(cache), ptr(base), ptr(pos), ptr(cap), R, self.scale,
+                 ptr(b.olat), c.n_heads * c.kv_rank, st)
+            call("dsv2_gemm_bf16", ptr(b.olat), c.n_heads * c.kv_rank, c.kv_rank, R, c.kv_rank, ptr(L.w_uv),
+                 c.v_dim * c.kv_rank, c.v_dim, c.n_heads, None, 0, ptr(b.attn), c.hidden, c.v_dim, 0, st)
+            call("dsv2_gemm_bf16", ptr(b.attn), c.hidden, 0, R, c.hidden, ptr(L.w_o), 0, c.hidden, 1, ptr(b.h),
+                 c.hidden, ptr(b.h), c.hidden, 0, 0, st)
+            return
         call("dsv2_mla_decode", ptr(b.q), ptr(cache), ptr(base), ptr(pos), ptr(cap), R, b.split_tokens,
              b.max_splits, self.scale, ptr(b.part_o), ptr(b.part_ml), st)
         if family == "small":

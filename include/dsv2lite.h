@@ -176,6 +176,15 @@ int dsv2_mla_decode(const void* q, const void* cache, const int64_t* base, const
                     int rows, int split_tokens, int max_splits, float softmax_scale, float* part_o, float* part_ml,
                     void* stream);
 
+/* dsv2_mla_decode with one split per row (a workgroup attends the whole row) and the
+ * normalisation done in the same launch: olat[r, h*512 + j] = bf16 o_lat [rows, 16, 512]
+ * (row stride olat_stride >= 8192), equal bit for bit to dsv2_mla_decode + dsv2_mla_combine
+ * (w_uv == NULL) with max_splits = 1; no partials.  For rows >= ~256, where one workgroup per
+ * row already fills the GPU.  Replaces the same reference functions as the pair. */
+int dsv2_mla_decode_rows(const void* q, const void* cache, const int64_t* base, const int32_t* pos,
+                         const int32_t* cap, int rows, float softmax_scale, void* olat, int64_t olat_stride,
+                         void* stream);
+
 /* Merge the splits of dsv2_mla_decode (same pos / cap).  With w_uv != NULL: out[r, h*128 + i] =
  * bf16(sum_j W_UV[h, i, j] o_lat[r, h, j]) (bf16 [rows, 2048], row stride out_stride);
  * with w_uv == NULL: out = bf16 o_lat [rows, 16, 512] for a grouped GEMM.

@@ -533,6 +533,49 @@ def test_mla_decode_combine_vs_fp32(B, lo, hi, seed, split):
     assert rel_err(out.float(), ref2) < 1e-2
 
 
+@pytest.mark.parametrize("B,lo,hi,seed", [(1, 1, 40, 70), (5, 1, 300, 71), (256, 2000, 2100, 72), (7, 900, 4200, 73)])
+def test_mla_decode_rows_equals_one_split_pair(B, lo, hi, seed):
+    """The one-launch decode (a workgroup per row, normalised bf16 o_lat) equals the split
+    decode + combine with one split covering every row, bit for bit, and fp32 attention
+    within 1e-2; a row of capacity 0 (nothing cached) gives zeros in both.  Lengths cover a
+    single partial tile, odd and even tile counts and the bsz=256 shape; o_lat rows are
+    written at a stride wider than 8192."""
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(lo, hi + 1, (B,), generator=g).tolist()
+    cap = [L + 5 for L in lens]
+    if B == 7:
+        cap[3] = 0
+    base = torch.tensor([0] + list(torch.cumsum(torch.tensor(cap), 0)[:-1].tolist()), dtype=torch.int64)
+    cache = torch.randn(max(sum(cap), 1), 576, generator=g).to(BF).to(DEV)
+    q = torch.randn(B, 16, 576, generator=g).to(BF).to(DEV)
+    pos = torch.tensor([L - 1 for L in lens], dtype=torch.int32, device=DEV)
+    scale = O.softmax_scale(O.Dims())
+    base_d = base.to(DEV)
+    cap_d = torch.tensor(cap, dtype=torch.int32, device=DEV)
+    split = math.ceil(max(max(cap), 1) / 32) * 32
+    po = torch.empty(B, 1, 16, 512, device=DEV)
+    pm = torch.empty(B, 1, 16, 2, device=DEV)
+    call("dsv2_mla_decode", q.data_ptr(), cache.data_ptr(), base_d.data_ptr(), pos.data_ptr(), cap_d.data_ptr(), B,
+         split, 1, scale, po.data_ptr(), pm.data_ptr(), st())
+    pair = torch.full((B, 16, 512), 7.0, dtype=BF, device=DEV)
+    call("dsv2_mla_combine", po.data_ptr(), pm.data_ptr(), pos.data_ptr(), cap_d.data_ptr(), B, split, 1, None,
+         pair.data_ptr(), 16 * 512, st())
+    wide = torch.full((B, 16 * 512 + 64), 7.0, dtype=BF, device=DEV)
+    call("dsv2_mla_decode_rows", q.data_ptr(), cache.data_ptr(), base_d.data_ptr(), pos.data_ptr(), cap_d.data_ptr(),
+         B, scale, wide.data_ptr(), 16 * 512 + 64, st())
+    torch.cuda.synchronize()
+    one = wide[:, :16 * 512].reshape(B, 16, 512)
+    assert torch.equal(one, pair)
+    assert torch.all(wide[:, 16 * 512:] == 7.0)  # nothing past the row's 8192 outputs
+    live = [b for b in range(B) if cap[b] > 0]
+    rows = [cache[int(base[b]):int(base[b]) + min(lens[b], cap[b])] for b in live]
+    ref = _mla_reference(q[live], rows, [min(lens[b], cap[b]) for b in live], scale)
+    assert rel_err(one[live].float(), ref) < 1e-2
+    for b in range(B):
+        if cap[b] == 0:
+            assert not one[b].float().any()
+
+
 def test_mla_constant_cache_returns_value():
     # every cached row identical -> o_lat equals the latent regardless of q
     B, L = 2, 777
