@@ -244,6 +244,33 @@ def test_router_topk6(rows, unit_norm):
     assert torch.allclose(w.cpu()[ok], ow[ok], rtol=1e-4, atol=1e-6)
 
 
+def test_router_topk6_exact_ties():
+    """W_r rows 9 and 40 identical and aligned with h (so they lead many rows' top-6) and rows
+    2 and 3 identical: equal logits, the lower index ranked first with an equal weight, in
+    every row that holds both."""
+    rows = 40
+    h, nw, wr = _router_case(rows, 440, False)
+    wr[40] = wr[9] = (h[:8].float().mean(0) * 0.05).to(BF)
+    wr[3] = wr[2]
+    ids = torch.empty(rows, 6, dtype=torch.int32, device=DEV)
+    w = torch.empty(rows, 6, dtype=torch.float32, device=DEV)
+    xn = torch.empty_like(h)
+    call("dsv2_router_topk6", h.data_ptr(), 2048, nw.data_ptr(), 1e-6, wr.data_ptr(), 1.0, rows, xn.data_ptr(),
+         ids.data_ptr(), None, w.data_ptr(), st())
+    idl, wl = ids.cpu().tolist(), w.cpu()
+    both = 0
+    for r in range(rows):
+        for a, b in ((9, 40), (2, 3)):
+            if a in idl[r] and b in idl[r]:
+                both += 1
+                ia, ib = idl[r].index(a), idl[r].index(b)
+                assert ia + 1 == ib and wl[r, ia] == wl[r, ib], (r, idl[r])
+    assert both >= 6
+    oid, ow, scores = O.router_topk(xn.float().cpu(), wr.float().cpu(), 6, 1.0)
+    for r in range(rows):  # the sets agree with the oracle on the kernel's own xn
+        assert sorted(idl[r]) == sorted(oid[r].tolist()) or O.topk_margin(scores[r:r + 1], 6)[0] <= 1e-3
+
+
 def test_router_from_logits_ties():
     lg = torch.zeros(2, 64, device=DEV)
     lg[0, [5, 9, 40]] = 3.0
