@@ -203,6 +203,24 @@ def time_other_kernels(eng, family: str, ctx_rows: list[int]) -> dict:
             entry("mla_attend_kernel (attention + W_UV over heads x W_UV quarters)", attend, moe,
                   2 * 16 * 128 * 512 + kv + B * 16 * 576 * 2 + B * 2048 * 2)
 
+        def qkva_absorb(li):
+            L = eng.w.layers[li]
+            call("dsv2_qkva_absorb_bf16", ptr(b.h), c.hidden, B, ptr(L.w_qkva), ptr(L.ln_in), c.eps, ptr(L.w_uk),
+                 ptr(b.qkva), c.qkva_dim, ptr(b.qlat_part), ptr(eng.cache.layer(li)), ptr(eng.cache.base),
+                 ptr(eng.cache.pos), ptr(eng.cache.cap), stream_ptr())
+
+        def attend_parts(li):
+            L = eng.w.layers[li]
+            call("dsv2_mla_attend_parts", ptr(b.qkva), c.qkva_dim, B, ptr(eng.cache.pos), ptr(eng.cache.base),
+                 ptr(eng.cache.cap), ptr(L.kv_norm), c.eps, ptr(eng.cos), ptr(eng.sin), eng.max_pos,
+                 ptr(b.qlat_part), ptr(L.w_uv), ptr(eng.cache.layer(li)), eng.scale, ptr(b.attn), c.hidden, None,
+                 stream_ptr())
+        if eng.absorb_mla:
+            entry("qkva_absorb_kernel (q|kv_a projection + W_UK absorption in 8 partial sums per head)",
+                  qkva_absorb, moe, B * 3648 * 2048 * 2 + 2 * 16 * 128 * 512 + B * 16 * 8 * 512 * 4)
+            entry("mla_quad_kernel<true> (new row + attention + W_UV from the partial absorbed queries)",
+                  attend_parts, moe, 2 * 16 * 128 * 512 + kv + B * 16 * 8 * 512 * 4 + B * 2048 * 2)
+
         def down(li):
             L = eng.w.layers[li]
             call("dsv2_moe_route_down", ptr(b.hbuf), B, ptr(b.ids32), ptr(b.wts), ptr(L.w_down), ptr(L.sh_down),
@@ -696,8 +714,9 @@ def main() -> None:
     ap.add_argument("--family", choices=("small", "batch"), default=None)
     ap.add_argument("--expert-dtype", choices=("bf16", "fp8"), default="bf16",
                     help="one config: MoE expert weights in bf16 or e4m3 (small family); 'all' runs C1 both ways")
-    ap.add_argument("--mla-path", choices=("fused", "spread", "split"), default="spread",
-                    help="small family: prepare + spread attention (two launches), one fused MLA kernel per "
+    ap.add_argument("--mla-path", choices=("fused", "spread", "split", "absorb"), default="absorb",
+                    help="small family: the absorption in the q|kv_a projection + one attention launch "
+                         "(absorb), prepare + spread attention (two launches), one fused MLA kernel per "
                          "layer, or prepare + split-KV decode + combine")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",

@@ -3,6 +3,7 @@
 
 namespace {
 constexpr int kRow = 576, kLat = 512;
+constexpr int kAbsBlocks = 8;  // q_nope rows of a head in blocks of 16: partial absorbed queries per head
 }
 
 // ---------------------------------------------------------------------------------------
@@ -235,6 +236,9 @@ __global__ __launch_bounds__(512) void mla_attend_kernel(const bf16_t* __restric
   att_finish(ta, tb, crow0, n, n, qc, qr, nullptr, wuv, scale_log2, sh, out + (int64_t)b * os + h * 128 + qq * 32);
 }
 
+// PARTS: q_lat is the sum of qkva_absorb_kernel's 8 fp32 partial products per head
+// (qlat_part[row][h][i][512]) instead of each workgroup absorbing q_h itself.
+template <bool PARTS>
 __global__ __launch_bounds__(512) void mla_quad_kernel(const bf16_t* __restrict__ qkva, int64_t qs,
                                                        const int32_t* __restrict__ pos,
                                                        const int64_t* __restrict__ base,
@@ -243,6 +247,7 @@ __global__ __launch_bounds__(512) void mla_quad_kernel(const bf16_t* __restrict_
                                                        const bf16_t* __restrict__ cosT,
                                                        const bf16_t* __restrict__ sinT, int max_pos,
                                                        const bf16_t* __restrict__ w_ukt,
+                                                       const float* __restrict__ qlat_part,
                                                        const bf16_t* __restrict__ w_uv, bf16_t* __restrict__ cache,
                                                        float scale_log2, bf16_t* __restrict__ out, int64_t os,
                                                        int32_t* __restrict__ status) {
@@ -268,9 +273,16 @@ __global__ __launch_bounds__(512) void mla_quad_kernel(const bf16_t* __restrict_
   // ---- entry loads: W_UK^T_h, q_nope_h, the W_UV rows, the new row's inputs, two batches --
   // absorption: thread (gi = tid / 16, k = tid % 16) owns latent rows gi + 32u, K slice k
   const int gi = tid >> 4, k = tid & 15;
-  const uint4 qn4 = ldg16(q + h * 192 + k * 8);
+  uint4 qn4 = {0u, 0u, 0u, 0u};
   uint4 wk[16];
-  {
+  float qp[kAbsBlocks];
+  if (PARTS) {
+    // thread tid sums latent element tid of the head's partial products
+    const float* pp = qlat_part + ((int64_t)b * 16 + h) * kAbsBlocks * kLat + tid;
+#pragma unroll
+    for (int i = 0; i < kAbsBlocks; ++i) qp[i] = pp[i * kLat];
+  } else {
+    qn4 = ldg16(q + h * 192 + k * 8);
     const bf16_t* wp = w_ukt + ((int64_t)h * kLat + gi) * 128 + k * 8;
 #pragma unroll
     for (int u = 0; u < 16; ++u) wk[u] = ldg16(wp + (int64_t)u * 32 * 128);
@@ -300,7 +312,9 @@ __global__ __launch_bounds__(512) void mla_quad_kernel(const bf16_t* __restrict_
   att_load(tb, crow0, kAttStep, n_ld, wv, li, rg);
 
   // ---- absorption: q_lat[c] = bf16(W_UK^T_h[c, :] . q_nope_h) ------------------------------
-  {
+  if (PARTS) {
+    qv[tid] = f2bf(((qp[0] + qp[1]) + (qp[2] + qp[3])) + ((qp[4] + qp[5]) + (qp[6] + qp[7])));
+  } else {
     float qn[8];
     unpack8(qn4, qn);
 #pragma unroll
@@ -346,6 +360,179 @@ __global__ __launch_bounds__(512) void mla_quad_kernel(const bf16_t* __restrict_
   for (int j = 0; j < 4; ++j) qc[j] = *reinterpret_cast<const uint4*>(qv + (li + 16 * j) * 8);
   const uint2 qr = *reinterpret_cast<const uint2*>(qv + kLat + 4 * li);
   att_finish(ta, tb, crow0, p, n_ld, qc, qr, nrow, wuv, scale_log2, sh, out + (int64_t)b * os + h * 128 + qq * 32);
+}
+
+// ---------------------------------------------------------------------------------------
+// The q | kv_a projection of one row (RMSNorm prologue) with the W_UK absorption of q_nope
+// spread over the projection's own workgroups, so the small-batch MLA needs no prepare
+// launch.  Workgroup w (512 threads, row blockIdx.y) owns projection rows 16w .. 16w+15,
+// wave v rows 16w + 2v, +1; each lane streams 4 chunks of 8 elements of each of its rows
+// (non-temporal) against x' in LDS, as gemv_k2048_kernel does (8 waves of 2 rows: 6.2 us per
+// launch on MI355X against 7.0 us for 4 waves of 4).  The 12 workgroups of head h
+// (w = 12h + i) hold its 192 q rows: i < 8 are the q_nope rows 16i .. 16i+15, whose bf16
+// outputs q_d each workgroup multiplies into its 16 rows of W_UK_h (each lane 8 latent
+// elements of the wave's 2 rows, requested at entry) -- partial[c] = sum_d W_UK_h[d, c] q_d
+// over the 16 rows (fp32, fixed order), written to qlat_part[row][h][i][512].  The last 36
+// workgroups hold the latent and k_pe rows.  Every workgroup also pulls an even share of the
+// row's first 256 cached tokens into its XCD's L2 for the attention launch that follows
+// (without it the C1 step is 1% slower).
+namespace {
+constexpr int kQkvRows = 3648, kQWgs = 16 * 12, kQkvWgs = kQkvRows / 16;
+}
+
+__global__ __launch_bounds__(512) void qkva_absorb_kernel(const bf16_t* __restrict__ x, int64_t xs,
+                                                          const bf16_t* __restrict__ nw, float eps,
+                                                          const bf16_t* __restrict__ W,
+                                                          const bf16_t* __restrict__ w_uk, bf16_t* __restrict__ qkva,
+                                                          int64_t qs, float* __restrict__ qlat_part,
+                                                          const bf16_t* __restrict__ cache,
+                                                          const int64_t* __restrict__ base,
+                                                          const int32_t* __restrict__ pos,
+                                                          const int32_t* __restrict__ cap) {
+  __shared__ float xl[2048];
+  __shared__ float red[8];
+  __shared__ float pw[8][kLat];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int b = blockIdx.y, w = blockIdx.x;
+  const int n0 = 16 * w + 2 * wv;
+  const int h = w / 12, blk = w % 12;
+  const bool absorb = w < kQWgs && blk < kAbsBlocks;  // uniform over the workgroup
+  const bf16_t* xr = x + b * xs;
+  // entry loads, in the order they are consumed: x and the norm weights (waves 4..7 repeat
+  // waves 0..3's chunks), W_UK (absorbing workgroups; the others re-read head 0's first rows,
+  // an L2 hit), then the weight rows
+  const int tc = tid & 255;
+  const uint4 xv4 = ldg16(xr + tc * 8);
+  const uint4 g4 = ldg16(nw + tc * 8);
+  uint4 wk[2];
+  {
+    const bf16_t* wp = w_uk + ((int64_t)(absorb ? h : 0) * 128 + (absorb ? 16 * blk + 2 * wv : 0)) * kLat + lane * 8;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) wk[j] = ldg16(wp + (int64_t)j * kLat);
+  }
+  uint4 wr[2][4];
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) wr[r][u] = ldg16_nt(W + (int64_t)(n0 + r) * 2048 + (lane + 64 * u) * 8);
+  // the prefetch share: tokens slot, slot + S, ... of the first min(n, 256) (workgroups w
+  // with equal w % 8 share an XCD; S of them per XCD)
+  constexpr int kSlots = (kQkvWgs + 7) / 8;
+  constexpr int kPfRows = (256 + kSlots - 1) / kSlots;
+  constexpr int kPf = (kPfRows * (kRow / 8) + 511) / 512;
+  uint4 pf[kPf];
+  {
+    const int slot = w >> 3;
+    const int n = min(min(max(pos[b], 0), cap[b]), 256);
+    const int nt = n > slot ? (n - 1 - slot) / kSlots + 1 : 0;
+    const bf16_t* crow0 = cache + base[b] * kRow;
+#pragma unroll
+    for (int i = 0; i < kPf; ++i) {
+      const int c = tid + 512 * i;
+      const bool live = c < nt * (kRow / 8);
+      const int t = live ? slot + kSlots * (c / (kRow / 8)) : 0;
+      pf[i] = ldg16(crow0 + (int64_t)t * kRow + (live ? c % (kRow / 8) : 0) * 8);
+    }
+  }
+  pin(xv4.x);
+  pin(g4.x);
+  // x' = w * bf16(x * rsqrt(mean x^2 + eps)) -> LDS (fp32)
+  {
+    float f[8], g8[8];
+    unpack8(xv4, f);
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(f[i], f[i], ss);
+    ss = wave_sum(ss);
+    if (lane == 0) red[wv] = ss;
+    __syncthreads();
+    const float rn = rsqrtf((red[0] + red[1] + red[2] + red[3]) / 2048.f + eps);  // waves 0..3: all of x
+    unpack8(g4, g8);
+    if (tid < 256) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xl[tid * 8 + i] = rbf(g8[i] * rbf(f[i] * rn));
+    }
+    __syncthreads();
+  }
+  float acc[2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    acc[r] = 0.f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc[r] += dot8(wr[r][u], &xl[(lane + 64 * u) * 8]);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1)
+#pragma unroll
+    for (int r = 0; r < 2; ++r) acc[r] += __shfl_xor(acc[r], off, 64);
+  float qd[2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) qd[r] = rbf(acc[r]);
+  if (lane == 0) {
+    *reinterpret_cast<uint32_t*>(qkva + b * qs + n0) = pack2(qd[0], qd[1]);
+  }
+  if (absorb) {
+    float f[8], p[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) p[e] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      unpack8(wk[j], f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) p[e] = __builtin_fmaf(f[e], qd[j], p[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) pw[wv][lane * 8 + e] = p[e];
+    __syncthreads();
+    const int c = tid;
+    float s0 = pw[0][c];
+#pragma unroll
+    for (int v = 1; v < 8; ++v) s0 += pw[v][c];
+    qlat_part[(((int64_t)b * 16 + h) * kAbsBlocks + blk) * kLat + c] = s0;
+  }
+  uint32_t sink = 0;
+#pragma unroll
+  for (int i = 0; i < kPf; ++i) sink ^= pf[i].x;
+  asm volatile("" ::"v"(sink));
+}
+
+extern "C" int dsv2_qkva_absorb_bf16(const void* x, int64_t x_stride, int rows, const void* w_qkva, const void* norm_w,
+                                     float eps, const void* w_uk, void* qkva, int64_t qkva_stride, float* qlat_part,
+                                     const void* cache, const int64_t* base, const int32_t* pos, const int32_t* cap,
+                                     void* stream) {
+  DSV2_REQUIRE(x && w_qkva && norm_w && w_uk && qkva && qlat_part && cache && base && pos && cap, DSV2_E_NULL,
+               "qkva_absorb: null pointer");
+  DSV2_REQUIRE(rows >= 0 && rows <= 65535 && x_stride >= 2048 && qkva_stride >= kQkvRows, DSV2_E_SHAPE,
+               "qkva_absorb: bad shape");
+  DSV2_REQUIRE(dsv2_aligned16(x) && x_stride % 8 == 0 && dsv2_aligned16(w_qkva) && dsv2_aligned16(norm_w) &&
+                   dsv2_aligned16(w_uk) && dsv2_aligned16(cache) && dsv2_aligned16(qkva) && qkva_stride % 8 == 0 &&
+                   dsv2_aligned16(qlat_part),
+               DSV2_E_ALIGN, "qkva_absorb: alignment");
+  if (rows == 0) return DSV2_OK;
+  hipLaunchKernelGGL(qkva_absorb_kernel, dim3(kQkvWgs, rows), dim3(512), 0, (hipStream_t)stream, (const bf16_t*)x,
+                     x_stride, (const bf16_t*)norm_w, eps, (const bf16_t*)w_qkva, (const bf16_t*)w_uk, (bf16_t*)qkva,
+                     qkva_stride, qlat_part, (const bf16_t*)cache, base, pos, cap);
+  return dsv2_launch_status("qkva_absorb");
+}
+
+extern "C" int dsv2_mla_attend_parts(const void* qkva, int64_t qkva_stride, int rows, const int32_t* pos,
+                                     const int64_t* base, const int32_t* cap, const void* kv_norm_w, float eps,
+                                     const void* rope_cos, const void* rope_sin, int max_pos, const float* qlat_part,
+                                     const void* w_uv, void* cache, float softmax_scale, void* out,
+                                     int64_t out_stride, int32_t* status, void* stream) {
+  DSV2_REQUIRE(qkva && pos && base && cap && kv_norm_w && rope_cos && rope_sin && qlat_part && w_uv && cache && out,
+               DSV2_E_NULL, "mla_attend_parts: null pointer");
+  DSV2_REQUIRE(rows >= 0 && rows <= 65535 && max_pos > 0 && qkva_stride >= kQkvRows && out_stride >= 2048,
+               DSV2_E_SHAPE, "mla_attend_parts: bad shape");
+  DSV2_REQUIRE(dsv2_aligned16(qkva) && qkva_stride % 8 == 0 && dsv2_aligned16(kv_norm_w) && dsv2_aligned16(cache) &&
+                   dsv2_aligned16(qlat_part) && dsv2_aligned16(w_uv) && dsv2_aligned16(out) && out_stride % 8 == 0,
+               DSV2_E_ALIGN, "mla_attend_parts: alignment");
+  if (rows == 0) return DSV2_OK;
+  hipLaunchKernelGGL(mla_quad_kernel<true>, dim3(64, rows), dim3(512), 0, (hipStream_t)stream, (const bf16_t*)qkva,
+                     qkva_stride, pos, base, cap, (const bf16_t*)kv_norm_w, eps, (const bf16_t*)rope_cos,
+                     (const bf16_t*)rope_sin, max_pos, nullptr, qlat_part, (const bf16_t*)w_uv, (bf16_t*)cache,
+                     softmax_scale * 1.4426950408889634f, (bf16_t*)out, out_stride, status);
+  return dsv2_launch_status("mla_attend_parts");
 }
 
 void mla_prepare_absorb_launch(const void* qkva, int64_t qkva_stride, int rows, const int32_t* pos,
@@ -407,9 +594,10 @@ extern "C" int dsv2_mla_fused(const void* qkva, int64_t qkva_stride, int rows, c
                    dsv2_aligned16(w_ukt) && dsv2_aligned16(w_uv) && dsv2_aligned16(out) && out_stride % 8 == 0,
                DSV2_E_ALIGN, "mla_fused: alignment");
   if (rows == 0) return DSV2_OK;
-  hipLaunchKernelGGL(mla_quad_kernel, dim3(64, rows), dim3(512), 0, (hipStream_t)stream, (const bf16_t*)qkva,
+  hipLaunchKernelGGL(mla_quad_kernel<false>, dim3(64, rows), dim3(512), 0, (hipStream_t)stream, (const bf16_t*)qkva,
                      qkva_stride, pos, base, cap, (const bf16_t*)kv_norm_w, eps, (const bf16_t*)rope_cos,
-                     (const bf16_t*)rope_sin, max_pos, (const bf16_t*)w_ukt, (const bf16_t*)w_uv, (bf16_t*)cache,
-                     softmax_scale * 1.4426950408889634f, (bf16_t*)out, out_stride, status);
+                     (const bf16_t*)rope_sin, max_pos, (const bf16_t*)w_ukt, nullptr, (const bf16_t*)w_uv,
+                     (bf16_t*)cache, softmax_scale * 1.4426950408889634f, (bf16_t*)out, out_stride, status);
   return dsv2_launch_status("mla_fused");
 }
+

@@ -129,6 +129,8 @@ class RowBuffers:
         self.router_logits = e(rows, cfg.n_experts, dt=torch.float32)
         if family == "small":
             self.hbuf = e(rows, cfg.top_k + 2, cfg.moe_inter)
+            if not prefill:  # partial absorbed queries of dsv2_qkva_absorb_bf16 (8 blocks per head)
+                self.qlat_part = e(rows, cfg.n_heads, cfg.qk_nope // 16, cfg.kv_rank, dt=torch.float32)
         else:
             R = rows * cfg.top_k
             if not prefill:
@@ -170,7 +172,7 @@ def _graph_node_count(g: torch.cuda.CUDAGraph) -> int:
 
 class DecodeEngine:
     def __init__(self, weights: ModelWeights, capacities: list[int], family: str = "small",
-                 max_prefill_rows: int = 8192, device="cuda", mla_path: str = "spread", moe_tile: int | None = None,
+                 max_prefill_rows: int = 8192, device="cuda", mla_path: str = "absorb", moe_tile: int | None = None,
                  expert_dtype: str = "bf16"):
         """capacities: cache tokens of each row (slot).  moe_tile (batch family): fix the
         grouped MoE token tile (16, 32 or 64) instead of choosing it from the routing of one
@@ -179,7 +181,7 @@ class DecodeEngine:
         quantize_experts_fp8 (prefill keeps the bf16 kernels on the dequantized weights)."""
         if family not in FAMILIES:
             raise ValueError(f"Unknown kernel family: {family}")
-        if mla_path not in ("split", "fused", "spread"):
+        if mla_path not in ("split", "fused", "spread", "absorb"):
             raise ValueError(f"Unknown MLA path: {mla_path}")
         if expert_dtype not in ("bf16", "fp8"):
             raise ValueError(f"Unknown expert dtype: {expert_dtype}")
@@ -213,7 +215,11 @@ class DecodeEngine:
         # small family, "spread": mla_prepare (absorption over 128 workgroups) then mla_attend
         # (64 workgroups per row over heads x W_UV quarters)
         self.spread_mla = family == "small" and self.max_pos <= FUSED_MLA_MAX_CTX and mla_path == "spread"
-        self.mla_path = "fused" if self.fused_mla else "spread" if self.spread_mla else "split"
+        # small family, "absorb": the q|kv_a projection also forms the absorbed query in partial
+        # sums (dsv2_qkva_absorb_bf16), then one attention launch (dsv2_mla_attend_parts)
+        self.absorb_mla = family == "small" and self.max_pos <= FUSED_MLA_MAX_CTX and mla_path == "absorb"
+        self.mla_path = ("fused" if self.fused_mla else "spread" if self.spread_mla else
+                         "absorb" if self.absorb_mla else "split")
         self.max_prefill_rows = max_prefill_rows
         self.graph = None
         self.kernels_per_step = 0  # set by capture()
@@ -233,6 +239,15 @@ class DecodeEngine:
                  None, 0, ptr(b.qkva), c.qkva_dim, 0, st)
             call("dsv2_mla_spread", ptr(b.qkva), c.qkva_dim, R, ptr(pos), ptr(base), ptr(cap), ptr(L.kv_norm),
                  c.eps, ptr(self.cos), ptr(self.sin), self.max_pos, ptr(L.w_ukt), ptr(L.w_uv), ptr(cache), ptr(b.q),
+                 self.scale, ptr(b.attn), c.hidden, ptr(self.cache.status), st)
+            call("dsv2_gemv_bf16", ptr(b.attn), c.hidden, R, c.hidden, ptr(L.w_o), c.hidden, None, 0.0, ptr(b.h),
+                 c.hidden, ptr(b.h), c.hidden, 0, st)
+            return
+        if family == "small" and self.absorb_mla and b is self.buf:
+            call("dsv2_qkva_absorb_bf16", ptr(b.h), c.hidden, R, ptr(L.w_qkva), ptr(L.ln_in), c.eps, ptr(L.w_uk),
+                 ptr(b.qkva), c.qkva_dim, ptr(b.qlat_part), ptr(cache), ptr(base), ptr(pos), ptr(cap), st)
+            call("dsv2_mla_attend_parts", ptr(b.qkva), c.qkva_dim, R, ptr(pos), ptr(base), ptr(cap), ptr(L.kv_norm),
+                 c.eps, ptr(self.cos), ptr(self.sin), self.max_pos, ptr(b.qlat_part), ptr(L.w_uv), ptr(cache),
                  self.scale, ptr(b.attn), c.hidden, ptr(self.cache.status), st)
             call("dsv2_gemv_bf16", ptr(b.attn), c.hidden, R, c.hidden, ptr(L.w_o), c.hidden, None, 0.0, ptr(b.h),
                  c.hidden, ptr(b.h), c.hidden, 0, st)

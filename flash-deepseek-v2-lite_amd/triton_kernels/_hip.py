@@ -57,6 +57,9 @@ _SIGS = {
     "dsv2_mla_attend": ([_p, _p, _p, _p, _p, _i32, _p, _f32, _p, _i64, _p], _i32),
     "dsv2_mla_spread": ([_p, _i64, _i32, _p, _p, _p, _p, _f32, _p, _p, _i32, _p, _p, _p, _p, _f32, _p, _i64, _p, _p],
                         _i32),
+    "dsv2_qkva_absorb_bf16": ([_p, _i64, _i32, _p, _p, _f32, _p, _p, _i64, _p, _p, _p, _p, _p, _p], _i32),
+    "dsv2_mla_attend_parts": ([_p, _i64, _i32, _p, _p, _p, _p, _f32, _p, _p, _i32, _p, _p, _p, _f32, _p, _i64, _p,
+                               _p], _i32),
     "dsv2_moe_route_gateup_logits_fp8": ([_p, _i32, _p, _f32, _p, _p, _p, _p, _p, _p, _i32, _p, _p], _i32),
     "dsv2_moe_route_down_fp8": ([_p, _i32, _p, _p, _p, _p, _p, _p, _i32, _i32, _p, _p, _p], _i32),
     "dsv2_router_topk6": ([_p, _i64, _p, _f32, _p, _f32, _i32, _p, _p, _p, _p, _p], _i32),

@@ -226,6 +226,31 @@ int dsv2_mla_spread(const void* qkva, int64_t qkva_stride, int rows, const int32
                     int max_pos, const void* w_ukt, const void* w_uv, void* cache, void* q_buf, float softmax_scale,
                     void* out, int64_t out_stride, int32_t* status, void* stream);
 
+/* The q | kv_a projection of rows x [rows, 2048] (row stride x_stride) with the RMSNorm
+ * prologue (norm_w, eps), as dsv2_gemv_bf16(x, ..., w_qkva [3648, 2048], 3648, norm_w, eps, ...)
+ * writes it into qkva [rows, 3648] (row stride qkva_stride), plus the W_UK absorption of its
+ * q_nope in partial sums: for head h and block i of its q_nope rows 16i .. 16i+15,
+ *   qlat_part[r, h, i, c] = sum_{d in block i} w_uk[h, d, c] * qkva[r, h*192 + d]   (fp32),
+ * with w_uk [16, 128, 512] (kv_b's k_nope rows).  The projection's workgroups also bring the
+ * first 256 cached rows of each row (cache / base / pos / cap as dsv2_mla_fused) into L2 for
+ * the attention that follows.  qlat_part holds rows * 16 * 8 * 512 floats.  Replaces the
+ * q+kv_a linear (attention_decode_small.py:55-96) and, with dsv2_mla_attend_parts, the small
+ * family's q/k build (attention_decode_small.py:141-264) and attention
+ * (attention_decode_small.py:553-674, :932-1070). */
+int dsv2_qkva_absorb_bf16(const void* x, int64_t x_stride, int rows, const void* w_qkva, const void* norm_w, float eps,
+                          const void* w_uk, void* qkva, int64_t qkva_stride, float* qlat_part, const void* cache,
+                          const int64_t* base, const int32_t* pos, const int32_t* cap, void* stream);
+
+/* dsv2_mla_fused with the absorbed query taken from dsv2_qkva_absorb_bf16's partial sums:
+ * q_lat[r, h, c] = bf16(sum over the 8 blocks of qlat_part[r, h, i, c]) instead of each head
+ * workgroup absorbing q_nope itself; otherwise the same inputs (qkva: q_pe, latent and k_pe
+ * are read from it), cache write, capacity rule and result.  Same reference functions as
+ * dsv2_qkva_absorb_bf16. */
+int dsv2_mla_attend_parts(const void* qkva, int64_t qkva_stride, int rows, const int32_t* pos, const int64_t* base,
+                          const int32_t* cap, const void* kv_norm_w, float eps, const void* rope_cos,
+                          const void* rope_sin, int max_pos, const float* qlat_part, const void* w_uv, void* cache,
+                          float softmax_scale, void* out, int64_t out_stride, int32_t* status, void* stream);
+
 /* q_len = 1 attention over an EXPANDED per-head cache (keys [B, H, L, q_dim], values
  * [B, H, L, v_dim], bf16, last dim contiguous, element strides as given):
  *   out[b, h, :] = bf16( softmax_n(scale * k[b,h,n,:] . q[b,h,:]) . v[b,h,n,:] ),  n = 0..pos

@@ -115,7 +115,8 @@ def test_run_cli_with_model_path_and_chat_prompt(ckpt):
                   "--prompt", "Write me a 500 word novel."])
     n = chat_prompt_ids(load_tokenizer(path), "Write me a 500 word novel.").numel()
     assert res["prompt_lens"] == n and res["batch_size"] == 1 and len(res["generated_token_ids"]) == 4
-    # embed; dense layer: qkv_a, MLA prepare + attend, o_proj, gate_up, down; MoE layer: qkv_a,
-    # MLA prepare + attend, o_proj, router logits, routed gate_up, routed down; lm_head + argmax
-    assert res["kernels_per_step"] == 1 + 6 + 7 + 2
+    # embed; dense layer: qkv_a with the W_UK absorption, MLA attention, o_proj, gate_up, down;
+    # MoE layer: qkv_a + absorption, MLA attention, o_proj, router logits, routed gate_up,
+    # routed down; lm_head + argmax
+    assert res["kernels_per_step"] == 1 + 5 + 6 + 2
     assert 0 < res["roofline_fraction"] < 1 and 7e8 < res["hbm_bytes_per_step"] < 8e8

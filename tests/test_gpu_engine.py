@@ -19,6 +19,7 @@ from engine_common import agree as _agree
 from engine_common import build_model
 from engine_common import check_trace as _check_trace
 from engine_common import close as _close
+from engine_common import mean_no_less_exact
 from engine_common import oracle_step as _oracle_step
 from engine_common import prompts as _prompts
 
@@ -32,6 +33,7 @@ def model():
 
 @pytest.mark.parametrize("family,lens,mla", [("small", [16], "split"), ("small", [16], "fused"), ("batch", [16], "split"),
                                              ("small", [16], "spread"), ("small", [5, 11], "spread"),
+                                             ("small", [16], "absorb"), ("small", [5, 11], "absorb"),
                                              ("small", [5, 11], "split"), ("small", [5, 11], "fused"),
                                              ("batch", [5, 16, 9, 1], "split")])
 def test_engine_decode_vs_oracle(model, family, lens, mla):
@@ -82,7 +84,8 @@ def test_engine_decode_vs_oracle(model, family, lens, mla):
     print(f"{family} {lens}: greedy agreement {agree}/{total}", flush=True)
 
 
-@pytest.mark.parametrize("family,mla", [("small", "fused"), ("small", "spread"), ("batch", "split")])
+@pytest.mark.parametrize("family,mla", [("small", "fused"), ("small", "spread"), ("small", "absorb"),
+                                        ("batch", "split")])
 def test_graph_replay_equals_eager_bitwise(model, family, mla):
     import dsv2lite
 
@@ -151,18 +154,20 @@ def test_greedy_agreement_teacher_forced_40_steps(model, family):
     tok = int(torch.argmax(res["logits"][-1]))
     agree = 0
     steps = 40
+    errs: list = []
     for s in range(steps):
         eng.ids.fill_(tok)
         rec = []
         eng.step(record=rec)
         res, tr = _oracle_step(om, cache, torch.tensor([tok]), 12 + s)
         ref = res["logits"][-1]
-        _, flipped = _check_trace(om, rec, tr, 0, (family, s), res)
-        _close(eng.logits[0].cpu(), ref, res["fp32"]["logits"][-1], flipped, (family, s))
+        _, flipped = _check_trace(om, rec, tr, 0, (family, s), res, errs)
+        _close(eng.logits[0].cpu(), ref, res["fp32"]["logits"][-1], flipped, (family, s), errs)
         agree += _agree(int(eng.ids[0].item()), ref, eng.logits[0].cpu(), (family, s))
         tok = int(torch.argmax(ref))
-    print(f"{family}: greedy agreement {agree}/{steps}", flush=True)
+    print(f"{family} ({eng.mla_path} MLA): greedy agreement {agree}/{steps}", flush=True)
     assert agree / steps >= 0.95, (agree, steps)
+    mean_no_less_exact(errs, (family, eng.mla_path))
 
 
 @pytest.mark.parametrize("family,bsz", [("small", 1), ("batch", 3)])

@@ -799,6 +799,76 @@ def test_mla_attend_matches_fused_and_fp32(lens):
         assert torch.equal(c_2, c_s) and torch.equal(q2, q) and torch.equal(out_2, out_s), step
 
 
+@pytest.mark.parametrize("lens", [[1], [2, 3], [231], [40, 7, 300], [700]])
+def test_qkva_absorb_and_attend_parts(lens):
+    """The q|kv_a projection with the absorption split over its workgroups: its projection is
+    the few-row GEMV's bit for bit, the partial absorbed queries sum to W_UK^T q_nope (fp32),
+    and the attention from them writes the fused kernel's cache rows and agrees with it and
+    with fp32 math, at two consecutive positions."""
+    from dsv2lite.config import DSV2Config
+    from dsv2lite.rope import cos_sin_tables
+
+    cfg = DSV2Config()
+    B = len(lens)
+    g = torch.Generator().manual_seed(11 * sum(lens))
+    cap = [L + 5 for L in lens]
+    base = torch.tensor([0] + list(torch.cumsum(torch.tensor(cap), 0)[:-1].tolist()), dtype=torch.int64)
+    cache0 = (torch.randn(sum(cap), 576, generator=g) * 0.5).to(BF).to(DEV)
+    h = rnd(B, 2048, seed=290)
+    ln = (rnd(2048, seed=291, std=0.1) + 1).to(BF)
+    w_qkva = rnd(3648, 2048, std=0.02, seed=292)
+    kvw = (rnd(512, seed=293, std=0.1) + 1).to(BF)
+    w_uk = rnd(16, 128, 512, std=0.05, seed=294)
+    w_uv = rnd(16, 128, 512, std=0.05, seed=295)
+    w_ukt = w_uk.transpose(1, 2).contiguous()
+    cos, sin = cos_sin_tables(cfg, 1024, device=DEV)
+    scale = cfg.softmax_scale
+    base_d = base.to(DEV)
+    cap_d = torch.tensor(cap, dtype=torch.int32, device=DEV)
+    status = torch.zeros(1, dtype=torch.int32, device=DEV)
+    ref_qkva = torch.empty(B, 3648, dtype=BF, device=DEV)
+    call("dsv2_gemv_bf16", h.data_ptr(), 2048, B, 2048, w_qkva.data_ptr(), 3648, ln.data_ptr(), 1e-6, None, 0,
+         ref_qkva.data_ptr(), 3648, 0, st())
+    for step in range(2):
+        pos_d = torch.tensor([L - 1 + step for L in lens], dtype=torch.int32, device=DEV)
+        qkva = torch.full((B, 3648), float("nan"), dtype=BF, device=DEV)
+        parts = torch.full((B, 16, 8, 512), float("nan"), dtype=torch.float32, device=DEV)
+        c_p, c_f = cache0.clone(), cache0.clone()
+        call("dsv2_qkva_absorb_bf16", h.data_ptr(), 2048, B, w_qkva.data_ptr(), ln.data_ptr(), 1e-6,
+             w_uk.data_ptr(), qkva.data_ptr(), 3648, parts.data_ptr(), c_p.data_ptr(), base_d.data_ptr(),
+             pos_d.data_ptr(), cap_d.data_ptr(), st())
+        torch.cuda.synchronize()
+        assert torch.equal(qkva, ref_qkva), step
+        q_nope = qkva.float().cpu()[:, :3072].view(B, 16, 192)[:, :, :128]
+        want = torch.einsum("bhd,hdc->bhc", q_nope.double(), w_uk.double().cpu())
+        got = parts.double().cpu().sum(2)
+        assert (got - want).abs().max() <= 1e-5 * want.abs().max(), step
+        out_p = torch.empty(B, 2048, dtype=BF, device=DEV)
+        out_f = torch.empty(B, 2048, dtype=BF, device=DEV)
+        call("dsv2_mla_attend_parts", qkva.data_ptr(), 3648, B, pos_d.data_ptr(), base_d.data_ptr(),
+             cap_d.data_ptr(), kvw.data_ptr(), 1e-6, cos.data_ptr(), sin.data_ptr(), 1024, parts.data_ptr(),
+             w_uv.data_ptr(), c_p.data_ptr(), scale, out_p.data_ptr(), 2048, status.data_ptr(), st())
+        call("dsv2_mla_fused", qkva.data_ptr(), 3648, B, pos_d.data_ptr(), base_d.data_ptr(), cap_d.data_ptr(),
+             kvw.data_ptr(), 1e-6, cos.data_ptr(), sin.data_ptr(), 1024, w_ukt.data_ptr(), w_uv.data_ptr(),
+             c_f.data_ptr(), scale, out_f.data_ptr(), 2048, status.data_ptr(), st())
+        torch.cuda.synchronize()
+        assert status.item() == 0
+        assert torch.equal(c_p, c_f), step  # the same new rows, nothing else written
+        assert rel_err(out_p.float().cpu(), out_f.float().cpu()) < 1e-2, step
+        # fp32 attention from the absorbed query the kernel forms (bf16 of the partial sum)
+        ocos, osin = O.yarn_cos_sin(O.Dims(), 1024, mode="bf16")
+        p = pos_d.cpu().long()
+        x = qkva.float().cpu()
+        q_pe = rb(O.rope_deinterleave(x[:, :3072].view(B, 16, 192)[:, :, 128:], ocos[p][:, None], osin[p][:, None],
+                                      lambda t: t))
+        q_full = torch.cat([rb(got.float()), q_pe], -1)
+        n = [L + step for L in lens]
+        rows = [c_p.float().cpu()[int(base[b]):int(base[b]) + n[b]] for b in range(B)]
+        olat = _mla_reference(q_full, rows, n, scale)
+        ref = torch.einsum("hij,bhj->bhi", w_uv.float().cpu(), olat).reshape(B, 2048)
+        assert rel_err(out_p.float().cpu(), ref) < 1e-2, step
+
+
 @pytest.mark.parametrize("rows", [1, 3])
 def test_router_logits_split_and_gateup_topk(rows):
     h, nw, wr = _router_case(rows, 95)
