@@ -500,12 +500,14 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const GemmArgs a, const D
       }
       dst[j] = (j >= 2 ? 8192 : 0) + (16 * wv + 8 * (j & 1)) * 128;
     }
-    // the item's K chunks start at a rotation of its own, a function of (expert or shared half,
-    // token tile, feature block) only -- so an expert's results do not depend on which other
-    // tiles share the launch -- that spreads the workgroups' concurrent requests over the
-    // weight rows' address range instead of one column of 128 B lines (C3 grouped gate_up
-    // 158.4 -> 153.6 us)
-    const int rot = (int)((unsigned)(fb * 7 + g * 13 + (t0 >> 6) * 5 + (shared ? 3 : 0)) % (unsigned)nch);
+    // the item's K chunks start at a rotation that spreads the workgroups' concurrent requests
+    // over the weight rows' address range instead of one column of 128 B lines (C3 grouped
+    // gate_up 158.4 -> 153.6 us).  It depends on (expert or shared half, feature block) only:
+    // an expert's results do not depend on which other tiles share the launch, and the token
+    // tiles of one weight block read its chunks in the same order, so the ones that run
+    // together share each chunk's fetch in L2 (a rotation per token tile as well made the
+    // reference workload at bsz=256 -- 4 tiles per expert -- 1.5x slower)
+    const int rot = (int)((unsigned)(fb * 7 + g * 13 + (shared ? 3 : 0)) % (unsigned)nch);
     auto issue = [&](int chunk, int buf) {
       int cc = min(chunk, nch - 1) + rot;  // past the last chunk: repeat it (never multiplied)
       if (cc >= nch) cc -= nch;
