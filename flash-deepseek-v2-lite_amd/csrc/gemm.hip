@@ -425,6 +425,7 @@ struct DmaShape {
   int tiles, nwg, nfb;
 };
 
+
 // SWIGLU: the 64 weight rows of a workgroup are, per 16 features, 16 gate rows then the 16
 // matching up rows (32 features per workgroup); a wave's two row blocks are then one
 // feature block's gate and up tiles, combined in its epilogue.
@@ -432,11 +433,16 @@ struct DmaShape {
 // the live (tile, feature block) items only, so the table's dead tiles cost no workgroup
 // launches; token rows are gathered through slot_row and the tile's expert selects the
 // weights.
-template <bool SWIGLU>
+template <bool SWIGLU, int WM = 32, int WN = 32, int ST = kDmaStages>
 __global__ __launch_bounds__(256) void gemm_dma_kernel(const GemmArgs a, const DmaShape sh) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // kDmaStages * 16 KB
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // ST stages of SB bytes
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, li = lane & 15, kg = lane >> 4;
-  constexpr int FPW = SWIGLU ? 32 : 64;  // output features per workgroup
+  constexpr int TM = 2 * WM, TN = 2 * WN;  // weight rows, tokens per workgroup (2 x 2 waves)
+  constexpr int SB = (TM + TN) * 128;      // stage: TM weight rows, then TN token rows, 128 B each
+  constexpr int LW = TM / 32, LL = (TM + TN) / 32;  // ring loads per wave per chunk: weights, all
+  constexpr int XM = WM / 16, XN = WN / 16;         // MFMA blocks per wave
+  constexpr int FPW = SWIGLU ? TM / 2 : TM;  // output features per workgroup
+  static_assert(LL <= 8 && XM <= 4 && XN <= 4, "local arrays have literal sizes");
   // grouped: items j = tile * nfb + fb over the live tiles (the shared halves' tiles, then the
   // table's), consecutive items round-robin over the XCDs (keeping all token tiles of a
   // feature block on one XCD measured slower: fewer feature blocks than XCD slots balance)
@@ -453,8 +459,8 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const GemmArgs a, const D
       if (tile < ns) {  // a shared-expert half's tile of tokens
         shared = true;
         g = tile / a.s_tiles;
-        t0 = (tile % a.s_tiles) * 64;
-        count = min(64, a.rows - t0);
+        t0 = (tile % a.s_tiles) * TN;
+        count = min(TN, a.rows - t0);
       } else {
         const int4 tt = reinterpret_cast<const int4*>(a.tiles)[tile - ns];
         g = tt.x;
@@ -468,24 +474,25 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const GemmArgs a, const D
       if (w >= sh.nfb * sh.tiles) break;
       const int tile = w % sh.tiles;
       fb = w / sh.tiles;
-      t0 = tile * 64;
-      count = min(64, a.rows - t0);
+      t0 = tile * TN;
+      count = min(TN, a.rows - t0);
     }
     const int f0 = fb * FPW;
     const int K = a.K, nch = K / 64;
-    // this wave's 4 ring loads per chunk: weight rows 16wv .. 16wv+15 (j = 0, 1) and token rows
-    // 16wv .. 16wv+15 (j = 2, 3), 8 rows per load; lane -> (row r, slot lane & 7), which holds
+    // this wave's LL ring loads per chunk, 8 rows x 128 B each: weight rows (TM / 4 per wave,
+    // j < LW) then token rows (TN / 4 per wave); lane -> (row r, slot lane & 7), which holds
     // piece (lane & 7) ^ (r & 7)
     const bf16_t* const wbase = shared ? a.W2 + g * a.w2g : a.W + g * a.wg;
     const int64_t wld = shared ? a.w2ld : K;
     const int upoff = shared ? a.w2up : a.N;
-    const bf16_t* src[4];
-    int dst[4];
+    const bf16_t* src[8];
+    int dst[8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int r = 16 * wv + 8 * (j & 1) + (lane >> 3);
+    for (int j = 0; j < LL; ++j) {
+      const bool tok = j >= LW;
+      const int r = (tok ? (TN / 4) * wv + 8 * (j - LW) : (TM / 4) * wv + 8 * j) + (lane >> 3);
       const int pc = (lane & 7) ^ (r & 7);
-      if (j >= 2) {
+      if (tok) {
         const int slot = t0 + (r < count ? r : 0);  // rows past the tile: the tile's first row
         if (shared) {
           src[j] = a.X2 + g * a.x2g + (int64_t)slot * a.x2s + pc * 8;
@@ -498,7 +505,7 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const GemmArgs a, const D
       } else {
         src[j] = wbase + (f0 + r) * wld + pc * 8;
       }
-      dst[j] = (j >= 2 ? 8192 : 0) + (16 * wv + 8 * (j & 1)) * 128;
+      dst[j] = (tok ? TM * 128 + ((TN / 4) * wv + 8 * (j - LW)) * 128 : ((TM / 4) * wv + 8 * j) * 128);
     }
     // the item's K chunks start at a rotation that spreads the workgroups' concurrent requests
     // over the weight rows' address range instead of one column of 128 B lines (C3 grouped
@@ -512,71 +519,80 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const GemmArgs a, const D
       int cc = min(chunk, nch - 1) + rot;  // past the last chunk: repeat it (never multiplied)
       if (cc >= nch) cc -= nch;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < LL; ++j)
         __builtin_amdgcn_global_load_lds(src[j] + cc * 64,
-                                         (__attribute__((address_space(3))) void*)(lds + buf * 16384 + dst[j]), 16, 0, 0);
+                                         (__attribute__((address_space(3))) void*)(lds + buf * SB + dst[j]), 16, 0, 0);
     };
-    floatx4_t acc[2][2];
+    floatx4_t acc[4][4];
 #pragma unroll
-    for (int x = 0; x < 2; ++x)
+    for (int x = 0; x < XM; ++x)
 #pragma unroll
-      for (int y = 0; y < 2; ++y) acc[x][y] = floatx4_t{0.f, 0.f, 0.f, 0.f};
-    const int wa = (wv & 1) * 32, wt = (wv >> 1) * 32;  // this wave's 32 features x 32 tokens
+      for (int y = 0; y < XN; ++y) acc[x][y] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+    const int wa = (wv & 1) * WM, wt = (wv >> 1) * WN;  // this wave's WM weight rows x WN tokens
 #pragma unroll
-    for (int s = 0; s + 1 < kDmaStages; ++s) issue(s, s);
-    for (int c0 = 0; c0 < nch; c0 += kDmaStages) {
+    for (int s = 0; s + 1 < ST; ++s) issue(s, s);
+    for (int c0 = 0; c0 < nch; c0 += ST) {
 #pragma unroll
-      for (int i = 0; i < kDmaStages; ++i) {
+      for (int i = 0; i < ST; ++i) {
         const int c = c0 + i;
         if (c >= nch) break;
-        // this wave's loads of chunk c have landed (the 4 of each newer chunk may not), then
+        // this wave's loads of chunk c have landed (the LL of each newer chunk may not), then
         // every wave's: chunk c is complete in LDS and chunk c - 1's stage is free
-        __builtin_amdgcn_s_waitcnt(vmcnt_only((kDmaStages - 2) * 4));
+        __builtin_amdgcn_s_waitcnt(vmcnt_only((ST - 2) * LL));
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        issue(c + kDmaStages - 1, (i + kDmaStages - 1) % kDmaStages);
-        const uint8_t* st = lds + i * 16384;
+        issue(c + ST - 1, (i + ST - 1) % ST);
+        const uint8_t* st = lds + i * SB;
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-          bf16x8_t af[2], bfr[2];
+          bf16x8_t af[4], bfr[4];
+          const int pc = 4 * s + kg;
 #pragma unroll
-          for (int x = 0; x < 2; ++x) {
-            const int r = wa + 16 * x + li, t = wt + 16 * x + li, pc = 4 * s + kg;
+          for (int x = 0; x < XM; ++x) {
+            const int r = wa + 16 * x + li;
             af[x] = *reinterpret_cast<const bf16x8_t*>(st + r * 128 + ((pc ^ (r & 7)) * 16));
-            bfr[x] = *reinterpret_cast<const bf16x8_t*>(st + 8192 + t * 128 + ((pc ^ (t & 7)) * 16));
           }
 #pragma unroll
-          for (int x = 0; x < 2; ++x)
+          for (int y = 0; y < XN; ++y) {
+            const int t = wt + 16 * y + li;
+            bfr[y] = *reinterpret_cast<const bf16x8_t*>(st + TM * 128 + t * 128 + ((pc ^ (t & 7)) * 16));
+          }
 #pragma unroll
-            for (int y = 0; y < 2; ++y) acc[x][y] = mfma16x16x32(af[x], bfr[y], acc[x][y]);
+          for (int x = 0; x < XM; ++x)
+#pragma unroll
+            for (int y = 0; y < XN; ++y) acc[x][y] = mfma16x16x32(af[x], bfr[y], acc[x][y]);
         }
       }
     }
     // the repeats past the last chunk must land before the workgroup's LDS is released
     __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
     if (SWIGLU) {
+      // the wave's row blocks alternate gate (x even) and up (x odd) of feature groups of 16
 #pragma unroll
-      for (int y = 0; y < 2; ++y) {
-        if (wt + 16 * y + li >= count) continue;
-        float v[4];
+      for (int q = 0; q < XM / 2; ++q)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = swiglu_bf(acc[0][y][e], acc[1][y][e]);
-        if (shared) {
-          uint2 o;
-          o.x = pack2(v[0], v[1]);
-          o.y = pack2(v[2], v[3]);
-          *reinterpret_cast<uint2*>(reinterpret_cast<bf16_t*>(a.Y2) + g * a.y2g +
-                                    (int64_t)(t0 + wt + 16 * y + li) * a.y2s + f0 + (wa >> 1) + 4 * kg) = o;
-        } else {
-          gemm_store4(a, g, t0 + wt + 16 * y + li, f0 + (wa >> 1) + 4 * kg, v);
+        for (int y = 0; y < XN; ++y) {
+          if (wt + 16 * y + li >= count) continue;
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = swiglu_bf(acc[2 * q][y][e], acc[2 * q + 1][y][e]);
+          const int n = f0 + (wa >> 1) + 16 * q + 4 * kg;
+          if (shared) {
+            uint2 o;
+            o.x = pack2(v[0], v[1]);
+            o.y = pack2(v[2], v[3]);
+            *reinterpret_cast<uint2*>(reinterpret_cast<bf16_t*>(a.Y2) + g * a.y2g +
+                                      (int64_t)(t0 + wt + 16 * y + li) * a.y2s + n) = o;
+          } else {
+            gemm_store4(a, g, t0 + wt + 16 * y + li, n, v);
+          }
         }
-      }
     } else {
 #pragma unroll
-      for (int x = 0; x < 2; ++x)
+      for (int x = 0; x < XM; ++x)
 #pragma unroll
-        for (int y = 0; y < 2; ++y) {
+        for (int y = 0; y < XN; ++y) {
           if (wt + 16 * y + li >= count) continue;
           if (shared) {  // fp32 partial of one half (the halves are summed by the consumer)
             float* yp = reinterpret_cast<float*>(a.Y2) + g * a.y2g + (int64_t)(t0 + wt + 16 * y + li) * a.y2s + f0 +
@@ -594,13 +610,24 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const GemmArgs a, const D
   }
 }
 
-// grouped: max_tiles entries of a 64-token tile table; dense: a.rows tokens
-static void launch_dma(const GemmArgs& a, bool swiglu, hipStream_t st, int max_tiles = 0) {
+// grouped: max_tiles entries of a tile table of 64 (big: 128) tokens; dense: a.rows tokens.
+// big: 128 weight rows x 128 tokens per workgroup (each wave 64 x 64, 4 x 4 MFMA blocks),
+// 32 KB stages, one workgroup per CU -- for expert tiles of hundreds of tokens (prefill,
+// every row on the same experts), where the 64 x 64 shape re-reads each weight chunk once
+// per 64 tokens and issues one MFMA per 2 KB of LDS reads.
+static void launch_dma(const GemmArgs& a, bool swiglu, hipStream_t st, int max_tiles = 0, bool big = false) {
   DmaShape sh;
-  sh.nfb = a.N / (swiglu ? 32 : 64);
-  sh.tiles = a.tiles ? max_tiles : (a.rows + 63) / 64;
-  // grouped: two resident workgroups per CU, looping over the live items
-  sh.nwg = a.tiles ? kDmaGroupedWgs : (sh.nfb * sh.tiles + 7) / 8 * 8;
+  const int tn = big ? 128 : 64;
+  sh.nfb = a.N / (swiglu ? (big ? 64 : 32) : (big ? 128 : 64));
+  sh.tiles = a.tiles ? max_tiles : (a.rows + tn - 1) / tn;
+  // grouped: resident workgroups (two per CU, big: one) looping over the live items
+  sh.nwg = a.tiles ? (big ? kDmaGroupedWgs / 2 : kDmaGroupedWgs) : (sh.nfb * sh.tiles + 7) / 8 * 8;
+  if (big) {
+    constexpr int lds = kDmaStages * 32768;
+    if (swiglu) hipLaunchKernelGGL((gemm_dma_kernel<true, 64, 64>), dim3(sh.nwg), dim3(256), lds, st, a, sh);
+    else hipLaunchKernelGGL((gemm_dma_kernel<false, 64, 64>), dim3(sh.nwg), dim3(256), lds, st, a, sh);
+    return;
+  }
   if (swiglu) hipLaunchKernelGGL(gemm_dma_kernel<true>, dim3(sh.nwg), dim3(256), kDmaStages * 16384, st, a, sh);
   else hipLaunchKernelGGL(gemm_dma_kernel<false>, dim3(sh.nwg), dim3(256), kDmaStages * 16384, st, a, sh);
 }
@@ -834,6 +861,7 @@ static int pick_tb(int rows) { return rows <= 16 ? 1 : (rows <= 32 ? 2 : (rows <
 // the largest token tile that still gives ~200 workgroups (SwiGLU: 64-token tiles); long K
 // with few features on 16/32-token tiles.  Returns false (nothing launched) for shapes left
 // to launch_gemm: huge N, long K with SwiGLU or groups, or N not a multiple of 16*rbw.
+constexpr int kBigTileRows = 512;
 static bool launch_dense_os(GemmArgs a, int groups, bool swiglu, hipStream_t st) {
   const int rows = a.rows, K = a.K;
   if (K > 4096 && !swiglu && groups == 1 && a.N % 64 == 0 && a.N < 16384) {
@@ -845,6 +873,11 @@ static bool launch_dense_os(GemmArgs a, int groups, bool swiglu, hipStream_t st)
     if (a.tiles_per_group > 65535) return false;
     if (tb == 1) launch_xlds_variant<1, false, 4, true, 2>(a, a.tiles_per_group, st);
     else launch_xlds_variant<2, false, 4, true, 2>(a, a.tiles_per_group, st);
+    return true;
+  }
+  if (groups == 1 && K <= 4096 && rows >= kBigTileRows && a.N % (swiglu ? 64 : 128) == 0) {
+    // prefill-size row counts: 128 weight rows x 128 tokens per workgroup
+    launch_dma(a, swiglu, st, 0, true);
     return true;
   }
   if (!swiglu && groups == 1 && K <= 4096 && a.N % 64 == 0 &&
@@ -951,8 +984,8 @@ extern "C" int dsv2_moe_grouped_gateup(const void* xn, const int32_t* sorted_rou
   DSV2_REQUIRE(xn && sorted_routes && tiles && num_tiles && w_gate_up && hsorted, DSV2_E_NULL,
                "moe_grouped_gateup: null pointer");
   DSV2_REQUIRE(max_tiles >= 0 && max_tiles <= 65535 && inter > 0 && inter % 16 == 0 &&
-                   (tile_tokens == 16 || tile_tokens == 32 || tile_tokens == 64),
-               DSV2_E_SHAPE, "moe_grouped_gateup: bad shape (inter %% 16, tile_tokens in {16,32,64})");
+                   (tile_tokens == 16 || tile_tokens == 32 || tile_tokens == 64 || tile_tokens == 128),
+               DSV2_E_SHAPE, "moe_grouped_gateup: bad shape (inter %% 16, tile_tokens in {16,32,64,128})");
   DSV2_REQUIRE(dsv2_aligned16(xn) && dsv2_aligned16(w_gate_up) && dsv2_aligned16(tiles), DSV2_E_ALIGN,
                "moe_grouped_gateup: alignment");
   if (max_tiles == 0) return DSV2_OK;
@@ -971,12 +1004,13 @@ extern "C" int dsv2_moe_grouped_gateup(const void* xn, const int32_t* sorted_rou
   a.Y = hsorted;
   a.ys = inter;
   a.yg = 0;
-  if (tile_tokens == 64 && inter % 32 == 0) {
-    // 64-token tiles on the direct-to-LDS ring (reference workload, 6 experts x 256 tokens:
-    // 45 us vs 71 us for the token-rows-in-LDS shape; x 64 tokens: 26.0 vs 26.8 us)
-    launch_dma(a, true, (hipStream_t)stream, max_tiles);
+  if ((tile_tokens == 64 && inter % 32 == 0) || (tile_tokens == 128 && inter % 64 == 0)) {
+    // 64- and 128-token tiles on the direct-to-LDS ring (reference workload, 6 experts x 256
+    // tokens: 45 us vs 71 us for the token-rows-in-LDS shape; x 64 tokens: 26.0 vs 26.8 us)
+    launch_dma(a, true, (hipStream_t)stream, max_tiles, tile_tokens == 128);
     return dsv2_launch_status("moe_grouped_gateup");
   }
+  DSV2_REQUIRE(tile_tokens != 128, DSV2_E_SHAPE, "moe_grouped_gateup: 128-token tiles need inter %% 64");
   return launch_gemm(a, tile_tb(tile_tokens), true, max_tiles, (hipStream_t)stream);
 }
 
@@ -987,9 +1021,9 @@ extern "C" int dsv2_moe_grouped_gateup_shared(const void* xn, int rows, const in
   DSV2_REQUIRE(xn && sorted_routes && tiles && num_tiles && w_gate_up && sh_gate_up && hsorted && shared_out,
                DSV2_E_NULL, "moe_grouped_gateup_shared: null pointer");
   DSV2_REQUIRE(rows >= 0 && max_tiles >= 0 && max_tiles <= 65535 && inter > 0 && inter % 64 == 0 &&
-                   (tile_tokens == 16 || tile_tokens == 32 || tile_tokens == 64) &&
-                   (tile_tokens == 64 || (int64_t)max_tiles + 2 * ((rows + tile_tokens - 1) / tile_tokens) <= 65535),
-               DSV2_E_SHAPE, "moe_grouped_gateup_shared: bad shape (inter %% 64, tile_tokens in {16,32,64})");
+                   (tile_tokens == 16 || tile_tokens == 32 || tile_tokens == 64 || tile_tokens == 128) &&
+                   (tile_tokens >= 64 || (int64_t)max_tiles + 2 * ((rows + tile_tokens - 1) / tile_tokens) <= 65535),
+               DSV2_E_SHAPE, "moe_grouped_gateup_shared: bad shape (inter %% 64, tile_tokens in {16,32,64,128})");
   DSV2_REQUIRE(dsv2_aligned16(xn) && dsv2_aligned16(w_gate_up) && dsv2_aligned16(sh_gate_up) &&
                    dsv2_aligned16(tiles) && dsv2_aligned16(shared_out),
                DSV2_E_ALIGN, "moe_grouped_gateup_shared: alignment");
@@ -1018,8 +1052,8 @@ extern "C" int dsv2_moe_grouped_gateup_shared(const void* xn, int rows, const in
   a.Y2 = shared_out;
   a.y2s = 2 * inter;
   a.y2g = inter;
-  if (tile_tokens == 64) {
-    launch_dma(a, true, (hipStream_t)stream, max_tiles);
+  if (tile_tokens >= 64) {
+    launch_dma(a, true, (hipStream_t)stream, max_tiles, tile_tokens == 128);
     return dsv2_launch_status("moe_grouped_gateup_shared");
   }
   return launch_gemm(a, tile_tb(tile_tokens), true, 2 * a.s_tiles + max_tiles, (hipStream_t)stream);
@@ -1032,9 +1066,9 @@ extern "C" int dsv2_moe_grouped_down_shared(const void* hsorted, int rows, const
   DSV2_REQUIRE(hsorted && tiles && num_tiles && w_down && shared_mid && sh_down && ysorted && shared_parts,
                DSV2_E_NULL, "moe_grouped_down_shared: null pointer");
   DSV2_REQUIRE(rows >= 0 && max_tiles >= 0 && max_tiles <= 65535 && inter > 0 && inter % 64 == 0 &&
-                   (tile_tokens == 16 || tile_tokens == 32 || tile_tokens == 64) &&
-                   (tile_tokens == 64 || (int64_t)max_tiles + 2 * ((rows + tile_tokens - 1) / tile_tokens) <= 65535),
-               DSV2_E_SHAPE, "moe_grouped_down_shared: bad shape (inter %% 64, tile_tokens in {16,32,64})");
+                   (tile_tokens == 16 || tile_tokens == 32 || tile_tokens == 64 || tile_tokens == 128) &&
+                   (tile_tokens >= 64 || (int64_t)max_tiles + 2 * ((rows + tile_tokens - 1) / tile_tokens) <= 65535),
+               DSV2_E_SHAPE, "moe_grouped_down_shared: bad shape (inter %% 64, tile_tokens in {16,32,64,128})");
   DSV2_REQUIRE(dsv2_aligned16(hsorted) && dsv2_aligned16(w_down) && dsv2_aligned16(shared_mid) &&
                    dsv2_aligned16(sh_down) && dsv2_aligned16(tiles) && dsv2_aligned16(ysorted) &&
                    dsv2_aligned16(shared_parts),
@@ -1063,8 +1097,8 @@ extern "C" int dsv2_moe_grouped_down_shared(const void* hsorted, int rows, const
   a.Y2 = shared_parts;
   a.y2s = 2048;
   a.y2g = (int64_t)rows * 2048;
-  if (tile_tokens == 64) {
-    launch_dma(a, false, (hipStream_t)stream, max_tiles);
+  if (tile_tokens >= 64) {
+    launch_dma(a, false, (hipStream_t)stream, max_tiles, tile_tokens == 128);
     return dsv2_launch_status("moe_grouped_down_shared");
   }
   return launch_gemm(a, tile_tb(tile_tokens), false, 2 * a.s_tiles + max_tiles, (hipStream_t)stream);
@@ -1075,7 +1109,7 @@ extern "C" int dsv2_moe_grouped_down(const void* hsorted, const int32_t* tiles, 
                                      void* stream) {
   DSV2_REQUIRE(hsorted && tiles && num_tiles && w_down && ysorted, DSV2_E_NULL, "moe_grouped_down: null pointer");
   DSV2_REQUIRE(max_tiles >= 0 && max_tiles <= 65535 && inter > 0 && inter % 64 == 0 &&
-                   (tile_tokens == 16 || tile_tokens == 32 || tile_tokens == 64),
+                   (tile_tokens == 16 || tile_tokens == 32 || tile_tokens == 64 || tile_tokens == 128),
                DSV2_E_SHAPE, "moe_grouped_down: bad shape");
   DSV2_REQUIRE(dsv2_aligned16(hsorted) && dsv2_aligned16(w_down) && dsv2_aligned16(tiles) && inter % 8 == 0,
                DSV2_E_ALIGN, "moe_grouped_down: alignment");
@@ -1095,9 +1129,9 @@ extern "C" int dsv2_moe_grouped_down(const void* hsorted, const int32_t* tiles, 
   a.Y = ysorted;
   a.ys = 2048;
   a.yg = 0;
-  if (tile_tokens == 64) {
+  if (tile_tokens >= 64) {
     // 6 experts x 256 tokens: 24 us vs 35 us; x 64 tokens: 12.0 vs 16.3 us
-    launch_dma(a, false, (hipStream_t)stream, max_tiles);
+    launch_dma(a, false, (hipStream_t)stream, max_tiles, tile_tokens == 128);
     return dsv2_launch_status("moe_grouped_down");
   }
   return launch_gemm(a, tile_tb(tile_tokens), false, max_tiles, (hipStream_t)stream);

@@ -41,6 +41,9 @@ FUSED_MLA_MAX_CTX = 2048
 # plus a one-wave top-6 per row (64 rows: 8.3 us vs 11.1 us for one workgroup per token on
 # MI355X); above it one workgroup per token (256 rows: 11.4 us vs 14.7 us)
 SPLIT_ROUTER_MAX_ROWS = 64
+# grouped MoE: above this many routes per expert the 128-token tiles (128 x 128 ring GEMM;
+# the reference workload at bsz=256, 256 routes per expert, is 2% faster on 64-token tiles)
+BIG_TILE_LOAD = 384
 
 
 def moe_tile_tokens(rows: int, n_experts: int = 64, top_k: int = 6) -> int:
@@ -56,7 +59,7 @@ def tile_tokens_for_load(load: float) -> int:
     7 routes per expert) 8.71k tok/s with 32-token tiles vs 8.58k with 16 and 8.13k with 64;
     bsz=256 (about 25) 22.42k with 64 vs 21.79k with 32; every row on the same 6 experts
     (64 or 256 routes per expert) 64."""
-    return 16 if load <= 3 else (32 if load <= 12 else 64)
+    return 16 if load <= 3 else (32 if load <= 12 else (64 if load <= BIG_TILE_LOAD else 128))
 
 
 def shared_in_grouped(rows: int, tile_tokens: int) -> bool:
@@ -150,10 +153,10 @@ class RowBuffers:
 
 
     def set_tile_tokens(self, tile_tokens: int) -> None:
-        """Token tile of the grouped MoE launches (16, 32 or 64); the tile table was sized
-        for the smallest."""
-        if tile_tokens not in (16, 32, 64):
-            raise ValueError(f"tile_tokens must be 16, 32 or 64, got {tile_tokens}")
+        """Token tile of the grouped MoE launches (16, 32, 64 or 128); the tile table was
+        sized for the smallest."""
+        if tile_tokens not in (16, 32, 64, 128):
+            raise ValueError(f"tile_tokens must be 16, 32, 64 or 128, got {tile_tokens}")
         self.tile_tokens = tile_tokens
         self.max_tiles = math.ceil(self._routes / tile_tokens) + self._n_experts
 
@@ -175,7 +178,7 @@ class DecodeEngine:
                  max_prefill_rows: int = 8192, device="cuda", mla_path: str = "absorb", moe_tile: int | None = None,
                  expert_dtype: str = "bf16"):
         """capacities: cache tokens of each row (slot).  moe_tile (batch family): fix the
-        grouped MoE token tile (16, 32 or 64) instead of choosing it from the routing of one
+        grouped MoE token tile (16, 32, 64 or 128) instead of choosing it from the routing of one
         eager step at capture -- for a serving loop whose batch changes under one graph.
         expert_dtype "fp8" (small family): the decode step reads the e4m3 expert weights of
         quantize_experts_fp8 (prefill keeps the bf16 kernels on the dequantized weights)."""
