@@ -433,13 +433,14 @@ struct DmaShape {
 // the live (tile, feature block) items only, so the table's dead tiles cost no workgroup
 // launches; token rows are gathered through slot_row and the tile's expert selects the
 // weights.
-template <bool SWIGLU, int WM = 32, int WN = 32, int ST = kDmaStages>
-__global__ __launch_bounds__(256) void gemm_dma_kernel(const GemmArgs a, const DmaShape sh) {
+template <bool SWIGLU, int WM = 32, int WN = 32, int ST = kDmaStages, int RWV = 2>
+__global__ __launch_bounds__(RWV * 128) void gemm_dma_kernel(const GemmArgs a, const DmaShape sh) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // ST stages of SB bytes
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, li = lane & 15, kg = lane >> 4;
-  constexpr int TM = 2 * WM, TN = 2 * WN;  // weight rows, tokens per workgroup (2 x 2 waves)
+  constexpr int NW = 2 * RWV;                // waves: RWV along the weight rows x 2 along the tokens
+  constexpr int TM = RWV * WM, TN = 2 * WN;  // weight rows, tokens per workgroup
   constexpr int SB = (TM + TN) * 128;      // stage: TM weight rows, then TN token rows, 128 B each
-  constexpr int LW = TM / 32, LL = (TM + TN) / 32;  // ring loads per wave per chunk: weights, all
+  constexpr int LW = TM / (8 * NW), LL = (TM + TN) / (8 * NW);  // ring loads per wave per chunk: weights, all
   constexpr int XM = WM / 16, XN = WN / 16;         // MFMA blocks per wave
   constexpr int FPW = SWIGLU ? TM / 2 : TM;  // output features per workgroup
   static_assert(LL <= 8 && XM <= 4 && XN <= 4, "local arrays have literal sizes");
@@ -490,7 +491,7 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const GemmArgs a, const D
 #pragma unroll
     for (int j = 0; j < LL; ++j) {
       const bool tok = j >= LW;
-      const int r = (tok ? (TN / 4) * wv + 8 * (j - LW) : (TM / 4) * wv + 8 * j) + (lane >> 3);
+      const int r = (tok ? (TN / NW) * wv + 8 * (j - LW) : (TM / NW) * wv + 8 * j) + (lane >> 3);
       const int pc = (lane & 7) ^ (r & 7);
       if (tok) {
         const int slot = t0 + (r < count ? r : 0);  // rows past the tile: the tile's first row
@@ -505,7 +506,7 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const GemmArgs a, const D
       } else {
         src[j] = wbase + (f0 + r) * wld + pc * 8;
       }
-      dst[j] = (tok ? TM * 128 + ((TN / 4) * wv + 8 * (j - LW)) * 128 : ((TM / 4) * wv + 8 * j) * 128);
+      dst[j] = (tok ? TM * 128 + ((TN / NW) * wv + 8 * (j - LW)) * 128 : ((TM / NW) * wv + 8 * j) * 128);
     }
     // the item's K chunks start at a rotation that spreads the workgroups' concurrent requests
     // over the weight rows' address range instead of one column of 128 B lines (C3 grouped
@@ -528,7 +529,7 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const GemmArgs a, const D
     for (int x = 0; x < XM; ++x)
 #pragma unroll
       for (int y = 0; y < XN; ++y) acc[x][y] = floatx4_t{0.f, 0.f, 0.f, 0.f};
-    const int wa = (wv & 1) * WM, wt = (wv >> 1) * WN;  // this wave's WM weight rows x WN tokens
+    const int wa = (wv % RWV) * WM, wt = (wv / RWV) * WN;  // this wave's WM weight rows x WN tokens
 #pragma unroll
     for (int s = 0; s + 1 < ST; ++s) issue(s, s);
     for (int c0 = 0; c0 < nch; c0 += ST) {
@@ -611,21 +612,28 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const GemmArgs a, const D
 }
 
 // grouped: max_tiles entries of a tile table of 64 (big: 128) tokens; dense: a.rows tokens.
-// big: 128 weight rows x 128 tokens per workgroup (each wave 64 x 64, 4 x 4 MFMA blocks),
-// 32 KB stages, one workgroup per CU -- for expert tiles of hundreds of tokens (prefill,
-// every row on the same experts), where the 64 x 64 shape re-reads each weight chunk once
-// per 64 tokens and issues one MFMA per 2 KB of LDS reads.
+// big: 256 weight rows x 128 tokens per 8-wave workgroup (each wave 64 x 64, 4 x 4 MFMA
+// blocks), three 48 KB stages, one workgroup per CU -- for expert tiles of hundreds of tokens
+// (prefill), where the 64 x 64 shape re-reads each weight chunk once per 64 tokens and
+// issues one MFMA per 2 KB of LDS reads (C3 prefill 7.1 s -> 6.0 s with 128 x 128 per 4-wave
+// workgroup, 5.3 s with 256 x 128 per 8 waves).
+constexpr int kBigRwv = 4, kBigStages = 3;  // big: waves along the weight rows, ring stages
+constexpr int kBigRows = 64 * kBigRwv;                 // weight rows per big workgroup
 static void launch_dma(const GemmArgs& a, bool swiglu, hipStream_t st, int max_tiles = 0, bool big = false) {
   DmaShape sh;
   const int tn = big ? 128 : 64;
-  sh.nfb = a.N / (swiglu ? (big ? 64 : 32) : (big ? 128 : 64));
+  sh.nfb = a.N / (swiglu ? (big ? kBigRows / 2 : 32) : (big ? kBigRows : 64));
   sh.tiles = a.tiles ? max_tiles : (a.rows + tn - 1) / tn;
   // grouped: resident workgroups (two per CU, big: one) looping over the live items
   sh.nwg = a.tiles ? (big ? kDmaGroupedWgs / 2 : kDmaGroupedWgs) : (sh.nfb * sh.tiles + 7) / 8 * 8;
   if (big) {
-    constexpr int lds = kDmaStages * 32768;
-    if (swiglu) hipLaunchKernelGGL((gemm_dma_kernel<true, 64, 64>), dim3(sh.nwg), dim3(256), lds, st, a, sh);
-    else hipLaunchKernelGGL((gemm_dma_kernel<false, 64, 64>), dim3(sh.nwg), dim3(256), lds, st, a, sh);
+    constexpr int lds = kBigStages * (kBigRows + 128) * 128;
+    if (swiglu)
+      hipLaunchKernelGGL((gemm_dma_kernel<true, 64, 64, kBigStages, kBigRwv>), dim3(sh.nwg), dim3(128 * kBigRwv), lds,
+                         st, a, sh);
+    else
+      hipLaunchKernelGGL((gemm_dma_kernel<false, 64, 64, kBigStages, kBigRwv>), dim3(sh.nwg), dim3(128 * kBigRwv),
+                         lds, st, a, sh);
     return;
   }
   if (swiglu) hipLaunchKernelGGL(gemm_dma_kernel<true>, dim3(sh.nwg), dim3(256), kDmaStages * 16384, st, a, sh);
@@ -875,7 +883,7 @@ static bool launch_dense_os(GemmArgs a, int groups, bool swiglu, hipStream_t st)
     else launch_xlds_variant<2, false, 4, true, 2>(a, a.tiles_per_group, st);
     return true;
   }
-  if (groups == 1 && K <= 4096 && rows >= kBigTileRows && a.N % (swiglu ? 64 : 128) == 0) {
+  if (groups == 1 && K <= 4096 && rows >= kBigTileRows && a.N % (swiglu ? kBigRows / 2 : kBigRows) == 0) {
     // prefill-size row counts: 128 weight rows x 128 tokens per workgroup
     launch_dma(a, swiglu, st, 0, true);
     return true;
@@ -1004,13 +1012,13 @@ extern "C" int dsv2_moe_grouped_gateup(const void* xn, const int32_t* sorted_rou
   a.Y = hsorted;
   a.ys = inter;
   a.yg = 0;
-  if ((tile_tokens == 64 && inter % 32 == 0) || (tile_tokens == 128 && inter % 64 == 0)) {
+  if ((tile_tokens == 64 && inter % 32 == 0) || (tile_tokens == 128 && inter % (kBigRows / 2) == 0)) {
     // 64- and 128-token tiles on the direct-to-LDS ring (reference workload, 6 experts x 256
     // tokens: 45 us vs 71 us for the token-rows-in-LDS shape; x 64 tokens: 26.0 vs 26.8 us)
     launch_dma(a, true, (hipStream_t)stream, max_tiles, tile_tokens == 128);
     return dsv2_launch_status("moe_grouped_gateup");
   }
-  DSV2_REQUIRE(tile_tokens != 128, DSV2_E_SHAPE, "moe_grouped_gateup: 128-token tiles need inter %% 64");
+  DSV2_REQUIRE(tile_tokens != 128, DSV2_E_SHAPE, "moe_grouped_gateup: 128-token tiles need inter %% %d", kBigRows / 2);
   return launch_gemm(a, tile_tb(tile_tokens), true, max_tiles, (hipStream_t)stream);
 }
 
