@@ -504,7 +504,7 @@ __global__ __launch_bounds__(RWV * 128) void gemm_dma_kernel(const GemmArgs a, c
       } else if (SWIGLU) {
         src[j] = wbase + (f0 + (r >> 5) * 16 + ((r >> 4) & 1) * upoff + (r & 15)) * wld + pc * 8;
       } else {
-        src[j] = wbase + (f0 + r) * wld + pc * 8;
+        src[j] = wbase + (int64_t)min(f0 + r, a.N - 1) * wld + pc * 8;  // a ragged last block repeats row N-1
       }
       dst[j] = (tok ? TM * 128 + ((TN / NW) * wv + 8 * (j - LW)) * 128 : ((TM / NW) * wv + 8 * j) * 128);
     }
@@ -594,7 +594,7 @@ __global__ __launch_bounds__(RWV * 128) void gemm_dma_kernel(const GemmArgs a, c
       for (int x = 0; x < XM; ++x)
 #pragma unroll
         for (int y = 0; y < XN; ++y) {
-          if (wt + 16 * y + li >= count) continue;
+          if (wt + 16 * y + li >= count || f0 + wa + 16 * x >= a.N) continue;
           if (shared) {  // fp32 partial of one half (the halves are summed by the consumer)
             float* yp = reinterpret_cast<float*>(a.Y2) + g * a.y2g + (int64_t)(t0 + wt + 16 * y + li) * a.y2s + f0 +
                         wa + 16 * x + 4 * kg;
@@ -622,7 +622,8 @@ constexpr int kBigRows = 64 * kBigRwv;                 // weight rows per big wo
 static void launch_dma(const GemmArgs& a, bool swiglu, hipStream_t st, int max_tiles = 0, bool big = false) {
   DmaShape sh;
   const int tn = big ? 128 : 64;
-  sh.nfb = a.N / (swiglu ? (big ? kBigRows / 2 : 32) : (big ? kBigRows : 64));
+  // plain: a last feature block past N (N % 64 == 0) repeats row N-1 and stores nothing there
+  sh.nfb = swiglu ? a.N / (big ? kBigRows / 2 : 32) : (a.N + (big ? kBigRows : 64) - 1) / (big ? kBigRows : 64);
   sh.tiles = a.tiles ? max_tiles : (a.rows + tn - 1) / tn;
   // grouped: resident workgroups (two per CU, big: one) looping over the live items
   sh.nwg = a.tiles ? (big ? kDmaGroupedWgs / 2 : kDmaGroupedWgs) : (sh.nfb * sh.tiles + 7) / 8 * 8;
@@ -883,7 +884,8 @@ static bool launch_dense_os(GemmArgs a, int groups, bool swiglu, hipStream_t st)
     else launch_xlds_variant<2, false, 4, true, 2>(a, a.tiles_per_group, st);
     return true;
   }
-  if (groups == 1 && K <= 4096 && rows >= kBigTileRows && a.N % (swiglu ? kBigRows / 2 : kBigRows) == 0) {
+  if (groups == 1 && K <= 4096 && rows >= kBigTileRows && a.N >= kBigRows &&
+      a.N % (swiglu ? kBigRows / 2 : 64) == 0) {
     // prefill-size row counts: 128 weight rows x 128 tokens per workgroup
     launch_dma(a, swiglu, st, 0, true);
     return true;

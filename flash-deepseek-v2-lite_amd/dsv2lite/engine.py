@@ -41,6 +41,8 @@ FUSED_MLA_MAX_CTX = 2048
 # plus a one-wave top-6 per row (64 rows: 8.3 us vs 11.1 us for one workgroup per token on
 # MI355X); above it one workgroup per token (256 rows: 11.4 us vs 14.7 us)
 SPLIT_ROUTER_MAX_ROWS = 64
+# from this many rows (prefill chunks) the router runs as RMSNorm + an MFMA logits GEMM + top-6
+GEMM_ROUTER_MIN_ROWS = 1024
 # grouped MoE: above this many routes per expert the 128-token tiles (128 x 128 ring GEMM;
 # the reference workload at bsz=256, 256 routes per expert, is 2% faster on 64-token tiles)
 BIG_TILE_LOAD = 384
@@ -351,7 +353,14 @@ class DecodeEngine:
                      ptr(b.h), H, ptr(b.h), H, 0, st)
             return
         if L.moe:
-            if R <= SPLIT_ROUTER_MAX_ROWS:
+            if R >= GEMM_ROUTER_MIN_ROWS:
+                # prefill chunks: the norm, the logits as an MFMA GEMM, then the top-6
+                call("dsv2_rmsnorm_bf16", ptr(b.h), H, ptr(L.ln_post), ptr(b.xn), H, R, H, c.eps, st)
+                call("dsv2_gemm_bf16", ptr(b.xn), H, 0, R, H, ptr(L.w_router), 0, c.n_experts, 1, None, 0,
+                     ptr(b.router_logits), c.n_experts, 0, LINEAR_OUT_F32, st)
+                call("dsv2_router_topk6_from_logits", ptr(b.router_logits), R, c.routed_scaling, ptr(b.ids32), None,
+                     ptr(b.wts), st)
+            elif R <= SPLIT_ROUTER_MAX_ROWS:
                 call("dsv2_router_logits", ptr(b.h), H, ptr(L.ln_post), c.eps, ptr(L.w_router), R, ptr(b.xn),
                      ptr(b.router_logits), st)
                 call("dsv2_router_topk6_from_logits", ptr(b.router_logits), R, c.routed_scaling, ptr(b.ids32), None,

@@ -151,14 +151,16 @@ def test_gemm_k_split_shapes(rows, K, N, swiglu):
     assert rel_err(y.float(), ref) < 1e-2
 
 
-@pytest.mark.parametrize("rows", [16, 64, 130, 256])
+@pytest.mark.parametrize("rows", [16, 64, 130, 256, 600, 1030])
 @pytest.mark.parametrize("K,N,mode", [(2048, 3648, "plain"), (2048, 2048, "residual"), (2048, 2816, "swiglu"),
                                       (2816, 2048, "plain"), (2048, 10944, "swiglu"), (10944, 2048, "residual"),
-                                      (2048, 2048, "f32")])
+                                      (2048, 2048, "f32"), (2048, 64, "f32")])
 def test_gemm_dense_model_shapes(rows, K, N, mode):
     """The batch family's dense projections (qkv_a, o_proj + residual, shared-expert
-    gate_up / down, layer-0 MLP gate_up / down + residual) at the token counts where the
-    one-shot and the token-rows-in-LDS shapes take over from the k-split kernel."""
+    gate_up / down, layer-0 MLP gate_up / down + residual, the router logits) at the token
+    counts where the one-shot and the token-rows-in-LDS shapes take over from the k-split
+    kernel, and at prefill sizes (from 512 rows: 256 x 128 ring tiles, qkv_a with a ragged
+    last feature block)."""
     x = rnd(rows, K, seed=K + N + rows)
     W = rnd(2 * N if mode == "swiglu" else N, K, std=0.02, seed=K + N)
     res = rnd(rows, N, seed=3 * rows) if mode == "residual" else None
