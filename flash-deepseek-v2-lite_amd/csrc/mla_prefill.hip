@@ -8,8 +8,9 @@
 // 320 multiply-adds per (query, key, head) against 1088 for the absorbed (latent) form the
 // decode step uses, which pays off when every cached token is attended by many queries.
 //
-// One 256-thread workgroup per (tile of <= 64 consecutive query tokens of one sequence,
-// head); wave w owns queries 16w .. 16w + 15 of the tile.  Keys go in 32-token tiles,
+// One 256-thread workgroup per (tile of <= 128 consecutive query tokens of one sequence,
+// head); wave w owns queries 32w .. 32w + 31 of the tile, two 16-query blocks that share
+// every K and V^T fragment the wave reads from LDS.  Keys go in 32-token tiles,
 // double-buffered in LDS (the next tile's 16-byte chunks in registers meanwhile):
 //   S^T = K Q^T   two 16-key blocks x 6 k-steps of v_mfma_f32_16x16x32_bf16 (queries = N)
 //   online softmax per query (column), fp32, the causal mask key <= query position
@@ -27,6 +28,8 @@ constexpr int kHeads = 16;
 constexpr int kCacheRow = 576;
 constexpr int kChunksPerKey = kQK / 8 + kVD / 8;  // 16-byte chunks per key: 16 nope + 8 rope + 16 v = 40
 constexpr int kLoads = kKT * kChunksPerKey / 256;  // per thread per tile: 5
+constexpr int kQB = 2;                             // 16-query blocks per wave
+constexpr int kQT = 4 * 16 * kQB;                  // queries per workgroup tile
 }  // namespace
 
 __global__ __launch_bounds__(256, 2) void mla_prefill_kernel(
@@ -40,21 +43,25 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_kernel(
   const int h = blockIdx.y;
   // every index derived from the tile table is clamped into the buffers the host described
   // (a malformed table gives wrong numbers, never an access outside them)
-  const int r0 = min(max(tl.x, 0), rows - 1), nr = min(max(tl.y, 1), min(64, rows - r0)), p0 = max(tl.z, 0);
+  const int r0 = min(max(tl.x, 0), rows - 1), nr = min(max(tl.y, 1), min(kQT, rows - r0)), p0 = max(tl.z, 0);
   const int64_t sb = tl.w;  // cache row of position 0 of the tile's sequence
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, li = lane & 15, kg = lane >> 4;
-  const int j = wv * 16 + li;                  // this lane's query (column) in the tile
-  const int r = r0 + min(j, nr - 1);           // its row (queries past the tile repeat the last one)
-  const int qp = p0 + j;                       // its position
-  const int nkv = p0 + nr;                     // keys [0, nkv) of the sequence
+  int jq[kQB], qp[kQB];
+  bf16x8_t qf[kQB][6];
+#pragma unroll
+  for (int qb = 0; qb < kQB; ++qb) {
+    jq[qb] = wv * 16 * kQB + 16 * qb + li;  // this lane's query (column) of block qb in the tile
+    const int r = r0 + min(jq[qb], nr - 1);  // its row (queries past the tile repeat the last one)
+    qp[qb] = p0 + jq[qb];                    // its position
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      qf[qb][kk] = as_bf16x8(ldg16(qkva + (int64_t)r * qs + h * 192 + kk * 32 + kg * 8));
+#pragma unroll
+    for (int kk = 4; kk < 6; ++kk)
+      qf[qb][kk] = as_bf16x8(ldg16(qrope + (int64_t)r * qrs + h * kCacheRow + 512 + (kk - 4) * 32 + kg * 8));
+  }
+  const int nkv = p0 + nr;  // keys [0, nkv) of the sequence
   const int ntiles = (nkv + kKT - 1) / kKT;
-
-  bf16x8_t qf[6];
-#pragma unroll
-  for (int kk = 0; kk < 4; ++kk) qf[kk] = as_bf16x8(ldg16(qkva + (int64_t)r * qs + h * 192 + kk * 32 + kg * 8));
-#pragma unroll
-  for (int kk = 4; kk < 6; ++kk)
-    qf[kk] = as_bf16x8(ldg16(qrope + (int64_t)r * qrs + h * kCacheRow + 512 + (kk - 4) * 32 + kg * 8));
 
   uint4 st[kLoads];
   auto load_tile = [&](int t0) {
@@ -89,75 +96,96 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_kernel(
   store_tile(0);
   __syncthreads();
 
-  float m_run = -INFINITY, l_run = 0.f;
-  floatx4_t acc[8];
+  float m_run[kQB], l_run[kQB];
+  floatx4_t acc[kQB][8];
 #pragma unroll
-  for (int mb = 0; mb < 8; ++mb) acc[mb] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+  for (int qb = 0; qb < kQB; ++qb) {
+    m_run[qb] = -INFINITY;
+    l_run[qb] = 0.f;
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) acc[qb][mb] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+  }
 
   for (int it = 0; it < ntiles; ++it) {
     const int buf = it & 1;
     const int t0 = it * kKT;
     if (it + 1 < ntiles) load_tile(t0 + kKT);
-    // S^T: sc[blk][e] = score(key t0 + blk*16 + 4kg + e, query j)
-    floatx4_t sc[2];
+    // S^T: sc[qb][blk][e] = score(key t0 + blk*16 + 4kg + e, query jq[qb]); each K fragment
+    // serves both query blocks
+    floatx4_t sc[kQB][2];
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk) {
-      floatx4_t sp = floatx4_t{0.f, 0.f, 0.f, 0.f};
+      floatx4_t sp[kQB];
+#pragma unroll
+      for (int qb = 0; qb < kQB; ++qb) sp[qb] = floatx4_t{0.f, 0.f, 0.f, 0.f};
       const bf16_t* kr = &kt[buf][(blk * 16 + li) * kKRow + kg * 8];
 #pragma unroll
-      for (int kk = 0; kk < 6; ++kk) sp = mfma16x16x32(*reinterpret_cast<const bf16x8_t*>(kr + kk * 32), qf[kk], sp);
-      sc[blk] = sp;
-    }
-    float p[8];
-    float mx = -INFINITY;
+      for (int kk = 0; kk < 6; ++kk) {
+        const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(kr + kk * 32);
 #pragma unroll
-    for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int kp = t0 + blk * 16 + 4 * kg + e;
-        const float v = kp <= qp ? sc[blk][e] * scale_log2 : -INFINITY;
-        p[blk * 4 + e] = v;
-        mx = fmaxf(mx, v);
+        for (int qb = 0; qb < kQB; ++qb) sp[qb] = mfma16x16x32(kf, qf[qb][kk], sp[qb]);
       }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);  // finite: key 0 is in the first tile of every query
-    const float alpha = exp2f(m_run - m_new);
-    float rsum = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      p[i] = exp2f(p[i] - m_new);
-      rsum += p[i];
+      for (int qb = 0; qb < kQB; ++qb) sc[qb][blk] = sp[qb];
     }
-    rsum += __shfl_xor(rsum, 16, 64);
-    rsum += __shfl_xor(rsum, 32, 64);
-    l_run = l_run * alpha + rsum;
-    m_run = m_new;
+    bf16x8_t pb[kQB];
 #pragma unroll
-    for (int mb = 0; mb < 8; ++mb) acc[mb] *= alpha;
+    for (int qb = 0; qb < kQB; ++qb) {
+      float p[8];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int kp = t0 + blk * 16 + 4 * kg + e;
+          const float v = kp <= qp[qb] ? sc[qb][blk][e] * scale_log2 : -INFINITY;
+          p[blk * 4 + e] = v;
+          mx = fmaxf(mx, v);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m_run[qb], mx);  // finite: key 0 is in the first tile of every query
+      const float alpha = exp2f(m_run[qb] - m_new);
+      float rsum = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        p[i] = exp2f(p[i] - m_new);
+        rsum += p[i];
+      }
+      rsum += __shfl_xor(rsum, 16, 64);
+      rsum += __shfl_xor(rsum, 32, 64);
+      l_run[qb] = l_run[qb] * alpha + rsum;
+      m_run[qb] = m_new;
+#pragma unroll
+      for (int mb = 0; mb < 8; ++mb) acc[qb][mb] *= alpha;
+      pb[qb] = as_bf16x8(pack8(p));
+    }
     // O^T += V^T P^T: lane (li, kg) addresses key 4kg + li/4 (then 16 + 4kg + li/4), dims
     // 16mb + 4(li % 4) .. +3, and receives V[4kg + e][16mb + li] (then V[16 + 4kg + e][..]),
-    // the keys of its P^T column in the same order
-    const bf16x8_t pb = as_bf16x8(pack8(p));
+    // the keys of its P^T column in the same order; each V^T fragment serves both blocks
     const bf16_t* vp = &vt[buf][(4 * kg + (li >> 2)) * kVRow + 4 * (li & 3)];
 #pragma unroll
     for (int mb = 0; mb < 8; ++mb) {
       const uint2 lo = lds_read_tr16(vp + mb * 16), hi = lds_read_tr16(vp + mb * 16 + 16 * kVRow);
-      acc[mb] = mfma16x16x32(as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y)), pb, acc[mb]);
+      const bf16x8_t vf = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+#pragma unroll
+      for (int qb = 0; qb < kQB; ++qb) acc[qb][mb] = mfma16x16x32(vf, pb[qb], acc[qb][mb]);
     }
     // buffer buf ^ 1 was last read in iteration it - 1, which every wave finished before
     // that iteration's closing barrier
     if (it + 1 < ntiles) store_tile(buf ^ 1);
     __syncthreads();
   }
-  if (j < nr) {
-    const float inv = 1.f / l_run;
-    bf16_t* o = out + (int64_t)(r0 + j) * os + h * kVD + 4 * kg;
+#pragma unroll
+  for (int qb = 0; qb < kQB; ++qb) {
+    if (jq[qb] >= nr) continue;
+    const float inv = 1.f / l_run[qb];
+    bf16_t* o = out + (int64_t)(r0 + jq[qb]) * os + h * kVD + 4 * kg;
 #pragma unroll
     for (int mb = 0; mb < 8; ++mb) {
       uint2 w;
-      w.x = pack2(acc[mb][0] * inv, acc[mb][1] * inv);
-      w.y = pack2(acc[mb][2] * inv, acc[mb][3] * inv);
+      w.x = pack2(acc[qb][mb][0] * inv, acc[qb][mb][1] * inv);
+      w.y = pack2(acc[qb][mb][2] * inv, acc[qb][mb][3] * inv);
       *reinterpret_cast<uint2*>(o + mb * 16) = w;
     }
   }

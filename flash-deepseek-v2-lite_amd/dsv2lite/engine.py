@@ -83,7 +83,7 @@ def routing_load(ids: torch.Tensor, n_experts: int = 64) -> float:
 
 
 class PrefillPlan:
-    """One prefill chunk's attention work: the query tiles (<= 64 consecutive rows of one
+    """One prefill chunk's attention work: the query tiles (<= 128 consecutive rows of one
     sequence each: first row, rows, first position, the sequence's cache base) and the cache
     rows [exp_lo, exp_lo + exp_rows) whose keys / values the chunk expands."""
 
@@ -93,7 +93,7 @@ class PrefillPlan:
         self.kexp, self.vexp = kexp, vexp
 
 
-def prefill_tiles(seq: torch.Tensor, posv: torch.Tensor, bases: list[int], tile: int = 64) -> tuple[torch.Tensor, int, int]:
+def prefill_tiles(seq: torch.Tensor, posv: torch.Tensor, bases: list[int], tile: int = 128) -> tuple[torch.Tensor, int, int]:
     """Query tiles of one chunk (seq[r]: sequence of chunk row r, posv[r]: its position;
     rows of a sequence are consecutive with consecutive positions) and the cache row range
     its attention reads: from the lowest sequence base to the last position of any row."""
@@ -311,7 +311,7 @@ class DecodeEngine:
         """A prefill chunk's attention in the expanded form: the chunk's cache rows and
         RoPE(q_pe) (mla_prepare), k_nope / v of every cache row the chunk attends (W_UK /
         W_UV over the latent: grouped GEMMs over the heads), causal flash attention per
-        (64-query tile, head), then o_proj with the residual."""
+        (128-query tile, head), then o_proj with the residual."""
         c = self.cfg
         H, nh = c.hidden, c.n_heads
         call("dsv2_gemm_bf16", ptr(b.xn), H, 0, R, H, ptr(L.w_qkva), 0, c.qkva_dim, 1, None, 0, ptr(b.qkva),
@@ -452,7 +452,7 @@ class DecodeEngine:
         """Eager prefill of one prompt per row: chunks of <= max_prefill_rows prompt tokens
         (one kernel row each, in sequence order) through the batch-family projections and
         grouped MoE, with the attention in MLA's expanded form (the chunk's cache rows, k_nope
-        / v of the cached prefix by grouped GEMMs, causal MFMA flash attention per 64-query
+        / v of the cached prefix by grouped GEMMs, causal MFMA flash attention per 128-query
         tile and head).  Writes the compressed cache, sets cache.pos = prompt lengths and
         self.ids = greedy first tokens (returned).  Mirrors _prefill_once (src/run.py:526-544).
         With `record`, it receives the per-layer records of each sequence's LAST prompt token,

@@ -274,7 +274,7 @@ int dsv2_attention_decode_expanded(const void* q, int64_t q_stride_b, int64_t q_
  *   v_nh = v[sb + n - exp_lo, h, :128]
  * k_nope / v [exp_rows, 16, 128] bf16 are W_UK / W_UV applied to cache rows exp_lo .. (the
  * kv_b projection of every cached token; dsv2_gemm_bf16 grouped over heads).  tiles [n_tiles]
- * int32x4 {first row, rows (1..64), position of the first row, sb}: <= 64 consecutive query
+ * int32x4 {first row, rows (1..128), position of the first row, sb}: <= 128 consecutive query
  * rows of one sequence each.  Indices derived from the table are clamped into rows /
  * cache_rows / exp_rows.  Replaces the prefill attention of the HF model the reference runs
  * eagerly (src/run.py:526-544; remote DeepseekV2Attention.forward over the expanded K/V). */

@@ -322,7 +322,7 @@ def test_bench_mfma_summary_uses_the_timing_graph_dispatches(tmp_path):
 
 
 def test_prefill_tiles_cover_every_row_once():
-    """The prefill attention's query tiles: <= 64 consecutive rows of one sequence each, every
+    """The prefill attention's query tiles: <= 128 consecutive rows of one sequence each, every
     chunk row in exactly one tile with its own position and its sequence's cache base; the
     expanded range spans every key any row attends."""
     from dsv2lite.engine import prefill_tiles
@@ -336,7 +336,7 @@ def test_prefill_tiles_cover_every_row_once():
     t, lo, n = prefill_tiles(seq[s:e], posv[s:e], bases)
     seen = torch.zeros(e - s, dtype=torch.int32)
     for r0, nr, p0, sb in t.tolist():
-        assert 1 <= nr <= 64
+        assert 1 <= nr <= 128
         rows = torch.arange(r0, r0 + nr)
         assert len(set(seq[s:e][rows].tolist())) == 1
         b = int(seq[s + r0])

@@ -964,7 +964,7 @@ def test_lm_head_argmax_matches_gemv_then_argmax(rows):
 def test_mla_prefill_attention_vs_fp32(lens, start):
     """Prefill attention (expanded form, causal) against fp32 torch: rows of several
     sequences (a chunk that may start inside the first sequence: its earlier keys come from
-    the cache), 64-query tiles with partial last tiles."""
+    the cache), 128-query tiles with partial last tiles."""
     from dsv2lite.engine import prefill_tiles
 
     caps = [n + 30 for n in lens]
