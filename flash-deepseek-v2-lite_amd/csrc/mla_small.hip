@@ -403,7 +403,7 @@ __global__ __launch_bounds__(512) void qkva_absorb_kernel(const bf16_t* __restri
   // an L2 hit), then the weight rows
   const int tc = tid & 255;
   const uint4 xv4 = ldg16(xr + tc * 8);
-  const uint4 g4 = ldg16(nw + tc * 8);
+  const uint4 g4 = ldg16((nw ? nw : xr) + tc * 8);  // no norm: a harmless read of x
   uint4 wk[2];
   {
     const bf16_t* wp = w_uk + ((int64_t)(absorb ? h : 0) * 128 + (absorb ? 16 * blk + 2 * wv : 0)) * kLat + lane * 8;
@@ -436,21 +436,25 @@ __global__ __launch_bounds__(512) void qkva_absorb_kernel(const bf16_t* __restri
   }
   pin(xv4.x);
   pin(g4.x);
-  // x' = w * bf16(x * rsqrt(mean x^2 + eps)) -> LDS (fp32)
+  // x' = w * bf16(x * rsqrt(mean x^2 + eps)) (nw == null: x' = x) -> LDS (fp32)
   {
     float f[8], g8[8];
     unpack8(xv4, f);
-    float ss = 0.f;
+    if (nw) {  // uniform
+      float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(f[i], f[i], ss);
-    ss = wave_sum(ss);
-    if (lane == 0) red[wv] = ss;
-    __syncthreads();
-    const float rn = rsqrtf((red[0] + red[1] + red[2] + red[3]) / 2048.f + eps);  // waves 0..3: all of x
-    unpack8(g4, g8);
+      for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(f[i], f[i], ss);
+      ss = wave_sum(ss);
+      if (lane == 0) red[wv] = ss;
+      __syncthreads();
+      const float rn = rsqrtf((red[0] + red[1] + red[2] + red[3]) / 2048.f + eps);  // waves 0..3: all of x
+      unpack8(g4, g8);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) f[i] = rbf(g8[i] * rbf(f[i] * rn));
+    }
     if (tid < 256) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) xl[tid * 8 + i] = rbf(g8[i] * rbf(f[i] * rn));
+      for (int i = 0; i < 8; ++i) xl[tid * 8 + i] = f[i];
     }
     __syncthreads();
   }
@@ -500,11 +504,11 @@ extern "C" int dsv2_qkva_absorb_bf16(const void* x, int64_t x_stride, int rows, 
                                      float eps, const void* w_uk, void* qkva, int64_t qkva_stride, float* qlat_part,
                                      const void* cache, const int64_t* base, const int32_t* pos, const int32_t* cap,
                                      void* stream) {
-  DSV2_REQUIRE(x && w_qkva && norm_w && w_uk && qkva && qlat_part && cache && base && pos && cap, DSV2_E_NULL,
+  DSV2_REQUIRE(x && w_qkva && w_uk && qkva && qlat_part && cache && base && pos && cap, DSV2_E_NULL,
                "qkva_absorb: null pointer");
   DSV2_REQUIRE(rows >= 0 && rows <= 65535 && x_stride >= 2048 && qkva_stride >= kQkvRows, DSV2_E_SHAPE,
                "qkva_absorb: bad shape");
-  DSV2_REQUIRE(dsv2_aligned16(x) && x_stride % 8 == 0 && dsv2_aligned16(w_qkva) && dsv2_aligned16(norm_w) &&
+  DSV2_REQUIRE(dsv2_aligned16(x) && x_stride % 8 == 0 && dsv2_aligned16(w_qkva) && (!norm_w || dsv2_aligned16(norm_w)) &&
                    dsv2_aligned16(w_uk) && dsv2_aligned16(cache) && dsv2_aligned16(qkva) && qkva_stride % 8 == 0 &&
                    dsv2_aligned16(qlat_part),
                DSV2_E_ALIGN, "qkva_absorb: alignment");

@@ -65,8 +65,9 @@ def plan_splits(rows: int, max_ctx: int, target_wgs: int = 256) -> tuple[int, in
     return split, math.ceil(max_ctx / split)
 
 
-# the small family runs the fused one-launch MLA while the cache is this short, like the
-# engine (dsv2lite.engine.FUSED_MLA_MAX_CTX); longer caches take the split-KV decode
+# the small family runs the absorb path (dsv2_qkva_absorb_bf16 + dsv2_mla_attend_parts) while
+# the cache is this short, like the engine (dsv2lite.engine.FUSED_MLA_MAX_CTX); longer caches
+# take the split-KV decode
 FUSED_MAX_CTX = 2048
 
 
@@ -81,6 +82,7 @@ class AttentionDecodeWorkspace:
     cap: torch.Tensor      # [B] int32
     status: torch.Tensor   # [1] int32: DSV2_DEVERR_* bits of every call so far
     qkva: torch.Tensor     # [B, 3648]
+    qlat_part: torch.Tensor  # [B, 16, 8, 512] fp32: partial absorbed queries (small family)
     q: torch.Tensor        # [B, 16, 576]
     split: int
     nsplit: int
@@ -100,7 +102,8 @@ def _workspace(packed: AttentionPackedWeights, dev: torch.device, B: int, L: int
         split, nsplit = plan_splits(B, L)
         ws = AttentionDecodeWorkspace(
             pos=e(B, dt=torch.int32), base=e(B, dt=torch.int64), cap=e(B, dt=torch.int32),
-            status=torch.zeros(1, dtype=torch.int32, device=dev), qkva=e(B, QKVA), q=e(B, NH, ROW), split=split,
+            status=torch.zeros(1, dtype=torch.int32, device=dev), qkva=e(B, QKVA),
+            qlat_part=e(B, NH, NOPE // 16, LAT, dt=torch.float32), q=e(B, NH, ROW), split=split,
             nsplit=nsplit, part_o=e(B, nsplit, NH, LAT, dt=torch.float32), part_ml=e(B, nsplit, NH, 2, dt=torch.float32),
             olat=e(B, NH, LAT), attn=e(B, HID), out=e(B, 1, HID))
         cache[key] = ws
@@ -148,12 +151,16 @@ def _attention_decode(family: str, hidden_states, cos, sin, position_ids, cache_
     P = lambda t: t.data_ptr()  # noqa: E731
     call("dsv2_fill_positions", P(cache_position), P(ws.pos), P(ws.base), P(ws.cap), L, B, st)
     if family == "small":
-        call("dsv2_gemv_bf16", P(x), HID, B, HID, P(packed.w_qkva), QKVA, None, 0.0, None, 0, P(ws.qkva), QKVA, 0, st)
         if L <= FUSED_MAX_CTX:
-            call("dsv2_mla_fused", P(ws.qkva), QKVA, B, P(ws.pos), P(ws.base), P(ws.cap), P(packed.kv_norm_weight),
-                 packed.kv_norm_eps, P(cos2), P(sin2), max_pos, P(packed.w_ukt), P(packed.w_uv), P(key_cache),
-                 float(softmax_scale), P(attn2), HID, P(ws.status), st)
+            # the engine's default small-batch MLA: the projection also forms the absorbed query
+            call("dsv2_qkva_absorb_bf16", P(x), HID, B, P(packed.w_qkva), None, 0.0, P(packed.w_uk), P(ws.qkva), QKVA,
+                 P(ws.qlat_part), P(key_cache), P(ws.base), P(ws.pos), P(ws.cap), st)
+            call("dsv2_mla_attend_parts", P(ws.qkva), QKVA, B, P(ws.pos), P(ws.base), P(ws.cap),
+                 P(packed.kv_norm_weight), packed.kv_norm_eps, P(cos2), P(sin2), max_pos, P(ws.qlat_part),
+                 P(packed.w_uv), P(key_cache), float(softmax_scale), P(attn2), HID, P(ws.status), st)
         else:
+            call("dsv2_gemv_bf16", P(x), HID, B, HID, P(packed.w_qkva), QKVA, None, 0.0, None, 0, P(ws.qkva), QKVA, 0,
+                 st)
             call("dsv2_mla_prepare", P(ws.qkva), QKVA, B, P(ws.pos), P(ws.base), P(ws.cap), P(packed.kv_norm_weight),
                  packed.kv_norm_eps, P(cos2), P(sin2), max_pos, P(packed.w_ukt), P(key_cache), P(ws.q), P(ws.status),
                  st)

@@ -1,7 +1,7 @@
-"""Absorbed-MLA decode attention, small family: GEMV q/kv_a and o projections around
-the one-launch fused MLA kernel (W_UK absorption, kv-norm + RoPE + cache write,
-softmax over the cached rows, W_UV) while the cache is at most 2048 tokens, else
-prepare + split-KV decode + combine with W_UV
+"""Absorbed-MLA decode attention, small family: the q/kv_a projection with the W_UK
+absorption in partial sums, one attention launch (kv-norm + RoPE + cache write, softmax over
+the cached rows, W_UV) and the o_proj GEMV while the cache is at most 2048 tokens, else
+GEMV + prepare + split-KV decode + combine with W_UV
 (reference: triton_kernels/attention_decode_small.py:553-674, 782-840, 932-1070).
 Same compressed-cache deviation as attention_decode_batch; batched_attention_decode_q1_triton
 (the expanded-cache attention) is shared with it."""

@@ -227,7 +227,8 @@ int dsv2_mla_spread(const void* qkva, int64_t qkva_stride, int rows, const int32
                     void* out, int64_t out_stride, int32_t* status, void* stream);
 
 /* The q | kv_a projection of rows x [rows, 2048] (row stride x_stride) with the RMSNorm
- * prologue (norm_w, eps), as dsv2_gemv_bf16(x, ..., w_qkva [3648, 2048], 3648, norm_w, eps, ...)
+ * prologue (norm_w, eps; norm_w == NULL: x is used as it is), as
+ * dsv2_gemv_bf16(x, ..., w_qkva [3648, 2048], 3648, norm_w, eps, ...)
  * writes it into qkva [rows, 3648] (row stride qkva_stride), plus the W_UK absorption of its
  * q_nope in partial sums: for head h and block i of its q_nope rows 16i .. 16i+15,
  *   qlat_part[r, h, i, c] = sum_{d in block i} w_uk[h, d, c] * qkva[r, h*192 + d]   (fp32),

@@ -402,9 +402,9 @@ def test_batched_attention_decode_q1_expanded_vs_fp32(B, H, L, pos, Dq, Dv):
 # --------------------------------------------------------------------------- capacity guard (C ABI)
 def test_mla_kernels_never_touch_another_rows_slots():
     """Row 0 at pos == cap (full), row 1 with room.  The split-KV path (prepare + decode +
-    combine) and the fused kernel must: write nothing for row 0, write row 1's slot, flag
-    the status, and read nothing outside a row's own slots (the slots after row 0's are NaN,
-    so any read of them would poison its output)."""
+    combine), the fused kernel and the attention of the absorb path must: write nothing for
+    row 0, write row 1's slot, flag the status, and read nothing outside a row's own slots
+    (the slots after row 0's are NaN, so any read of them would poison its output)."""
     from dsv2lite.config import DSV2Config
     from dsv2lite.rope import cos_sin_tables
 
@@ -425,7 +425,10 @@ def test_mla_kernels_never_touch_another_rows_slots():
     cos, sin = cos_sin_tables(cfg, 128, device=DEV)
     scale = cfg.softmax_scale
     outs = {}
-    for path in ("split", "fused"):
+    # the absorb path's partial absorbed queries, formed here from qkva (8 blocks of 16 q_nope rows)
+    qn = c(qkva)[:, :3072].view(B, 16, 192)[:, :, :128].reshape(B, 16, 8, 16)
+    parts = torch.einsum("bhid,hidc->bhic", qn, c(w_uk).view(16, 8, 16, 512)).contiguous().to(DEV)
+    for path in ("split", "fused", "absorb"):
         cch = cache.clone()
         status = torch.zeros(1, dtype=torch.int32, device=DEV)
         out = torch.empty(B, 2048, dtype=BF, device=DEV)
@@ -440,9 +443,13 @@ def test_mla_kernels_never_touch_another_rows_slots():
                  32, 4, scale, po.data_ptr(), pm.data_ptr(), st())
             call("dsv2_mla_combine", po.data_ptr(), pm.data_ptr(), pos.data_ptr(), capd.data_ptr(), B, 32, 4,
                  w_uv.data_ptr(), out.data_ptr(), 2048, st())
-        else:
+        elif path == "fused":
             call("dsv2_mla_fused", qkva.data_ptr(), 3648, B, pos.data_ptr(), base.data_ptr(), capd.data_ptr(),
                  kvw.data_ptr(), 1e-6, cos.data_ptr(), sin.data_ptr(), 128, w_ukt.data_ptr(), w_uv.data_ptr(),
+                 cch.data_ptr(), scale, out.data_ptr(), 2048, status.data_ptr(), st())
+        else:
+            call("dsv2_mla_attend_parts", qkva.data_ptr(), 3648, B, pos.data_ptr(), base.data_ptr(), capd.data_ptr(),
+                 kvw.data_ptr(), 1e-6, cos.data_ptr(), sin.data_ptr(), 128, parts.data_ptr(), w_uv.data_ptr(),
                  cch.data_ptr(), scale, out.data_ptr(), 2048, status.data_ptr(), st())
         torch.cuda.synchronize()
         assert status.item() == 1, path
@@ -450,5 +457,6 @@ def test_mla_kernels_never_touch_another_rows_slots():
         assert changed == [48 + 33], (path, changed)  # only row 1's slot 33
         assert torch.isfinite(out.float()).all(), path
         outs[path] = out
-    # row 1 (within capacity) agrees between the two paths; row 0 attended its 40 rows only
+    # row 1 (within capacity) agrees between the paths; row 0 attended its 40 rows only
     assert rel_err(c(outs["fused"][1]), c(outs["split"][1])) < 2e-2
+    assert rel_err(c(outs["absorb"][1]), c(outs["split"][1])) < 2e-2
