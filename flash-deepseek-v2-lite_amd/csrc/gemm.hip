@@ -443,7 +443,7 @@ __global__ __launch_bounds__(RWV * 128) void gemm_dma_kernel(const GemmArgs a, c
   constexpr int LW = TM / (8 * NW), LL = (TM + TN) / (8 * NW);  // ring loads per wave per chunk: weights, all
   constexpr int XM = WM / 16, XN = WN / 16;         // MFMA blocks per wave
   constexpr int FPW = SWIGLU ? TM / 2 : TM;  // output features per workgroup
-  static_assert(LL <= 8 && XM <= 4 && XN <= 4, "local arrays have literal sizes");
+  static_assert(LL <= 8 && XM <= 4 && XN <= 8, "local arrays have literal sizes");
   // grouped: items j = tile * nfb + fb over the live tiles (the shared halves' tiles, then the
   // table's), consecutive items round-robin over the XCDs (keeping all token tiles of a
   // feature block on one XCD measured slower: fewer feature blocks than XCD slots balance)
@@ -524,7 +524,7 @@ __global__ __launch_bounds__(RWV * 128) void gemm_dma_kernel(const GemmArgs a, c
         __builtin_amdgcn_global_load_lds(src[j] + cc * 64,
                                          (__attribute__((address_space(3))) void*)(lds + buf * SB + dst[j]), 16, 0, 0);
     };
-    floatx4_t acc[4][4];
+    floatx4_t acc[4][8];
 #pragma unroll
     for (int x = 0; x < XM; ++x)
 #pragma unroll
@@ -547,7 +547,7 @@ __global__ __launch_bounds__(RWV * 128) void gemm_dma_kernel(const GemmArgs a, c
         const uint8_t* st = lds + i * SB;
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-          bf16x8_t af[4], bfr[4];
+          bf16x8_t af[4], bfr[8];
           const int pc = 4 * s + kg;
 #pragma unroll
           for (int x = 0; x < XM; ++x) {
@@ -611,29 +611,31 @@ __global__ __launch_bounds__(RWV * 128) void gemm_dma_kernel(const GemmArgs a, c
   }
 }
 
-// grouped: max_tiles entries of a tile table of 64 (big: 128) tokens; dense: a.rows tokens.
-// big: 256 weight rows x 128 tokens per 8-wave workgroup (each wave 64 x 64, 4 x 4 MFMA
-// blocks), three 48 KB stages, one workgroup per CU -- for expert tiles of hundreds of tokens
-// (prefill), where the 64 x 64 shape re-reads each weight chunk once per 64 tokens and
-// issues one MFMA per 2 KB of LDS reads (C3 prefill 7.1 s -> 6.0 s with 128 x 128 per 4-wave
-// workgroup, 5.3 s with 256 x 128 per 8 waves).
-constexpr int kBigRwv = 4, kBigStages = 3;  // big: waves along the weight rows, ring stages
+// grouped: max_tiles entries of a tile table of 64 (big: 256) tokens; dense: a.rows tokens.
+// big: 256 weight rows x 256 tokens per 8-wave workgroup (each wave 64 x 128, 4 x 8 MFMA
+// blocks), two 64 KB stages (a third does not fit the 160 KB of LDS), one workgroup per CU
+// -- for expert tiles of hundreds of tokens (prefill), where the 64 x 64 shape re-reads each
+// weight chunk once per 64 tokens and issues one MFMA per 2 KB of LDS reads (C3 prefill
+// 7.1 s -> 6.0 s with 128 x 128 per 4-wave workgroup, 5.3 s with 256 x 128 per 8 waves and
+// three 48 KB stages; with the later attention changes 4.76 s -> 4.43 s with 256 x 256).
+constexpr int kBigRwv = 4, kBigStages = 2, kBigWn = 128;  // big: waves along the weight rows, ring stages,
+constexpr int kBigTokens = 2 * kBigWn;                    // tokens per wave; tokens per workgroup
 constexpr int kBigRows = 64 * kBigRwv;                 // weight rows per big workgroup
 static void launch_dma(const GemmArgs& a, bool swiglu, hipStream_t st, int max_tiles = 0, bool big = false) {
   DmaShape sh;
-  const int tn = big ? 128 : 64;
+  const int tn = big ? kBigTokens : 64;
   // plain: a last feature block past N (N % 64 == 0) repeats row N-1 and stores nothing there
   sh.nfb = swiglu ? a.N / (big ? kBigRows / 2 : 32) : (a.N + (big ? kBigRows : 64) - 1) / (big ? kBigRows : 64);
   sh.tiles = a.tiles ? max_tiles : (a.rows + tn - 1) / tn;
   // grouped: resident workgroups (two per CU, big: one) looping over the live items
   sh.nwg = a.tiles ? (big ? kDmaGroupedWgs / 2 : kDmaGroupedWgs) : (sh.nfb * sh.tiles + 7) / 8 * 8;
   if (big) {
-    constexpr int lds = kBigStages * (kBigRows + 128) * 128;
+    constexpr int lds = kBigStages * (kBigRows + kBigTokens) * 128;
     if (swiglu)
-      hipLaunchKernelGGL((gemm_dma_kernel<true, 64, 64, kBigStages, kBigRwv>), dim3(sh.nwg), dim3(128 * kBigRwv), lds,
+      hipLaunchKernelGGL((gemm_dma_kernel<true, 64, kBigWn, kBigStages, kBigRwv>), dim3(sh.nwg), dim3(128 * kBigRwv), lds,
                          st, a, sh);
     else
-      hipLaunchKernelGGL((gemm_dma_kernel<false, 64, 64, kBigStages, kBigRwv>), dim3(sh.nwg), dim3(128 * kBigRwv),
+      hipLaunchKernelGGL((gemm_dma_kernel<false, 64, kBigWn, kBigStages, kBigRwv>), dim3(sh.nwg), dim3(128 * kBigRwv),
                          lds, st, a, sh);
     return;
   }
@@ -994,8 +996,8 @@ extern "C" int dsv2_moe_grouped_gateup(const void* xn, const int32_t* sorted_rou
   DSV2_REQUIRE(xn && sorted_routes && tiles && num_tiles && w_gate_up && hsorted, DSV2_E_NULL,
                "moe_grouped_gateup: null pointer");
   DSV2_REQUIRE(max_tiles >= 0 && max_tiles <= 65535 && inter > 0 && inter % 16 == 0 &&
-                   (tile_tokens == 16 || tile_tokens == 32 || tile_tokens == 64 || tile_tokens == 128),
-               DSV2_E_SHAPE, "moe_grouped_gateup: bad shape (inter %% 16, tile_tokens in {16,32,64,128})");
+                   (tile_tokens == 16 || tile_tokens == 32 || tile_tokens == 64 || tile_tokens == kBigTokens),
+               DSV2_E_SHAPE, "moe_grouped_gateup: bad shape (inter %% 16, tile_tokens in {16,32,64,256})");
   DSV2_REQUIRE(dsv2_aligned16(xn) && dsv2_aligned16(w_gate_up) && dsv2_aligned16(tiles), DSV2_E_ALIGN,
                "moe_grouped_gateup: alignment");
   if (max_tiles == 0) return DSV2_OK;
@@ -1014,13 +1016,13 @@ extern "C" int dsv2_moe_grouped_gateup(const void* xn, const int32_t* sorted_rou
   a.Y = hsorted;
   a.ys = inter;
   a.yg = 0;
-  if ((tile_tokens == 64 && inter % 32 == 0) || (tile_tokens == 128 && inter % (kBigRows / 2) == 0)) {
-    // 64- and 128-token tiles on the direct-to-LDS ring (reference workload, 6 experts x 256
+  if ((tile_tokens == 64 && inter % 32 == 0) || (tile_tokens == kBigTokens && inter % (kBigRows / 2) == 0)) {
+    // 64- and 256-token tiles on the direct-to-LDS ring (reference workload, 6 experts x 256
     // tokens: 45 us vs 71 us for the token-rows-in-LDS shape; x 64 tokens: 26.0 vs 26.8 us)
-    launch_dma(a, true, (hipStream_t)stream, max_tiles, tile_tokens == 128);
+    launch_dma(a, true, (hipStream_t)stream, max_tiles, tile_tokens == kBigTokens);
     return dsv2_launch_status("moe_grouped_gateup");
   }
-  DSV2_REQUIRE(tile_tokens != 128, DSV2_E_SHAPE, "moe_grouped_gateup: 128-token tiles need inter %% %d", kBigRows / 2);
+  DSV2_REQUIRE(tile_tokens != kBigTokens, DSV2_E_SHAPE, "moe_grouped_gateup: 256-token tiles need inter %% %d", kBigRows / 2);
   return launch_gemm(a, tile_tb(tile_tokens), true, max_tiles, (hipStream_t)stream);
 }
 
@@ -1031,9 +1033,9 @@ extern "C" int dsv2_moe_grouped_gateup_shared(const void* xn, int rows, const in
   DSV2_REQUIRE(xn && sorted_routes && tiles && num_tiles && w_gate_up && sh_gate_up && hsorted && shared_out,
                DSV2_E_NULL, "moe_grouped_gateup_shared: null pointer");
   DSV2_REQUIRE(rows >= 0 && max_tiles >= 0 && max_tiles <= 65535 && inter > 0 && inter % 64 == 0 &&
-                   (tile_tokens == 16 || tile_tokens == 32 || tile_tokens == 64 || tile_tokens == 128) &&
+                   (tile_tokens == 16 || tile_tokens == 32 || tile_tokens == 64 || tile_tokens == kBigTokens) &&
                    (tile_tokens >= 64 || (int64_t)max_tiles + 2 * ((rows + tile_tokens - 1) / tile_tokens) <= 65535),
-               DSV2_E_SHAPE, "moe_grouped_gateup_shared: bad shape (inter %% 64, tile_tokens in {16,32,64,128})");
+               DSV2_E_SHAPE, "moe_grouped_gateup_shared: bad shape (inter %% 64, tile_tokens in {16,32,64,256})");
   DSV2_REQUIRE(dsv2_aligned16(xn) && dsv2_aligned16(w_gate_up) && dsv2_aligned16(sh_gate_up) &&
                    dsv2_aligned16(tiles) && dsv2_aligned16(shared_out),
                DSV2_E_ALIGN, "moe_grouped_gateup_shared: alignment");
@@ -1063,7 +1065,7 @@ extern "C" int dsv2_moe_grouped_gateup_shared(const void* xn, int rows, const in
   a.y2s = 2 * inter;
   a.y2g = inter;
   if (tile_tokens >= 64) {
-    launch_dma(a, true, (hipStream_t)stream, max_tiles, tile_tokens == 128);
+    launch_dma(a, true, (hipStream_t)stream, max_tiles, tile_tokens == kBigTokens);
     return dsv2_launch_status("moe_grouped_gateup_shared");
   }
   return launch_gemm(a, tile_tb(tile_tokens), true, 2 * a.s_tiles + max_tiles, (hipStream_t)stream);
@@ -1076,9 +1078,9 @@ extern "C" int dsv2_moe_grouped_down_shared(const void* hsorted, int rows, const
   DSV2_REQUIRE(hsorted && tiles && num_tiles && w_down && shared_mid && sh_down && ysorted && shared_parts,
                DSV2_E_NULL, "moe_grouped_down_shared: null pointer");
   DSV2_REQUIRE(rows >= 0 && max_tiles >= 0 && max_tiles <= 65535 && inter > 0 && inter % 64 == 0 &&
-                   (tile_tokens == 16 || tile_tokens == 32 || tile_tokens == 64 || tile_tokens == 128) &&
+                   (tile_tokens == 16 || tile_tokens == 32 || tile_tokens == 64 || tile_tokens == kBigTokens) &&
                    (tile_tokens >= 64 || (int64_t)max_tiles + 2 * ((rows + tile_tokens - 1) / tile_tokens) <= 65535),
-               DSV2_E_SHAPE, "moe_grouped_down_shared: bad shape (inter %% 64, tile_tokens in {16,32,64,128})");
+               DSV2_E_SHAPE, "moe_grouped_down_shared: bad shape (inter %% 64, tile_tokens in {16,32,64,256})");
   DSV2_REQUIRE(dsv2_aligned16(hsorted) && dsv2_aligned16(w_down) && dsv2_aligned16(shared_mid) &&
                    dsv2_aligned16(sh_down) && dsv2_aligned16(tiles) && dsv2_aligned16(ysorted) &&
                    dsv2_aligned16(shared_parts),
@@ -1108,7 +1110,7 @@ extern "C" int dsv2_moe_grouped_down_shared(const void* hsorted, int rows, const
   a.y2s = 2048;
   a.y2g = (int64_t)rows * 2048;
   if (tile_tokens >= 64) {
-    launch_dma(a, false, (hipStream_t)stream, max_tiles, tile_tokens == 128);
+    launch_dma(a, false, (hipStream_t)stream, max_tiles, tile_tokens == kBigTokens);
     return dsv2_launch_status("moe_grouped_down_shared");
   }
   return launch_gemm(a, tile_tb(tile_tokens), false, 2 * a.s_tiles + max_tiles, (hipStream_t)stream);
@@ -1119,7 +1121,7 @@ extern "C" int dsv2_moe_grouped_down(const void* hsorted, const int32_t* tiles, 
                                      void* stream) {
   DSV2_REQUIRE(hsorted && tiles && num_tiles && w_down && ysorted, DSV2_E_NULL, "moe_grouped_down: null pointer");
   DSV2_REQUIRE(max_tiles >= 0 && max_tiles <= 65535 && inter > 0 && inter % 64 == 0 &&
-                   (tile_tokens == 16 || tile_tokens == 32 || tile_tokens == 64 || tile_tokens == 128),
+                   (tile_tokens == 16 || tile_tokens == 32 || tile_tokens == 64 || tile_tokens == kBigTokens),
                DSV2_E_SHAPE, "moe_grouped_down: bad shape");
   DSV2_REQUIRE(dsv2_aligned16(hsorted) && dsv2_aligned16(w_down) && dsv2_aligned16(tiles) && inter % 8 == 0,
                DSV2_E_ALIGN, "moe_grouped_down: alignment");
@@ -1141,7 +1143,7 @@ extern "C" int dsv2_moe_grouped_down(const void* hsorted, const int32_t* tiles, 
   a.yg = 0;
   if (tile_tokens >= 64) {
     // 6 experts x 256 tokens: 24 us vs 35 us; x 64 tokens: 12.0 vs 16.3 us
-    launch_dma(a, false, (hipStream_t)stream, max_tiles, tile_tokens == 128);
+    launch_dma(a, false, (hipStream_t)stream, max_tiles, tile_tokens == kBigTokens);
     return dsv2_launch_status("moe_grouped_down");
   }
   return launch_gemm(a, tile_tb(tile_tokens), false, max_tiles, (hipStream_t)stream);

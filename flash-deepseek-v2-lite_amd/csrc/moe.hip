@@ -840,7 +840,7 @@ __global__ __launch_bounds__(1024) void bucket_kernel(const int32_t* __restrict_
 extern "C" int dsv2_moe_bucket(const int32_t* ids, int rows, int tile_tokens, int32_t* sorted_routes,
                                int32_t* route_pos, int32_t* tiles, int32_t* num_tiles, void* stream) {
   DSV2_REQUIRE(ids && sorted_routes && route_pos && tiles && num_tiles, DSV2_E_NULL, "moe_bucket: null pointer");
-  DSV2_REQUIRE(rows >= 0 && rows * kTopK <= kMaxRoutes && tile_tokens >= 1 && tile_tokens <= 128, DSV2_E_SHAPE,
+  DSV2_REQUIRE(rows >= 0 && rows * kTopK <= kMaxRoutes && tile_tokens >= 1 && tile_tokens <= 256, DSV2_E_SHAPE,
                "moe_bucket: rows*6 must be <= %d (got %d)", kMaxRoutes, rows * kTopK);
   DSV2_REQUIRE(dsv2_aligned16(tiles), DSV2_E_ALIGN, "moe_bucket: tiles must be 16-byte aligned");
   hipLaunchKernelGGL(bucket_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, ids, rows * kTopK, tile_tokens,

@@ -43,25 +43,32 @@ FUSED_MLA_MAX_CTX = 2048
 SPLIT_ROUTER_MAX_ROWS = 64
 # from this many rows (prefill chunks) the router runs as RMSNorm + an MFMA logits GEMM + top-6
 GEMM_ROUTER_MIN_ROWS = 1024
-# grouped MoE: above this many routes per expert the 128-token tiles (128 x 128 ring GEMM;
-# the reference workload at bsz=256, 256 routes per expert, is 2% faster on 64-token tiles)
-BIG_TILE_LOAD = 384
+# grouped MoE: from this many routes in a launch the 256-token tiles (256 x 256 ring GEMM, one
+# MFMA per 384 B of LDS reads) beat the 64-token ones.  The crossover follows the launch's
+# routes rather than their spread over the experts: measured on MI355X, routed gate_up + down,
+# uniform routing (all 64 experts) 4096 routes 297 vs 321 us (64 vs 256 tokens), 6144 routes
+# 421 vs 358 us, 49152 routes 2264 vs 1155 us; every row on the same 6 experts 3072 routes
+# 109 vs 120 us, 6144 routes 213 vs 194 us
+BIG_TILE_ROUTES = 5120
 
 
 def moe_tile_tokens(rows: int, n_experts: int = 64, top_k: int = 6) -> int:
     """Token tile of the expert-grouped MoE GEMMs before any routing has been seen, from the
     mean routes per expert under uniform routing (see tile_tokens_for_load)."""
-    return tile_tokens_for_load(rows * top_k / n_experts)
+    return tile_tokens_for_load(rows * top_k / n_experts, rows * top_k)
 
 
-def tile_tokens_for_load(load: float) -> int:
-    """Token tile for a mean of `load` routes per routed expert.  Measured on MI355X, whole
+def tile_tokens_for_load(load: float, routes: int = 0) -> int:
+    """Token tile for a mean of `load` routes per routed expert in a launch of `routes` routes
+    (256 from BIG_TILE_ROUTES, whatever the spread).  Measured on MI355X, whole
     decode step (the 64-token tiles run on the direct-to-LDS ring GEMM, every size with the
     shared experts folded in where shared_in_grouped allows): bsz=64 random prompts (about
     7 routes per expert) 8.71k tok/s with 32-token tiles vs 8.58k with 16 and 8.13k with 64;
     bsz=256 (about 25) 22.42k with 64 vs 21.79k with 32; every row on the same 6 experts
     (64 or 256 routes per expert) 64."""
-    return 16 if load <= 3 else (32 if load <= 12 else (64 if load <= BIG_TILE_LOAD else 128))
+    if routes >= BIG_TILE_ROUTES:
+        return 256
+    return 16 if load <= 3 else (32 if load <= 12 else 64)
 
 
 def shared_in_grouped(rows: int, tile_tokens: int) -> bool:
@@ -155,10 +162,10 @@ class RowBuffers:
 
 
     def set_tile_tokens(self, tile_tokens: int) -> None:
-        """Token tile of the grouped MoE launches (16, 32, 64 or 128); the tile table was
+        """Token tile of the grouped MoE launches (16, 32, 64 or 256); the tile table was
         sized for the smallest."""
-        if tile_tokens not in (16, 32, 64, 128):
-            raise ValueError(f"tile_tokens must be 16, 32, 64 or 128, got {tile_tokens}")
+        if tile_tokens not in (16, 32, 64, 256):
+            raise ValueError(f"tile_tokens must be 16, 32, 64 or 256, got {tile_tokens}")
         self.tile_tokens = tile_tokens
         self.max_tiles = math.ceil(self._routes / tile_tokens) + self._n_experts
 
@@ -180,7 +187,7 @@ class DecodeEngine:
                  max_prefill_rows: int = 8192, device="cuda", mla_path: str = "absorb", moe_tile: int | None = None,
                  expert_dtype: str = "bf16"):
         """capacities: cache tokens of each row (slot).  moe_tile (batch family): fix the
-        grouped MoE token tile (16, 32, 64 or 128) instead of choosing it from the routing of one
+        grouped MoE token tile (16, 32, 64 or 256) instead of choosing it from the routing of one
         eager step at capture -- for a serving loop whose batch changes under one graph.
         expert_dtype "fp8" (small family): the decode step reads the e4m3 expert weights of
         quantize_experts_fp8 (prefill keeps the bf16 kernels on the dequantized weights)."""
@@ -593,7 +600,7 @@ class DecodeEngine:
         self.step(record=rec)
         self.restore(snap)
         loads = sorted(routing_load(r[2], self.cfg.n_experts) for r in rec if r[0] == "router")
-        tile = tile_tokens_for_load(loads[len(loads) // 2]) if loads else self.buf.tile_tokens
+        tile = tile_tokens_for_load(loads[len(loads) // 2], self.buf._routes) if loads else self.buf.tile_tokens
         self.buf.set_tile_tokens(tile)
         self._moe_tiles_tuned = True
         return tile

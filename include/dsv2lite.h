@@ -355,14 +355,14 @@ int dsv2_moe_route_down_fp8(const void* hbuf, int rows, const int32_t* ids, cons
  *   sorted_routes[p] = route index r*6+s in expert order, stable in r;
  *   route_pos[r*6+s] = p;  tiles[t] = {expert, first slot, count<=tile_tokens, 0} (int32x4);
  *   num_tiles[0] = number of tiles (<= rows*6/tile_tokens + 64).  rows*6 <= 49152 (8192 rows),
- *   1 <= tile_tokens <= 128.
+ *   1 <= tile_tokens <= 256.
  * Replaces _build_route_indices_kernel + _build_route_blocks_kernel (moe_batch.py:95-148). */
 int dsv2_moe_bucket(const int32_t* ids, int rows, int tile_tokens, int32_t* sorted_routes, int32_t* route_pos,
                     int32_t* tiles, int32_t* num_tiles, void* stream);
 
 /* Expert-grouped gate_up + SwiGLU on bf16 MFMA over the tiles of dsv2_moe_bucket:
  *   hsorted[p, :inter] for p in tile = SwiGLU(xn[sorted_routes[p]/6] . W_e^T).
- * tile_tokens 16, 32, 64 or 128 (128: inter % 64 == 0).
+ * tile_tokens 16, 32, 64 or 256 (256: inter % 128 == 0).
  * Grid is sized by max_tiles; tiles >= num_tiles[0] exit.  Replaces
  * _grouped_gate_up_swiglu_kernel (moe_batch.py:152-234). */
 int dsv2_moe_grouped_gateup(const void* xn, const int32_t* sorted_routes, const int32_t* tiles,
@@ -373,7 +373,7 @@ int dsv2_moe_grouped_gateup(const void* xn, const int32_t* sorted_routes, const 
  * shared_out[t, h*inter + i] = SwiGLU(xn[t] . gate/up rows h*inter + i of sh_gate_up)
  * for t < rows, h = 0, 1 (sh_gate_up [2*2*inter, 2048]: gate rows, then up rows), i.e. the
  * dense shared gate_up of dsv2_gemm_bf16 with DSV2_LINEAR_SWIGLU.  The tile table must come
- * from dsv2_moe_bucket with the same tile_tokens (16, 32, 64 or 128).  Replaces _grouped_gate_up_swiglu_kernel
+ * from dsv2_moe_bucket with the same tile_tokens (16, 32, 64 or 256).  Replaces _grouped_gate_up_swiglu_kernel
  * (moe_batch.py:152-234) and the shared MLP's gate_proj / up_proj + SiLU-mul (src/run.py:341-351). */
 int dsv2_moe_grouped_gateup_shared(const void* xn, int rows, const int32_t* sorted_routes, const int32_t* tiles,
                                    const int32_t* num_tiles, int max_tiles, int tile_tokens, const void* w_gate_up,

@@ -104,6 +104,8 @@ def test_moe_tile_choice_and_cache_layout():
     assert 6 < routing_load(uniform) < 10 and tile_tokens_for_load(routing_load(uniform)) == 32
     assert routing_load(same) == 64 and tile_tokens_for_load(routing_load(same)) == 64
     assert tile_tokens_for_load(24.5) == 64 and tile_tokens_for_load(2.0) == 16
+    assert tile_tokens_for_load(384, 2304) == 64 and tile_tokens_for_load(96, 6144) == 256
+    assert moe_tile_tokens(853) == 64 and moe_tile_tokens(854) == 256 and moe_tile_tokens(8192) == 256
     from dsv2lite.engine import shared_in_grouped
 
     assert shared_in_grouped(64, 16) and shared_in_grouped(64, 64) and shared_in_grouped(256, 64)

@@ -403,8 +403,8 @@ def test_moe_batch_family_grouped(rows):
 
 @pytest.mark.parametrize("rows,replicated", [(64, True), (200, True), (150, False)])
 def test_moe_grouped_tile_sizes(rows, replicated):
-    """Bucketing + grouped gate_up / down + combine with 16-, 32-, 64- and 128-token expert
-    tiles (64, 128: the direct-to-LDS ring GEMM; replicated rows give full and partial tiles,
+    """Bucketing + grouped gate_up / down + combine with 16-, 32-, 64- and 256-token expert
+    tiles (64, 256: the direct-to-LDS ring GEMM; replicated rows give full and partial tiles,
     random routing mostly near-empty ones) against the oracle on a subset of rows."""
     gu, dn, sgu, sdn = _moe_layer(60)
     xn = rnd(rows, 2048, seed=61)
@@ -417,7 +417,7 @@ def test_moe_grouped_tile_sizes(rows, replicated):
     ids32, wd = ids.to(torch.int32).to(DEV), w.to(DEV)
     R = rows * 6
     outs = {}
-    for tt in (16, 32, 64, 128):
+    for tt in (16, 32, 64, 256):
         max_tiles = math.ceil(R / tt) + 64
         srt = torch.empty(R, dtype=torch.int32, device=DEV)
         rpos = torch.empty(R, dtype=torch.int32, device=DEV)
@@ -445,7 +445,7 @@ def test_moe_grouped_tile_sizes(rows, replicated):
 
 @pytest.mark.parametrize("rows,replicated,tt", [(64, True, 64), (130, False, 64), (64, False, 16), (37, False, 16),
                                                 (200, False, 32), (130, True, 32), (1024, False, 64),
-                                                (300, True, 128), (1024, False, 128)])
+                                                (300, True, 256), (1024, False, 256)])
 def test_moe_grouped_gateup_with_shared(rows, replicated, tt):
     """The grouped gate_up / down with the shared halves in the same launches (16-, 32- and
     64-token tiles): routed rows equal the plain grouped launches' bit for bit, the shared
