@@ -421,8 +421,17 @@ constexpr int kDmaGroupedWgs = 512;  // 256 CUs x 2 (64 KB of LDS each)
 // outstanding, leaving the LDS/scalar (15) and export (7) counters unconstrained
 constexpr int vmcnt_only(int n) { return (n & 0xf) | (0x7 << 4) | (0xf << 8) | (((n >> 4) & 3) << 14); }
 
+// xcd_blocked (the prefill shape): the work items, token-tile-major (all feature blocks of a
+// token tile, then the next tile, an expert's tiles in a row), are cut into 8 contiguous
+// ranges, one per XCD (workgroup i runs on XCD i % 8), and every item reads its K chunks in
+// order.  The ~32 items an XCD runs at once then share each token chunk among the tile's
+// feature blocks and each weight chunk among the expert's tiles in that XCD's L2; the decode
+// order instead puts all token tiles of a feature block on one XCD, which at prefill sizes
+// (token rows 3x the weight bytes) re-reads every token row from HBM on every XCD
+// (8192 x 2048 x 2048: 80.4 -> 74.2 us; C3 prefill 4.27 -> 4.15 s).
 struct DmaShape {
   int tiles, nwg, nfb;
+  int xcd_blocked;
 };
 
 
@@ -433,17 +442,23 @@ struct DmaShape {
 // the live (tile, feature block) items only, so the table's dead tiles cost no workgroup
 // launches; token rows are gathered through slot_row and the tile's expert selects the
 // weights.
-template <bool SWIGLU, int WM = 32, int WN = 32, int ST = kDmaStages, int RWV = 2>
+template <bool SWIGLU, int WM = 32, int WN = 32, int ST = kDmaStages, int RWV = 2, int KC = 64>
 __global__ __launch_bounds__(RWV * 128) void gemm_dma_kernel(const GemmArgs a, const DmaShape sh) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // ST stages of SB bytes
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, li = lane & 15, kg = lane >> 4;
   constexpr int NW = 2 * RWV;                // waves: RWV along the weight rows x 2 along the tokens
   constexpr int TM = RWV * WM, TN = 2 * WN;  // weight rows, tokens per workgroup
-  constexpr int SB = (TM + TN) * 128;      // stage: TM weight rows, then TN token rows, 128 B each
-  constexpr int LW = TM / (8 * NW), LL = (TM + TN) / (8 * NW);  // ring loads per wave per chunk: weights, all
-  constexpr int XM = WM / 16, XN = WN / 16;         // MFMA blocks per wave
+  constexpr int RB = 2 * KC, PR = KC / 8;    // a chunk's bytes per row, its 16 B pieces per row
+  constexpr int RPL = 64 / PR;               // rows per ring load (64 lanes x 16 B)
+  constexpr int SB = (TM + TN) * RB;         // stage: TM weight rows, then TN token rows
+  constexpr int LW = TM / (RPL * NW), LL = (TM + TN) / (RPL * NW);  // ring loads per wave per chunk: weights, all
+  constexpr int XM = WM / 16, XN = WN / 16;  // MFMA blocks per wave
   constexpr int FPW = SWIGLU ? TM / 2 : TM;  // output features per workgroup
   static_assert(LL <= 8 && XM <= 4 && XN <= 8, "local arrays have literal sizes");
+  static_assert(KC == 64 || KC == 32, "64- or 32-wide K chunks");
+  // piece p of row r sits in slot p ^ swz(r): the 16 rows one MFMA fragment reads hit
+  // distinct banks in every group of 8 lanes
+  auto swz = [](int r) { return PR == 8 ? (r & 7) : ((r >> 1) & 3); };
   // grouped: items j = tile * nfb + fb over the live tiles (the shared halves' tiles, then the
   // table's), consecutive items round-robin over the XCDs (keeping all token tiles of a
   // feature block on one XCD measured slower: fewer feature blocks than XCD slots balance)
@@ -453,7 +468,14 @@ __global__ __launch_bounds__(RWV * 128) void gemm_dma_kernel(const GemmArgs a, c
     int fb, g = 0, t0, count;
     bool shared = false;
     if (a.tiles) {
-      const int j = blockIdx.x + it * gridDim.x;
+      int j;
+      if (sh.xcd_blocked) {  // XCD blockIdx % 8 runs items [x * per, (x + 1) * per)
+        const int per = (live * sh.nfb + 7) / 8, jl = blockIdx.x / 8 + it * (gridDim.x / 8);
+        if (jl >= per) break;
+        j = (blockIdx.x % 8) * per + jl;
+      } else {
+        j = blockIdx.x + it * gridDim.x;
+      }
       if (j >= live * sh.nfb) break;
       const int tile = j / sh.nfb;
       fb = j % sh.nfb;
@@ -473,16 +495,16 @@ __global__ __launch_bounds__(RWV * 128) void gemm_dma_kernel(const GemmArgs a, c
       const int per = sh.nwg / 8;
       const int w = (blockIdx.x % 8) * per + blockIdx.x / 8;
       if (w >= sh.nfb * sh.tiles) break;
-      const int tile = w % sh.tiles;
-      fb = w / sh.tiles;
+      const int tile = sh.xcd_blocked ? w / sh.nfb : w % sh.tiles;
+      fb = sh.xcd_blocked ? w % sh.nfb : w / sh.tiles;
       t0 = tile * TN;
       count = min(TN, a.rows - t0);
     }
     const int f0 = fb * FPW;
-    const int K = a.K, nch = K / 64;
-    // this wave's LL ring loads per chunk, 8 rows x 128 B each: weight rows (TM / 4 per wave,
-    // j < LW) then token rows (TN / 4 per wave); lane -> (row r, slot lane & 7), which holds
-    // piece (lane & 7) ^ (r & 7)
+    const int K = a.K, nch = K / KC;
+    // this wave's LL ring loads per chunk, RPL rows x RB bytes each: weight rows (TM / NW per
+    // wave, j < LW) then token rows (TN / NW per wave); lane -> (row r, slot lane % PR), which
+    // holds piece (lane % PR) ^ swz(r)
     const bf16_t* const wbase = shared ? a.W2 + g * a.w2g : a.W + g * a.wg;
     const int64_t wld = shared ? a.w2ld : K;
     const int upoff = shared ? a.w2up : a.N;
@@ -491,8 +513,8 @@ __global__ __launch_bounds__(RWV * 128) void gemm_dma_kernel(const GemmArgs a, c
 #pragma unroll
     for (int j = 0; j < LL; ++j) {
       const bool tok = j >= LW;
-      const int r = (tok ? (TN / NW) * wv + 8 * (j - LW) : (TM / NW) * wv + 8 * j) + (lane >> 3);
-      const int pc = (lane & 7) ^ (r & 7);
+      const int r = (tok ? (TN / NW) * wv + RPL * (j - LW) : (TM / NW) * wv + RPL * j) + lane / PR;
+      const int pc = (lane % PR) ^ swz(r);
       if (tok) {
         const int slot = t0 + (r < count ? r : 0);  // rows past the tile: the tile's first row
         if (shared) {
@@ -506,7 +528,7 @@ __global__ __launch_bounds__(RWV * 128) void gemm_dma_kernel(const GemmArgs a, c
       } else {
         src[j] = wbase + (int64_t)min(f0 + r, a.N - 1) * wld + pc * 8;  // a ragged last block repeats row N-1
       }
-      dst[j] = (tok ? TM * 128 + ((TN / NW) * wv + 8 * (j - LW)) * 128 : ((TM / NW) * wv + 8 * j) * 128);
+      dst[j] = (tok ? TM * RB + ((TN / NW) * wv + RPL * (j - LW)) * RB : ((TM / NW) * wv + RPL * j) * RB);
     }
     // the item's K chunks start at a rotation that spreads the workgroups' concurrent requests
     // over the weight rows' address range instead of one column of 128 B lines (C3 grouped
@@ -515,13 +537,13 @@ __global__ __launch_bounds__(RWV * 128) void gemm_dma_kernel(const GemmArgs a, c
     // tiles of one weight block read its chunks in the same order, so the ones that run
     // together share each chunk's fetch in L2 (a rotation per token tile as well made the
     // reference workload at bsz=256 -- 4 tiles per expert -- 1.5x slower)
-    const int rot = (int)((unsigned)(fb * 7 + g * 13 + (shared ? 3 : 0)) % (unsigned)nch);
+    const int rot = sh.xcd_blocked ? 0 : (int)((unsigned)(fb * 7 + g * 13 + (shared ? 3 : 0)) % (unsigned)nch);
     auto issue = [&](int chunk, int buf) {
       int cc = min(chunk, nch - 1) + rot;  // past the last chunk: repeat it (never multiplied)
       if (cc >= nch) cc -= nch;
 #pragma unroll
       for (int j = 0; j < LL; ++j)
-        __builtin_amdgcn_global_load_lds(src[j] + cc * 64,
+        __builtin_amdgcn_global_load_lds(src[j] + cc * KC,
                                          (__attribute__((address_space(3))) void*)(lds + buf * SB + dst[j]), 16, 0, 0);
     };
     floatx4_t acc[4][8];
@@ -530,6 +552,26 @@ __global__ __launch_bounds__(RWV * 128) void gemm_dma_kernel(const GemmArgs a, c
 #pragma unroll
       for (int y = 0; y < XN; ++y) acc[x][y] = floatx4_t{0.f, 0.f, 0.f, 0.f};
     const int wa = (wv % RWV) * WM, wt = (wv / RWV) * WN;  // this wave's WM weight rows x WN tokens
+    // this wave's MFMA fragments of sub-step s (K 32 s .. 32 s + 31) of the chunk in stage st
+    auto frags = [&](const uint8_t* st, int s, bf16x8_t* af, bf16x8_t* bfr) {
+      const int pc = 4 * s + kg;
+#pragma unroll
+      for (int x = 0; x < XM; ++x) {
+        const int r = wa + 16 * x + li;
+        af[x] = *reinterpret_cast<const bf16x8_t*>(st + r * RB + ((pc ^ swz(r)) * 16));
+      }
+#pragma unroll
+      for (int y = 0; y < XN; ++y) {
+        const int t = wt + 16 * y + li;
+        bfr[y] = *reinterpret_cast<const bf16x8_t*>(st + TM * RB + t * RB + ((pc ^ swz(t)) * 16));
+      }
+    };
+    auto mfmas = [&](const bf16x8_t* af, const bf16x8_t* bfr) {
+#pragma unroll
+      for (int x = 0; x < XM; ++x)
+#pragma unroll
+        for (int y = 0; y < XN; ++y) acc[x][y] = mfma16x16x32(af[x], bfr[y], acc[x][y]);
+    };
 #pragma unroll
     for (int s = 0; s + 1 < ST; ++s) issue(s, s);
     for (int c0 = 0; c0 < nch; c0 += ST) {
@@ -543,26 +585,39 @@ __global__ __launch_bounds__(RWV * 128) void gemm_dma_kernel(const GemmArgs a, c
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        issue(c + ST - 1, (i + ST - 1) % ST);
-        const uint8_t* st = lds + i * SB;
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
+        if constexpr (ST == 2 && KC == 64 && XM == 4 && XN == 8 && LL == 8) {
+          // the prefill shape: the next chunk's 8 ring loads go out one per 4 MFMAs of the
+          // first sub-step (sched_barrier pins the order) instead of as one burst that holds
+          // up the wave's MFMA issue (8192 x 2816 x 2048: 132.3 -> 121.7 us)
+          int cc = min(c + 1, nch - 1) + rot;
+          if (cc >= nch) cc -= nch;
+          const int buf = (i + 1) % ST;
           bf16x8_t af[4], bfr[8];
-          const int pc = 4 * s + kg;
-#pragma unroll
-          for (int x = 0; x < XM; ++x) {
-            const int r = wa + 16 * x + li;
-            af[x] = *reinterpret_cast<const bf16x8_t*>(st + r * 128 + ((pc ^ (r & 7)) * 16));
-          }
-#pragma unroll
-          for (int y = 0; y < XN; ++y) {
-            const int t = wt + 16 * y + li;
-            bfr[y] = *reinterpret_cast<const bf16x8_t*>(st + TM * 128 + t * 128 + ((pc ^ (t & 7)) * 16));
-          }
+          frags(lds + i * SB, 0, af, bfr);
 #pragma unroll
           for (int x = 0; x < XM; ++x)
 #pragma unroll
-            for (int y = 0; y < XN; ++y) acc[x][y] = mfma16x16x32(af[x], bfr[y], acc[x][y]);
+            for (int y = 0; y < XN; ++y) {
+              acc[x][y] = mfma16x16x32(af[x], bfr[y], acc[x][y]);
+              if (y % 4 == 3) {
+                const int j = x * 2 + y / 4;
+                __builtin_amdgcn_sched_barrier(0);
+                __builtin_amdgcn_global_load_lds(src[j] + cc * KC,
+                                                 (__attribute__((address_space(3))) void*)(lds + buf * SB + dst[j]),
+                                                 16, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+              }
+            }
+          frags(lds + i * SB, 1, af, bfr);
+          mfmas(af, bfr);
+        } else {
+          issue(c + ST - 1, (i + ST - 1) % ST);
+#pragma unroll
+          for (int s = 0; s < KC / 32; ++s) {
+            bf16x8_t af[4], bfr[8];
+            frags(lds + i * SB, s, af, bfr);
+            mfmas(af, bfr);
+          }
         }
       }
     }
@@ -619,10 +674,11 @@ __global__ __launch_bounds__(RWV * 128) void gemm_dma_kernel(const GemmArgs a, c
 // 7.1 s -> 6.0 s with 128 x 128 per 4-wave workgroup, 5.3 s with 256 x 128 per 8 waves and
 // three 48 KB stages; with the later attention changes 4.76 s -> 4.43 s with 256 x 256).
 constexpr int kBigRwv = 4, kBigStages = 2, kBigWn = 128;  // big: waves along the weight rows, ring stages,
-constexpr int kBigTokens = 2 * kBigWn;                    // tokens per wave; tokens per workgroup
+constexpr int kBigTokens = 2 * kBigWn, kBigKc = 64;       // tokens per wave; tokens per workgroup, K chunk
 constexpr int kBigRows = 64 * kBigRwv;                 // weight rows per big workgroup
 static void launch_dma(const GemmArgs& a, bool swiglu, hipStream_t st, int max_tiles = 0, bool big = false) {
   DmaShape sh;
+  sh.xcd_blocked = big;
   const int tn = big ? kBigTokens : 64;
   // plain: a last feature block past N (N % 64 == 0) repeats row N-1 and stores nothing there
   sh.nfb = swiglu ? a.N / (big ? kBigRows / 2 : 32) : (a.N + (big ? kBigRows : 64) - 1) / (big ? kBigRows : 64);
@@ -630,13 +686,13 @@ static void launch_dma(const GemmArgs& a, bool swiglu, hipStream_t st, int max_t
   // grouped: resident workgroups (two per CU, big: one) looping over the live items
   sh.nwg = a.tiles ? (big ? kDmaGroupedWgs / 2 : kDmaGroupedWgs) : (sh.nfb * sh.tiles + 7) / 8 * 8;
   if (big) {
-    constexpr int lds = kBigStages * (kBigRows + kBigTokens) * 128;
+    constexpr int lds = kBigStages * (kBigRows + kBigTokens) * 2 * kBigKc;
     if (swiglu)
-      hipLaunchKernelGGL((gemm_dma_kernel<true, 64, kBigWn, kBigStages, kBigRwv>), dim3(sh.nwg), dim3(128 * kBigRwv), lds,
-                         st, a, sh);
+      hipLaunchKernelGGL((gemm_dma_kernel<true, 64, kBigWn, kBigStages, kBigRwv, kBigKc>), dim3(sh.nwg),
+                         dim3(128 * kBigRwv), lds, st, a, sh);
     else
-      hipLaunchKernelGGL((gemm_dma_kernel<false, 64, kBigWn, kBigStages, kBigRwv>), dim3(sh.nwg), dim3(128 * kBigRwv),
-                         lds, st, a, sh);
+      hipLaunchKernelGGL((gemm_dma_kernel<false, 64, kBigWn, kBigStages, kBigRwv, kBigKc>), dim3(sh.nwg),
+                         dim3(128 * kBigRwv), lds, st, a, sh);
     return;
   }
   if (swiglu) hipLaunchKernelGGL(gemm_dma_kernel<true>, dim3(sh.nwg), dim3(256), kDmaStages * 16384, st, a, sh);

@@ -13,7 +13,8 @@
 // every K and V^T fragment the wave reads from LDS.  Keys go in 32-token tiles,
 // double-buffered in LDS (the next tile's 16-byte chunks in registers meanwhile):
 //   S^T = K Q^T   two 16-key blocks x 6 k-steps of v_mfma_f32_16x16x32_bf16 (queries = N)
-//   online softmax per query (column), fp32, the causal mask key <= query position
+//   online softmax per query (column), fp32, the causal mask key <= query position on the
+//                   tiles that cross the diagonal, lazy rescaling of O and l
 //   O^T += V^T P^T  8 x 16 value dims; V^T fragments by transposed LDS reads
 //                   (ds_read_b64_tr_b16), P^T packed to bf16 in the order the reads give.
 #include "common.h"
@@ -39,8 +40,15 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_kernel(
     float scale_log2, bf16_t* __restrict__ out, int64_t os) {
   __shared__ __attribute__((aligned(16))) bf16_t kt[2][kKT * kKRow];
   __shared__ __attribute__((aligned(16))) bf16_t vt[2][kKT * kVRow];
-  const int4 tl = tiles[blockIdx.x];
-  const int h = blockIdx.y;
+  // 1-D grid over (head, tile) items cut into 8 contiguous ranges, one per XCD (workgroup i
+  // runs on XCD i % 8): the query tiles of one (sequence, head) run on one XCD at about the
+  // same time and sweep the same keys from key 0, so each key tile comes from HBM once per
+  // XCD and from that XCD's L2 for the rest; tiles are taken last first (a sequence's last
+  // tiles attend the most keys), which shortens the launch's tail
+  const int n_tiles = gridDim.x / kHeads;
+  const int item = (blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8;
+  const int h = item / n_tiles;
+  const int4 tl = tiles[n_tiles - 1 - item % n_tiles];
   // every index derived from the tile table is clamped into the buffers the host described
   // (a malformed table gives wrong numbers, never an access outside them)
   const int r0 = min(max(tl.x, 0), rows - 1), nr = min(max(tl.y, 1), min(kQT, rows - r0)), p0 = max(tl.z, 0);
@@ -128,36 +136,48 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_kernel(
 #pragma unroll
       for (int qb = 0; qb < kQB; ++qb) sc[qb][blk] = sp[qb];
     }
+    // the causal mask only on tiles that reach past the wave's first query position
+    const bool diag = t0 + kKT - 1 > p0 + wv * 16 * kQB;
     bf16x8_t pb[kQB];
 #pragma unroll
     for (int qb = 0; qb < kQB; ++qb) {
       float p[8];
-      float mx = -INFINITY;
+      float mx = -INFINITY;  // of the raw scores (scale_log2 > 0 keeps the order)
 #pragma unroll
       for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int kp = t0 + blk * 16 + 4 * kg + e;
-          const float v = kp <= qp[qb] ? sc[qb][blk][e] * scale_log2 : -INFINITY;
+          const float v = !diag || kp <= qp[qb] ? sc[qb][blk][e] : -INFINITY;
           p[blk * 4 + e] = v;
           mx = fmaxf(mx, v);
         }
       mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_run[qb], mx);  // finite: key 0 is in the first tile of every query
-      const float alpha = exp2f(m_run[qb] - m_new);
+      // lazy rescaling: the running maximum m (log2 units) moves, and O and l are rescaled,
+      // only where the tile's maximum exceeds it by more than 8, so p = 2^(s - m) <= 256
+      // (bf16 and the fp32 sums hold it) while most tiles skip the rescale; O / l does not
+      // depend on the m chosen.  The first tile always moves m (key 0 is in every query's
+      // first tile); a query all of whose keys in a tile are masked has mx = -inf there.
+      const float tm = mx * scale_log2;
+      const bool grow = tm > m_run[qb] + 8.f;
+      if (__any(grow)) {
+        const float m_new = grow ? tm : m_run[qb];
+        const float alpha = exp2f(m_run[qb] - m_new);  // 0 from m = -inf, 1 where m stays
+        l_run[qb] *= alpha;
+        m_run[qb] = m_new;
+#pragma unroll
+        for (int mb = 0; mb < 8; ++mb) acc[qb][mb] *= alpha;
+      }
       float rsum = 0.f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        p[i] = exp2f(p[i] - m_new);
+        p[i] = exp2f(fmaf(p[i], scale_log2, -m_run[qb]));
         rsum += p[i];
       }
       rsum += __shfl_xor(rsum, 16, 64);
       rsum += __shfl_xor(rsum, 32, 64);
-      l_run[qb] = l_run[qb] * alpha + rsum;
-      m_run[qb] = m_new;
-#pragma unroll
-      for (int mb = 0; mb < 8; ++mb) acc[qb][mb] *= alpha;
+      l_run[qb] += rsum;
       pb[qb] = as_bf16x8(pack8(p));
     }
     // O^T += V^T P^T: lane (li, kg) addresses key 4kg + li/4 (then 16 + 4kg + li/4), dims
@@ -198,7 +218,7 @@ extern "C" int dsv2_mla_prefill_attention(const void* qkva, int64_t qkva_stride,
                                           int64_t out_stride, void* stream) {
   DSV2_REQUIRE(qkva && q_rope && cache && k_nope && v && tiles && out, DSV2_E_NULL,
                "mla_prefill_attention: null pointer");
-  DSV2_REQUIRE(n_tiles >= 0 && n_tiles <= 0x7fffffff && exp_lo >= 0 && qkva_stride >= 3648 &&
+  DSV2_REQUIRE(n_tiles >= 0 && n_tiles <= 0x7ffffff && exp_lo >= 0 && qkva_stride >= 3648 &&
                    q_rope_stride >= kHeads * kCacheRow && out_stride >= kHeads * kVD && rows >= 0 &&
                    cache_rows > 0 && exp_rows > 0,
                DSV2_E_SHAPE, "mla_prefill_attention: bad shape");
@@ -207,7 +227,7 @@ extern "C" int dsv2_mla_prefill_attention(const void* qkva, int64_t qkva_stride,
                    q_rope_stride % 8 == 0 && out_stride % 4 == 0,
                DSV2_E_ALIGN, "mla_prefill_attention: alignment");
   if (n_tiles == 0 || rows == 0) return DSV2_OK;
-  hipLaunchKernelGGL(mla_prefill_kernel, dim3(n_tiles, kHeads), dim3(256), 0, (hipStream_t)stream,
+  hipLaunchKernelGGL(mla_prefill_kernel, dim3(n_tiles * kHeads), dim3(256), 0, (hipStream_t)stream,
                      (const bf16_t*)qkva, qkva_stride, (const bf16_t*)q_rope, q_rope_stride, (const bf16_t*)cache,
                      cache_rows, (const bf16_t*)k_nope, (const bf16_t*)v, exp_lo, exp_rows, rows, (const int4*)tiles,
                      softmax_scale * 1.4426950408889634f, (bf16_t*)out, out_stride);

@@ -326,9 +326,12 @@ class DecodeEngine:
         call("dsv2_mla_prepare", ptr(b.qkva), c.qkva_dim, R, ptr(pos), ptr(base), ptr(cap), ptr(L.kv_norm), c.eps,
              ptr(self.cos), ptr(self.sin), self.max_pos, None, ptr(cache), ptr(b.q), ptr(self.cache.status), st)
         crow = cache.data_ptr() + pf.exp_lo * c.cache_row * cache.element_size()
-        for w, out in ((L.w_uk, pf.kexp), (L.w_uv, pf.vexp)):
-            call("dsv2_gemm_bf16", crow, c.cache_row, 0, pf.exp_rows, c.kv_rank, ptr(w), c.qk_nope * c.kv_rank,
-                 c.qk_nope, nh, None, 0, ptr(out), nh * c.qk_nope, c.qk_nope, 0, st)
+        # W_UK / W_UV [16, 128, 512] are the [2048, 512] weights of one dense GEMM whose output
+        # row is [16, 128] (the heads side by side): the prefill-size ring tiles, not 16 groups
+        # of 128 features (C3 prefill: 73 -> ~25 us per expansion)
+        for w, out, n in ((L.w_uk, pf.kexp, nh * c.qk_nope), (L.w_uv, pf.vexp, nh * c.v_dim)):
+            call("dsv2_gemm_bf16", crow, c.cache_row, 0, pf.exp_rows, c.kv_rank, ptr(w), 0, n, 1, None, 0, ptr(out), n,
+                 0, 0, st)
         call("dsv2_mla_prefill_attention", ptr(b.qkva), c.qkva_dim, ptr(b.q), nh * c.cache_row, R, ptr(cache),
              cache.shape[0], ptr(pf.kexp), ptr(pf.vexp), pf.exp_lo, pf.exp_rows, ptr(pf.tiles), pf.n_tiles,
              self.scale, ptr(b.attn), H, st)

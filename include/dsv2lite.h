@@ -274,9 +274,10 @@ int dsv2_attention_decode_expanded(const void* q, int64_t q_stride_b, int64_t q_
  *   k_nh = [k_nope[sb + n - exp_lo, h, :128] | cache[sb + n, 512 .. 576]],
  *   v_nh = v[sb + n - exp_lo, h, :128]
  * k_nope / v [exp_rows, 16, 128] bf16 are W_UK / W_UV applied to cache rows exp_lo .. (the
- * kv_b projection of every cached token; dsv2_gemm_bf16 grouped over heads).  tiles [n_tiles]
- * int32x4 {first row, rows (1..128), position of the first row, sb}: <= 128 consecutive query
- * rows of one sequence each.  Indices derived from the table are clamped into rows /
+ * kv_b projection of every cached token: one dsv2_gemm_bf16 over the heads side by side).
+ * tiles [n_tiles <= 2^27 - 1] int32x4 {first row, rows (1..128), position of the first row,
+ * sb}: <= 128 consecutive query rows of one sequence each, a sequence's tiles consecutive
+ * (the XCD placement assumes it; any order gives the same result).  Indices derived from the table are clamped into rows /
  * cache_rows / exp_rows.  Replaces the prefill attention of the HF model the reference runs
  * eagerly (src/run.py:526-544; remote DeepseekV2Attention.forward over the expanded K/V). */
 int dsv2_mla_prefill_attention(const void* qkva, int64_t qkva_stride, const void* q_rope, int64_t q_rope_stride,
