@@ -75,6 +75,9 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 // ds_read_b64_tr_b16 (gfx950): in each 16-lane group, lane i receives element i % 4 of the
 // four 16-bit elements that lane 4e + i / 4 addressed, for e = 0..3 (measured with a probe
 // kernel on MI355X: LDS element values = their index).  p must point into LDS, 8-byte aligned.
+// s_waitcnt immediate (gfx9 encoding): wait until at most n vector-memory operations are
+// outstanding, leaving the LDS/scalar (15) and export (7) counters unconstrained
+constexpr int vmcnt_only(int n) { return (n & 0xf) | (0x7 << 4) | (0xf << 8) | (((n >> 4) & 3) << 14); }
 __device__ __forceinline__ uint2 lds_read_tr16(const bf16_t* p) {
   typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
   const bf16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4_t*)p);
@@ -134,9 +137,42 @@ __device__ __forceinline__ float dot8(const uint4& w, const float* x) {
 }
 
 // ---- wave / block reductions (wave64) ---------------------------------------
+// v combined with lane l ^ 32 (xor32_*) or l ^ 16 (xor16_*) by the gfx950 VALU lane swaps
+// instead of LDS-routed shuffles: v_permlane32_swap on two copies of v leaves [lo, lo] in
+// one and [hi, hi] in the other (the wave's 32-lane halves), v_permlane16_swap does the same
+// for rows 0 / 1 and 2 / 3; op(a, b) is symmetric, so every lane gets exactly the value of
+// v op __shfl_xor(v, 32 or 16) (checked bit for bit on MI355X)
+__device__ __forceinline__ float xor32_sum(float v) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ float xor16_sum(float v) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ float xor32_max(float v) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ __forceinline__ float xor16_max(float v) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+
+// one butterfly step, v op (v at lane l ^ off): the lane swaps for off = 32 and 16 (a
+// compile-time constant in the unrolled loops that call these), a shuffle below
+__device__ __forceinline__ float xor_sum(float v, int off) {
+  return off == 32 ? xor32_sum(v) : (off == 16 ? xor16_sum(v) : v + __shfl_xor(v, off, DSV2_WAVE));
+}
+__device__ __forceinline__ float xor_max(float v, int off) {
+  return off == 32 ? xor32_max(v) : (off == 16 ? xor16_max(v) : fmaxf(v, __shfl_xor(v, off, DSV2_WAVE)));
+}
+
+// butterfly over the 64 lanes, l ^ 32 first (every lane gets the same, fixed-order sum)
 __device__ __forceinline__ float wave_sum(float v) {
+  v = xor16_sum(xor32_sum(v));
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, DSV2_WAVE);
+  for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o, DSV2_WAVE);
   return v;
 }
 
@@ -159,8 +195,9 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
 }
 
 __device__ __forceinline__ float wave_max(float v) {
+  v = xor16_max(xor32_max(v));
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, DSV2_WAVE));
+  for (int o = 8; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, DSV2_WAVE));
   return v;
 }
 

@@ -417,9 +417,6 @@ __device__ __forceinline__ void gemm_store4(const GemmArgs& a, int g, int slot, 
 // shape; without the XCD grouping 18.3 us).
 constexpr int kDmaStages = 4;
 constexpr int kDmaGroupedWgs = 512;  // 256 CUs x 2 (64 KB of LDS each)
-// s_waitcnt immediate (gfx9 encoding): wait until at most n vector-memory operations are
-// outstanding, leaving the LDS/scalar (15) and export (7) counters unconstrained
-constexpr int vmcnt_only(int n) { return (n & 0xf) | (0x7 << 4) | (0xf << 8) | (((n >> 4) & 3) << 14); }
 
 // xcd_blocked (the prefill shape): the work items, token-tile-major (all feature blocks of a
 // token tile, then the next tile, an expert's tiles in a row), are cut into 8 contiguous

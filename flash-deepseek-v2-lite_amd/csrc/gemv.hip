@@ -149,8 +149,8 @@ __global__ __launch_bounds__(256) void gemv_k2048_kernel(const bf16_t* __restric
       for (int r = 0; r < RPW; ++r)
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
-          acc[r][b] += __shfl_xor(acc[r][b], off, 64);
-          if (SWIGLU) accu[r][b] += __shfl_xor(accu[r][b], off, 64);
+          acc[r][b] = xor_sum(acc[r][b], off);
+          if (SWIGLU) accu[r][b] = xor_sum(accu[r][b], off);
         }
     if (lane == 0) {
 #pragma unroll
@@ -254,8 +254,8 @@ __global__ __launch_bounds__(256) void gemv_b1_kernel(const bf16_t* __restrict__
   for (int off = 32; off > 0; off >>= 1)
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
-      ag[r] += __shfl_xor(ag[r], off, 64);
-      if (SW) au[r] += __shfl_xor(au[r], off, 64);
+      ag[r] = xor_sum(ag[r], off);
+      if (SW) au[r] = xor_sum(au[r], off);
     }
   // every lane forms the outputs (the residual is consumed in this block, so its load stays
   // where it was issued, in flight with the weights); lane 0 stores them
@@ -349,7 +349,7 @@ __global__ __launch_bounds__(256) void gemv_klong_kernel(const bf16_t* __restric
 #pragma unroll
     for (int r = 0; r < RPW; ++r)
 #pragma unroll
-      for (int b = 0; b < NB; ++b) acc[r][b] += __shfl_xor(acc[r][b], off, 64);
+      for (int b = 0; b < NB; ++b) acc[r][b] = xor_sum(acc[r][b], off);
   if (lane == 0) {
 #pragma unroll
     for (int b = 0; b < NB; ++b) {

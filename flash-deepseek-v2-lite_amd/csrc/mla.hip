@@ -102,7 +102,7 @@ __global__ __launch_bounds__(256) void mla_prepare_kernel(const bf16_t* __restri
 #pragma unroll
       for (int off = 8; off > 0; off >>= 1)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) sdot[q] += __shfl_xor(sdot[q], off, 64);
+        for (int q = 0; q < 4; ++q) sdot[q] = xor_sum(sdot[q], off);
       if (k == 0) {
         uint2 o;
         o.x = pack2(sdot[0], sdot[1]);
@@ -299,8 +299,8 @@ __global__ __launch_bounds__(256, 2) void mla_decode_kernel(const bf16_t* __rest
         p[blk * 4 + e] = v;
         mx = fmaxf(mx, v);
       }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = xor16_max(mx);
+    mx = xor32_max(mx);
     const float m_new = fmaxf(m_run, mx);
     const float alpha = exp2f(m_run - m_new);
     float rsum = 0.f;
@@ -309,8 +309,8 @@ __global__ __launch_bounds__(256, 2) void mla_decode_kernel(const bf16_t* __rest
       p[i] = exp2f(p[i] - m_new);
       rsum += p[i];
     }
-    rsum += __shfl_xor(rsum, 16, 64);
-    rsum += __shfl_xor(rsum, 32, 64);
+    rsum = xor16_sum(rsum);
+    rsum = xor32_sum(rsum);
     l_run = l_run * alpha + rsum;
     m_run = m_new;
 #pragma unroll
@@ -471,7 +471,7 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(const float* __restric
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) r[i] += __shfl_xor(r[i], off, 64);
+    for (int i = 0; i < 8; ++i) r[i] = xor_sum(r[i], off);
   if (lane == 0) *reinterpret_cast<uint4*>(out + b * os + h * 128 + part * 32 + wv * 8) = pack8(r);
 }
 

@@ -20,15 +20,20 @@
 #include "common.h"
 
 namespace {
-constexpr int kKT = 32;         // keys per tile
-constexpr int kQK = 192;        // q.k dims: 128 nope + 64 rope
-constexpr int kVD = 128;        // value dims
-constexpr int kKRow = kQK + 8;  // padded LDS rows (elements): 400 B
-constexpr int kVRow = kVD + 8;  // 272 B
+constexpr int kKT = 32;   // keys per tile
+constexpr int kQK = 192;  // q.k dims: 128 nope + 64 rope
+constexpr int kVD = 128;  // value dims
 constexpr int kHeads = 16;
 constexpr int kCacheRow = 576;
-constexpr int kChunksPerKey = kQK / 8 + kVD / 8;  // 16-byte chunks per key: 16 nope + 8 rope + 16 v = 40
-constexpr int kLoads = kKT * kChunksPerKey / 256;  // per thread per tile: 5
+constexpr int kKC = kQK / 8, kVC = kVD / 8;      // 16-byte chunks per key: K 16 nope + 8 rope, V 16
+constexpr int kStageK = kKT * kKC * 16;          // a stage: the tile's K rows (384 B each), then
+constexpr int kStage = kStageK + kKT * kVC * 16;  // its V rows (256 B each): 20 KB
+constexpr int kStages = 3;
+constexpr int kLoads = kKT * (kKC + kVC) / 256;  // 16-byte ring loads per thread per tile: 5
+// chunk c of key row r sits in slot swz(c, r) (an involution within each aligned group of 8
+// chunks): the 16 rows one K fragment reads, and the 4 rows of a transposed V read, fall in
+// different banks
+__device__ __forceinline__ int swz(int c, int r) { return (c & ~7) | ((c ^ r) & 7); }
 constexpr int kQB = 2;                             // 16-query blocks per wave
 constexpr int kQT = 4 * 16 * kQB;                  // queries per workgroup tile
 }  // namespace
@@ -38,8 +43,7 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_kernel(
     const bf16_t* __restrict__ cache, int64_t cache_rows, const bf16_t* __restrict__ knope,
     const bf16_t* __restrict__ vexp, int64_t exp_lo, int64_t exp_rows, int rows, const int4* __restrict__ tiles,
     float scale_log2, bf16_t* __restrict__ out, int64_t os) {
-  __shared__ __attribute__((aligned(16))) bf16_t kt[2][kKT * kKRow];
-  __shared__ __attribute__((aligned(16))) bf16_t vt[2][kKT * kVRow];
+  __shared__ __attribute__((aligned(16))) uint8_t ring[kStages * kStage];
   // 1-D grid over (head, tile) items cut into 8 contiguous ranges, one per XCD (workgroup i
   // runs on XCD i % 8): the query tiles of one (sequence, head) run on one XCD at about the
   // same time and sweep the same keys from key 0, so each key tile comes from HBM once per
@@ -71,15 +75,27 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_kernel(
   const int nkv = p0 + nr;  // keys [0, nkv) of the sequence
   const int ntiles = (nkv + kKT - 1) / kKT;
 
-  uint4 st[kLoads];
-  auto load_tile = [&](int t0) {
+  // K/V tiles stream straight into a 3-stage LDS ring (global_load_lds, 16 B per lane): ring
+  // load i of wave wv fills slots 64 (4i + wv) .. + 63 of a stage, slot s holding K chunk
+  // slot s % 24 of key s / 24 (s < 768), else V chunk slot (s - 768) % 16 of key
+  // (s - 768) / 16; each lane fetches the chunk that belongs in its slot
+  int lkey[kLoads], lchunk[kLoads];
+#pragma unroll
+  for (int i = 0; i < kLoads; ++i) {
+    const int sl = 64 * (4 * i + wv) + lane;
+    const bool kpart = sl < kKT * kKC;
+    const int s2 = kpart ? sl : sl - kKT * kKC, per = kpart ? kKC : kVC;
+    lkey[i] = s2 / per;
+    lchunk[i] = swz(s2 % per, lkey[i]) + (kpart ? 0 : kKC);  // 0..23 K, 24..39 V
+  }
+  auto issue = [&](int t, int stage) {
+    const int t0 = t * kKT;
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
-      const int c = tid + 256 * i;
-      const int key = c / kChunksPerKey, part = c % kChunksPerKey;
-      const int64_t row = sb + min(t0 + key, nkv - 1);  // past the prefix: the last key (masked)
+      const int64_t row = sb + min(t0 + lkey[i], nkv - 1);  // past the prefix: the last key (masked)
       const int64_t crow = min(max(row, (int64_t)0), cache_rows - 1);
       const int64_t erow = min(max(row - exp_lo, (int64_t)0), exp_rows - 1);
+      const int part = lchunk[i];
       const bf16_t* src;
       if (part < 16)
         src = knope + erow * (kHeads * kVD) + h * kVD + part * 8;
@@ -87,22 +103,15 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_kernel(
         src = cache + crow * kCacheRow + 512 + (part - 16) * 8;
       else
         src = vexp + erow * (kHeads * kVD) + h * kVD + (part - 24) * 8;
-      st[i] = ldg16(src);
+      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(ring + stage * kStage +
+                                                                                          (4 * i + wv) * 1024),
+                                       16, 0, 0);
     }
   };
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < kLoads; ++i) {
-      const int c = tid + 256 * i;
-      const int key = c / kChunksPerKey, part = c % kChunksPerKey;
-      bf16_t* dst = part < 24 ? &kt[buf][key * kKRow + part * 8] : &vt[buf][key * kVRow + (part - 24) * 8];
-      *reinterpret_cast<uint4*>(dst) = st[i];
-    }
-  };
-
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
+  // tiles past the last one repeat its keys into a stage nobody reads: every wave then has
+  // exactly kLoads newer loads in flight at each wait
+  issue(0, 0);
+  issue(1, 1);
 
   float m_run[kQB], l_run[kQB];
   floatx4_t acc[kQB][8];
@@ -115,9 +124,16 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_kernel(
   }
 
   for (int it = 0; it < ntiles; ++it) {
-    const int buf = it & 1;
     const int t0 = it * kKT;
-    if (it + 1 < ntiles) load_tile(t0 + kKT);
+    // this wave's loads of tile it have landed (tile it + 1's may not), then every wave's:
+    // the tile is complete and tile it - 1's stage is free for tile it + 2
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(kLoads));
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    issue(it + 2, (it + 2) % kStages);
+    const uint8_t* const kst = ring + (it % kStages) * kStage;
+    const uint8_t* const vst = kst + kStageK;
     // S^T: sc[qb][blk][e] = score(key t0 + blk*16 + 4kg + e, query jq[qb]); each K fragment
     // serves both query blocks
     floatx4_t sc[kQB][2];
@@ -126,10 +142,11 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_kernel(
       floatx4_t sp[kQB];
 #pragma unroll
       for (int qb = 0; qb < kQB; ++qb) sp[qb] = floatx4_t{0.f, 0.f, 0.f, 0.f};
-      const bf16_t* kr = &kt[buf][(blk * 16 + li) * kKRow + kg * 8];
+      const int krow = blk * 16 + li;
+      const uint8_t* kr = kst + krow * (kKC * 16);
 #pragma unroll
       for (int kk = 0; kk < 6; ++kk) {
-        const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(kr + kk * 32);
+        const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(kr + swz(4 * kk + kg, krow) * 16);
 #pragma unroll
         for (int qb = 0; qb < kQB; ++qb) sp[qb] = mfma16x16x32(kf, qf[qb][kk], sp[qb]);
       }
@@ -152,8 +169,8 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_kernel(
           p[blk * 4 + e] = v;
           mx = fmaxf(mx, v);
         }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      mx = xor16_max(mx);
+      mx = xor32_max(mx);
       // lazy rescaling: the running maximum m (log2 units) moves, and O and l are rescaled,
       // only where the tile's maximum exceeds it by more than 8, so p = 2^(s - m) <= 256
       // (bf16 and the fp32 sums hold it) while most tiles skip the rescale; O / l does not
@@ -175,27 +192,27 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_kernel(
         p[i] = exp2f(fmaf(p[i], scale_log2, -m_run[qb]));
         rsum += p[i];
       }
-      rsum += __shfl_xor(rsum, 16, 64);
-      rsum += __shfl_xor(rsum, 32, 64);
+      rsum = xor16_sum(rsum);
+      rsum = xor32_sum(rsum);
       l_run[qb] += rsum;
       pb[qb] = as_bf16x8(pack8(p));
     }
     // O^T += V^T P^T: lane (li, kg) addresses key 4kg + li/4 (then 16 + 4kg + li/4), dims
     // 16mb + 4(li % 4) .. +3, and receives V[4kg + e][16mb + li] (then V[16 + 4kg + e][..]),
     // the keys of its P^T column in the same order; each V^T fragment serves both blocks
-    const bf16_t* vp = &vt[buf][(4 * kg + (li >> 2)) * kVRow + 4 * (li & 3)];
+    const int vr = 4 * kg + (li >> 2);  // then vr + 16
 #pragma unroll
     for (int mb = 0; mb < 8; ++mb) {
-      const uint2 lo = lds_read_tr16(vp + mb * 16), hi = lds_read_tr16(vp + mb * 16 + 16 * kVRow);
+      const int vc = 2 * mb + ((li & 3) >> 1), vo = (li & 1) * 8;  // chunk, byte in it
+      const uint2 lo = lds_read_tr16(reinterpret_cast<const bf16_t*>(vst + vr * (kVC * 16) + swz(vc, vr) * 16 + vo));
+      const uint2 hi =
+          lds_read_tr16(reinterpret_cast<const bf16_t*>(vst + (vr + 16) * (kVC * 16) + swz(vc, vr + 16) * 16 + vo));
       const bf16x8_t vf = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
 #pragma unroll
       for (int qb = 0; qb < kQB; ++qb) acc[qb][mb] = mfma16x16x32(vf, pb[qb], acc[qb][mb]);
     }
-    // buffer buf ^ 1 was last read in iteration it - 1, which every wave finished before
-    // that iteration's closing barrier
-    if (it + 1 < ntiles) store_tile(buf ^ 1);
-    __syncthreads();
   }
+  __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // the repeats land before the LDS is released
 #pragma unroll
   for (int qb = 0; qb < kQB; ++qb) {
     if (jq[qb] >= nr) continue;

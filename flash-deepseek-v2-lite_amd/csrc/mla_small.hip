@@ -172,11 +172,11 @@ __device__ __forceinline__ void att_finish(AttTok (&ta)[kAttTB], AttTok (&tb)[kA
     const float mw = lane < kAttRows ? sh.wm[lane] : -INFINITY;
     float M = mw;
 #pragma unroll
-    for (int off = 16; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+    for (int off = 16; off > 0; off >>= 1) M = xor_max(M, off);
     const float sw = exp2f(mw - M);
     float L = lane < kAttRows ? sh.wl[lane] * sw : 0.f;
 #pragma unroll
-    for (int off = 16; off > 0; off >>= 1) L += __shfl_xor(L, off, 64);
+    for (int off = 16; off > 0; off >>= 1) L = xor_sum(L, off);
     if (lane < kAttRows) sh.wm[lane] = sw / L;
   }
   __syncthreads();
@@ -468,7 +468,7 @@ __global__ __launch_bounds__(512) void qkva_absorb_kernel(const bf16_t* __restri
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1)
 #pragma unroll
-    for (int r = 0; r < 2; ++r) acc[r] += __shfl_xor(acc[r], off, 64);
+    for (int r = 0; r < 2; ++r) acc[r] = xor_sum(acc[r], off);
   float qd[2];
 #pragma unroll
   for (int r = 0; r < 2; ++r) qd[r] = rbf(acc[r]);

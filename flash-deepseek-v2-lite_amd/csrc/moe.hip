@@ -82,7 +82,7 @@ __global__ __launch_bounds__(1024) void router_kernel(const bf16_t* __restrict__
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[r] += __shfl_xor(acc[r], off, 64);
+      for (int r = 0; r < 4; ++r) acc[r] = xor_sum(acc[r], off);
     if (lane < 4) lg[wv * 4 + lane] = lane == 0 ? acc[0] : (lane == 1 ? acc[1] : (lane == 2 ? acc[2] : acc[3]));
     __syncthreads();
   } else {
@@ -306,8 +306,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) voi
   for (int off = 32; off > 0; off >>= 1)
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
-      ag[r] += __shfl_xor(ag[r], off, 64);
-      au[r] += __shfl_xor(au[r], off, 64);
+      ag[r] = xor_sum(ag[r], off);
+      au[r] = xor_sum(au[r], off);
     }
   if (lane == 0) {
 #pragma unroll
@@ -388,8 +388,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) voi
   for (int off = 32; off > 0; off >>= 1)
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
-      ag[r] += __shfl_xor(ag[r], off, 64);
-      au[r] += __shfl_xor(au[r], off, 64);
+      ag[r] = xor_sum(ag[r], off);
+      au[r] = xor_sum(au[r], off);
     }
   if (lane == 0) {
 #pragma unroll
@@ -567,7 +567,7 @@ __global__ __launch_bounds__(256) void route_down_kernel(const bf16_t* __restric
 #pragma unroll
       for (int q = 0; q < 2; ++q)
 #pragma unroll
-        for (int r = 0; r < 2; ++r) acc[q][r] += __shfl_xor(acc[q][r], off, 64);
+        for (int r = 0; r < 2; ++r) acc[q][r] = xor_sum(acc[q][r], off);
     if (lane == 0) {
 #pragma unroll
       for (int q = 0; q < 2; ++q)
@@ -669,7 +669,7 @@ __global__ __launch_bounds__(256) void route_down_fp8_kernel(const bf16_t* __res
 #pragma unroll
       for (int q = 0; q < 2; ++q)
 #pragma unroll
-        for (int r = 0; r < 2; ++r) acc[q][r] += __shfl_xor(acc[q][r], off, 64);
+        for (int r = 0; r < 2; ++r) acc[q][r] = xor_sum(acc[q][r], off);
     if (lane == 0) {
 #pragma unroll
       for (int q = 0; q < 2; ++q)
