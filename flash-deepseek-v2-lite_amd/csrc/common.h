@@ -159,20 +159,32 @@ __device__ __forceinline__ float xor16_max(float v) {
   return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
 }
 
-// one butterfly step, v op (v at lane l ^ off): the lane swaps for off = 32 and 16 (a
-// compile-time constant in the unrolled loops that call these), a shuffle below
+#define DSV2_DPP(v, ctrl) \
+  __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, (v)), (ctrl), 0xF, 0xF, false))
+// v at lane l ^ off for off = 1, 2, 4, 8 by DPP within the 16-lane rows: quad_perm [1,0,3,2]
+// and [2,3,0,1], row_ror:8, and for 4 row_shl:4 / row_shr:4 chosen by lane bit 2 (each the
+// exact xor partner, checked against __shfl_xor on MI355X)
+__device__ __forceinline__ float xor_partner_row(float v, int off) {
+  if (off == 1) return DSV2_DPP(v, 0xB1);
+  if (off == 2) return DSV2_DPP(v, 0x4E);
+  if (off == 8) return DSV2_DPP(v, 0x128);
+  const float up = DSV2_DPP(v, 0x104), dn = DSV2_DPP(v, 0x114);
+  return (threadIdx.x & 4) ? dn : up;
+}
+// one butterfly step, v op (v at lane l ^ off), off a compile-time constant in the unrolled
+// loops that call these: lane swaps for 32 and 16, DPP below -- no LDS-routed shuffles
 __device__ __forceinline__ float xor_sum(float v, int off) {
-  return off == 32 ? xor32_sum(v) : (off == 16 ? xor16_sum(v) : v + __shfl_xor(v, off, DSV2_WAVE));
+  return off == 32 ? xor32_sum(v) : (off == 16 ? xor16_sum(v) : v + xor_partner_row(v, off));
 }
 __device__ __forceinline__ float xor_max(float v, int off) {
-  return off == 32 ? xor32_max(v) : (off == 16 ? xor16_max(v) : fmaxf(v, __shfl_xor(v, off, DSV2_WAVE)));
+  return off == 32 ? xor32_max(v) : (off == 16 ? xor16_max(v) : fmaxf(v, xor_partner_row(v, off)));
 }
 
 // butterfly over the 64 lanes, l ^ 32 first (every lane gets the same, fixed-order sum)
 __device__ __forceinline__ float wave_sum(float v) {
   v = xor16_sum(xor32_sum(v));
 #pragma unroll
-  for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o, DSV2_WAVE);
+  for (int o = 8; o > 0; o >>= 1) v = xor_sum(v, o);
   return v;
 }
 
@@ -180,8 +192,6 @@ __device__ __forceinline__ float wave_sum(float v) {
 // row_half_mirror and row_mirror leave the row's sum in all 16 lanes), then the four row
 // sums read into scalars.  Uniform result; a different (fixed) summation order from
 // wave_sum, with no LDS traffic and a short dependency chain.
-#define DSV2_DPP(v, ctrl) \
-  __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, (v)), (ctrl), 0xF, 0xF, false))
 __device__ __forceinline__ float wave_sum_dpp(float v) {
   v += DSV2_DPP(v, 0xB1);   // quad_perm [1,0,3,2]
   v += DSV2_DPP(v, 0x4E);   // quad_perm [2,3,0,1]
@@ -197,7 +207,7 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
 __device__ __forceinline__ float wave_max(float v) {
   v = xor16_max(xor32_max(v));
 #pragma unroll
-  for (int o = 8; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, DSV2_WAVE));
+  for (int o = 8; o > 0; o >>= 1) v = xor_max(v, o);
   return v;
 }
 
