@@ -289,32 +289,41 @@ __global__ __launch_bounds__(256, 2) void mla_decode_kernel(const bf16_t* __rest
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk) sc[blk] = spart[2 * blk][lane] + spart[2 * blk + 1][lane];
     float p[8];
-    float mx = -INFINITY;
+    float mx = -INFINITY;  // of the raw scores (scale_log2 > 0 keeps the order)
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int tok = t0 + blk * 16 + 4 * kg + e;
-        const float v = tok < t_end ? sc[blk][e] * scale_log2 : -INFINITY;
+        const float v = tok < t_end ? sc[blk][e] : -INFINITY;
         p[blk * 4 + e] = v;
         mx = fmaxf(mx, v);
       }
     mx = xor16_max(mx);
     mx = xor32_max(mx);
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = exp2f(m_run - m_new);
+    // lazy rescaling: the running maximum m (log2 units) moves, and O and l are rescaled,
+    // only where the tile's maximum exceeds it by more than 8, so p = 2^(s - m) <= 256
+    // (bf16 and the fp32 sums hold it) while most tiles skip the rescale; (O, l, m) stay a
+    // consistent triple for the combine.  The first tile always moves m (it holds a token).
+    const float tm = mx * scale_log2;
+    const bool grow = tm > m_run + 8.f;
+    if (__any(grow)) {
+      const float m_new = grow ? tm : m_run;
+      const float alpha = exp2f(m_run - m_new);  // 0 from m = -inf, 1 where m stays
+      l_run *= alpha;
+      m_run = m_new;
+#pragma unroll
+      for (int mb = 0; mb < 8; ++mb) acc[mb] *= alpha;
+    }
     float rsum = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      p[i] = exp2f(p[i] - m_new);
+      p[i] = exp2f(fmaf(p[i], scale_log2, -m_run));
       rsum += p[i];
     }
     rsum = xor16_sum(rsum);
     rsum = xor32_sum(rsum);
-    l_run = l_run * alpha + rsum;
-    m_run = m_new;
-#pragma unroll
-    for (int mb = 0; mb < 8; ++mb) acc[mb] *= alpha;
+    l_run += rsum;
 
     // P^T (B operand): head li, tokens {4kg+e} then {16+4kg+e}; the V^T A operand takes the
     // same tokens of dim d0 + li through two transposed LDS reads (ds_read_b64_tr_b16): in
