@@ -110,8 +110,8 @@ def time_dominant_kernel(eng, family: str, reps: int = 4) -> dict:
         from dsv2lite.engine import shared_in_grouped
 
         sym = {16: "gemm_xlds_kernel<1, true, 4, true, 2, 2, 1, false>",
-               32: "gemm_xlds_kernel<2, true, 4, true, 2, 4, 2, true>", 64: "gemm_dma_kernel<true, 32, 32, 4, 2, 64>",
-               256: "gemm_dma_kernel<true, 64, 128, 2, 4, 64>"}[b.tile_tokens]
+               32: "gemm_xlds_kernel<2, true, 4, true, 2, 4, 2, true>", 64: "gemm_dma_kernel<true, 32, 32, 4, 2>",
+               256: "gemm_dma_kernel<true, 64, 128, 2, 4>"}[b.tile_tokens]
         n_exp = int(torch.unique(b.ids32[:B]).numel())
         bytes_per = n_exp * 2 * c.moe_inter * c.hidden * 2 + B * 6 * c.moe_inter * 2
         if shared_in_grouped(B, b.tile_tokens):

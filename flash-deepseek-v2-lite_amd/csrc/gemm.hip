@@ -439,23 +439,22 @@ struct DmaShape {
 // the live (tile, feature block) items only, so the table's dead tiles cost no workgroup
 // launches; token rows are gathered through slot_row and the tile's expert selects the
 // weights.
-template <bool SWIGLU, int WM = 32, int WN = 32, int ST = kDmaStages, int RWV = 2, int KC = 64>
+template <bool SWIGLU, int WM = 32, int WN = 32, int ST = kDmaStages, int RWV = 2>
 __global__ __launch_bounds__(RWV * 128) void gemm_dma_kernel(const GemmArgs a, const DmaShape sh) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // ST stages of SB bytes
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, li = lane & 15, kg = lane >> 4;
   constexpr int NW = 2 * RWV;                // waves: RWV along the weight rows x 2 along the tokens
   constexpr int TM = RWV * WM, TN = 2 * WN;  // weight rows, tokens per workgroup
-  constexpr int RB = 2 * KC, PR = KC / 8;    // a chunk's bytes per row, its 16 B pieces per row
-  constexpr int RPL = 64 / PR;               // rows per ring load (64 lanes x 16 B)
+  constexpr int KC = 64, RB = 2 * KC;        // K per chunk; a chunk's bytes per row (8 pieces of 16 B)
+  constexpr int RPL = 8;                     // rows per ring load (64 lanes x 16 B)
   constexpr int SB = (TM + TN) * RB;         // stage: TM weight rows, then TN token rows
   constexpr int LW = TM / (RPL * NW), LL = (TM + TN) / (RPL * NW);  // ring loads per wave per chunk: weights, all
   constexpr int XM = WM / 16, XN = WN / 16;  // MFMA blocks per wave
   constexpr int FPW = SWIGLU ? TM / 2 : TM;  // output features per workgroup
   static_assert(LL <= 8 && XM <= 4 && XN <= 8, "local arrays have literal sizes");
-  static_assert(KC == 64 || KC == 32, "64- or 32-wide K chunks");
-  // piece p of row r sits in slot p ^ swz(r): the 16 rows one MFMA fragment reads hit
+  // piece p of row r sits in slot p ^ (r & 7): the 16 rows one MFMA fragment reads hit
   // distinct banks in every group of 8 lanes
-  auto swz = [](int r) { return PR == 8 ? (r & 7) : ((r >> 1) & 3); };
+  auto swz = [](int r) { return r & 7; };
   // grouped: items j = tile * nfb + fb over the live tiles (the shared halves' tiles, then the
   // table's), consecutive items round-robin over the XCDs (keeping all token tiles of a
   // feature block on one XCD measured slower: fewer feature blocks than XCD slots balance)
@@ -499,9 +498,9 @@ __global__ __launch_bounds__(RWV * 128) void gemm_dma_kernel(const GemmArgs a, c
     }
     const int f0 = fb * FPW;
     const int K = a.K, nch = K / KC;
-    // this wave's LL ring loads per chunk, RPL rows x RB bytes each: weight rows (TM / NW per
-    // wave, j < LW) then token rows (TN / NW per wave); lane -> (row r, slot lane % PR), which
-    // holds piece (lane % PR) ^ swz(r)
+    // this wave's LL ring loads per chunk, 8 rows x 128 B each: weight rows (TM / NW per wave,
+    // j < LW) then token rows (TN / NW per wave); lane -> (row r, slot lane & 7), which holds
+    // piece (lane & 7) ^ (r & 7)
     const bf16_t* const wbase = shared ? a.W2 + g * a.w2g : a.W + g * a.wg;
     const int64_t wld = shared ? a.w2ld : K;
     const int upoff = shared ? a.w2up : a.N;
@@ -510,8 +509,8 @@ __global__ __launch_bounds__(RWV * 128) void gemm_dma_kernel(const GemmArgs a, c
 #pragma unroll
     for (int j = 0; j < LL; ++j) {
       const bool tok = j >= LW;
-      const int r = (tok ? (TN / NW) * wv + RPL * (j - LW) : (TM / NW) * wv + RPL * j) + lane / PR;
-      const int pc = (lane % PR) ^ swz(r);
+      const int r = (tok ? (TN / NW) * wv + RPL * (j - LW) : (TM / NW) * wv + RPL * j) + (lane >> 3);
+      const int pc = (lane & 7) ^ swz(r);
       if (tok) {
         const int slot = t0 + (r < count ? r : 0);  // rows past the tile: the tile's first row
         if (shared) {
@@ -582,7 +581,7 @@ __global__ __launch_bounds__(RWV * 128) void gemm_dma_kernel(const GemmArgs a, c
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        if constexpr (ST == 2 && KC == 64 && XM == 4 && XN == 8 && LL == 8) {
+        if constexpr (ST == 2 && XM == 4 && XN == 8 && LL == 8) {
           // the prefill shape: the next chunk's 8 ring loads go out one per 4 MFMAs of the
           // first sub-step (sched_barrier pins the order) instead of as one burst that holds
           // up the wave's MFMA issue (8192 x 2816 x 2048: 132.3 -> 121.7 us)
@@ -671,7 +670,7 @@ __global__ __launch_bounds__(RWV * 128) void gemm_dma_kernel(const GemmArgs a, c
 // 7.1 s -> 6.0 s with 128 x 128 per 4-wave workgroup, 5.3 s with 256 x 128 per 8 waves and
 // three 48 KB stages; with the later attention changes 4.76 s -> 4.43 s with 256 x 256).
 constexpr int kBigRwv = 4, kBigStages = 2, kBigWn = 128;  // big: waves along the weight rows, ring stages,
-constexpr int kBigTokens = 2 * kBigWn, kBigKc = 64;       // tokens per wave; tokens per workgroup, K chunk
+constexpr int kBigTokens = 2 * kBigWn;                    // tokens per wave; tokens per workgroup
 constexpr int kBigRows = 64 * kBigRwv;                 // weight rows per big workgroup
 static void launch_dma(const GemmArgs& a, bool swiglu, hipStream_t st, int max_tiles = 0, bool big = false) {
   DmaShape sh;
@@ -683,12 +682,12 @@ static void launch_dma(const GemmArgs& a, bool swiglu, hipStream_t st, int max_t
   // grouped: resident workgroups (two per CU, big: one) looping over the live items
   sh.nwg = a.tiles ? (big ? kDmaGroupedWgs / 2 : kDmaGroupedWgs) : (sh.nfb * sh.tiles + 7) / 8 * 8;
   if (big) {
-    constexpr int lds = kBigStages * (kBigRows + kBigTokens) * 2 * kBigKc;
+    constexpr int lds = kBigStages * (kBigRows + kBigTokens) * 128;
     if (swiglu)
-      hipLaunchKernelGGL((gemm_dma_kernel<true, 64, kBigWn, kBigStages, kBigRwv, kBigKc>), dim3(sh.nwg),
+      hipLaunchKernelGGL((gemm_dma_kernel<true, 64, kBigWn, kBigStages, kBigRwv>), dim3(sh.nwg),
                          dim3(128 * kBigRwv), lds, st, a, sh);
     else
-      hipLaunchKernelGGL((gemm_dma_kernel<false, 64, kBigWn, kBigStages, kBigRwv, kBigKc>), dim3(sh.nwg),
+      hipLaunchKernelGGL((gemm_dma_kernel<false, 64, kBigWn, kBigStages, kBigRwv>), dim3(sh.nwg),
                          dim3(128 * kBigRwv), lds, st, a, sh);
     return;
   }
