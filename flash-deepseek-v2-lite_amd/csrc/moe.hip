@@ -849,6 +849,145 @@ extern "C" int dsv2_moe_bucket(const int32_t* ids, int rows, int tile_tokens, in
 }
 
 // ---------------------------------------------------------------------------
+// bucketing over many workgroups (prefill chunks): the same counting sort as bucket_kernel,
+// bit for bit, in three launches -- per-chunk histograms (one wave per 64-route chunk), the
+// exclusive prefix over chunks per expert with the tile table (one workgroup), the stable
+// scatter (one wave per chunk).  The histograms live in the caller's workspace (int32
+// [chunks][64], then the 64 expert starts).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(1024) void bucket_hist_kernel(const int32_t* __restrict__ ids, int R,
+                                                           int32_t* __restrict__ hist) {
+  __shared__ int cnt[16][kE];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int c = blockIdx.x * 16 + wv, nchunks = (R + 63) / 64;
+  const bool live = c < nchunks;  // per wave
+  int e = kE, before = 0;
+  bool last = false;
+  if (live) before = route_rank(ids, c * 64 + lane, R, lane, e, last);
+  cnt[wv][lane] = 0;
+  __syncthreads();  // the lanes' count writes below land after every zero
+  if (live && c * 64 + lane < R && last) cnt[wv][e] = before + 1;
+  __syncthreads();
+  if (live) hist[(int64_t)c * kE + lane] = cnt[wv][lane];
+}
+
+__global__ __launch_bounds__(1024) void bucket_scan_kernel(int R, int tile_tokens, int32_t* __restrict__ hist,
+                                                           int32_t* __restrict__ tiles, int32_t* __restrict__ num_tiles) {
+  __shared__ int start[kE], tstart[kE], total[kE];
+  __shared__ int segtot[16][kE];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int nchunks = (R + 63) / 64;
+  {
+    // wave wv owns a segment of the chunks for all 64 experts (lane = expert): its counts are
+    // requested at once (coalesced rows of hist), the segments' totals meet in LDS
+    constexpr int kSegMax = kMaxChunks / 16;
+    const int seg = (nchunks + 15) / 16, c0 = wv * seg;
+    int v[kSegMax];
+#pragma unroll
+    for (int k = 0; k < kSegMax; ++k) {  // unconditional loads (clamped rows), masked values
+      const int c = c0 + k;
+      const int x = hist[(int64_t)min(c, max(nchunks - 1, 0)) * kE + lane];
+      v[k] = (k < seg && c < nchunks) ? x : 0;
+    }
+    int loc = 0;
+#pragma unroll
+    for (int k = 0; k < kSegMax; ++k) loc += v[k];
+    segtot[wv][lane] = loc;
+    __syncthreads();
+    int run = 0, all = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int t = segtot[j][lane];
+      run += j < wv ? t : 0;
+      all += t;
+    }
+#pragma unroll
+    for (int k = 0; k < kSegMax; ++k) {
+      const int c = c0 + k;
+      if (k < seg && c < nchunks) hist[(int64_t)c * kE + lane] = run;
+      run += v[k];
+    }
+    if (wv == 0) total[lane] = all;
+  }
+  __syncthreads();
+  if (wv == 0) {
+    const int tot = total[lane];
+    const int nt = (tot + tile_tokens - 1) / tile_tokens;
+    int incl = tot, tincl = nt;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int a = __shfl_up(incl, o, 64), bt = __shfl_up(tincl, o, 64);
+      if (lane >= o) {
+        incl += a;
+        tincl += bt;
+      }
+    }
+    start[lane] = incl - tot;
+    tstart[lane] = tincl - nt;
+    hist[(int64_t)nchunks * kE + lane] = incl - tot;  // the expert starts, for the scatter
+    if (lane == 63) num_tiles[0] = tincl;
+  }
+  __syncthreads();
+  for (int e = wv; e < kE; e += 16) {
+    const int tot = total[e];
+    const int nt = (tot + tile_tokens - 1) / tile_tokens;
+    for (int i = lane; i < nt; i += 64) {
+      int4 t;
+      t.x = e;
+      t.y = start[e] + i * tile_tokens;
+      t.z = min(tile_tokens, tot - i * tile_tokens);
+      t.w = 0;
+      reinterpret_cast<int4*>(tiles)[tstart[e] + i] = t;
+    }
+  }
+}
+
+__global__ __launch_bounds__(1024) void bucket_scatter_kernel(const int32_t* __restrict__ ids, int R,
+                                                              const int32_t* __restrict__ hist,
+                                                              int32_t* __restrict__ sorted_routes,
+                                                              int32_t* __restrict__ route_pos) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int c = blockIdx.x * 16 + wv, nchunks = (R + 63) / 64;
+  if (c >= nchunks) return;
+  const int r = c * 64 + lane;
+  int e;
+  bool last;
+  const int before = route_rank(ids, r, R, lane, e, last);
+  if (r < R) {
+    const int p = hist[(int64_t)nchunks * kE + e] + hist[(int64_t)c * kE + e] + before;
+    sorted_routes[p] = r;
+    route_pos[r] = p;
+  }
+}
+
+extern "C" int64_t dsv2_moe_bucket_workspace_size(int rows) {
+  const int64_t nchunks = ((int64_t)max(rows, 0) * kTopK + 63) / 64;
+  return (nchunks + 1) * kE * (int64_t)sizeof(int32_t);
+}
+
+extern "C" int dsv2_moe_bucket_wide(const int32_t* ids, int rows, int tile_tokens, int32_t* sorted_routes,
+                                    int32_t* route_pos, int32_t* tiles, int32_t* num_tiles, void* workspace,
+                                    int64_t workspace_bytes, void* stream) {
+  DSV2_REQUIRE(ids && sorted_routes && route_pos && tiles && num_tiles && workspace, DSV2_E_NULL,
+               "moe_bucket_wide: null pointer");
+  DSV2_REQUIRE(rows >= 0 && rows * kTopK <= kMaxRoutes && tile_tokens >= 1 && tile_tokens <= 256, DSV2_E_SHAPE,
+               "moe_bucket_wide: rows*6 must be <= %d (got %d)", kMaxRoutes, rows * kTopK);
+  DSV2_REQUIRE(workspace_bytes >= dsv2_moe_bucket_workspace_size(rows), DSV2_E_SHAPE,
+               "moe_bucket_wide: workspace of %lld bytes, %lld needed", (long long)workspace_bytes,
+               (long long)dsv2_moe_bucket_workspace_size(rows));
+  DSV2_REQUIRE(dsv2_aligned16(tiles) && dsv2_aligned16(workspace), DSV2_E_ALIGN, "moe_bucket_wide: alignment");
+  const int R = rows * kTopK, nchunks = (R + 63) / 64;
+  int32_t* hist = reinterpret_cast<int32_t*>(workspace);
+  const int groups = (nchunks + 15) / 16;
+  hipStream_t st = (hipStream_t)stream;
+  if (groups > 0) hipLaunchKernelGGL(bucket_hist_kernel, dim3(groups), dim3(1024), 0, st, ids, R, hist);
+  hipLaunchKernelGGL(bucket_scan_kernel, dim3(1), dim3(1024), 0, st, R, tile_tokens, hist, tiles, num_tiles);
+  if (groups > 0)
+    hipLaunchKernelGGL(bucket_scatter_kernel, dim3(groups), dim3(1024), 0, st, ids, R, hist, sorted_routes, route_pos);
+  return dsv2_launch_status("moe_bucket_wide");
+}
+
+// ---------------------------------------------------------------------------
 // combine: one workgroup per token (256 threads x 8 elements)
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void moe_combine_kernel(const bf16_t* __restrict__ ys,

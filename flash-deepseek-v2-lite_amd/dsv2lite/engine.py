@@ -43,6 +43,9 @@ FUSED_MLA_MAX_CTX = 2048
 SPLIT_ROUTER_MAX_ROWS = 64
 # from this many rows (prefill chunks) the router runs as RMSNorm + an MFMA logits GEMM + top-6
 GEMM_ROUTER_MIN_ROWS = 1024
+# prefill chunks from this many rows bucket their routes over many workgroups (one workgroup
+# is VALU-bound there: 8192 rows 74 us, against three short launches)
+WIDE_BUCKET_MIN_ROWS = 1024
 # grouped MoE: from this many routes in a launch the 256-token tiles (256 x 256 ring GEMM, one
 # MFMA per 384 B of LDS reads) beat the 64-token ones.  The crossover follows the launch's
 # routes rather than their spread over the experts: measured on MI355X, routed gate_up + down,
@@ -159,6 +162,9 @@ class RowBuffers:
             self.shmid = e(rows, cfg.shared_inter)
             self.shout = e(rows, H)
             self.shparts = e(2, rows, H, dt=torch.float32)  # shared down halves (64-token tiles)
+            # per-chunk route histograms of dsv2_moe_bucket_wide (prefill chunks)
+            self.bucket_ws = (e(_hip.lib.dsv2_moe_bucket_workspace_size(rows), dt=torch.uint8)
+                              if prefill and rows >= WIDE_BUCKET_MIN_ROWS else None)
 
 
     def set_tile_tokens(self, tile_tokens: int) -> None:
@@ -378,8 +384,12 @@ class DecodeEngine:
             else:
                 call("dsv2_router_topk6", ptr(b.h), H, ptr(L.ln_post), c.eps, ptr(L.w_router), c.routed_scaling, R,
                      ptr(b.xn), ptr(b.ids32), None, ptr(b.wts), st)
-            call("dsv2_moe_bucket", ptr(b.ids32), R, b.tile_tokens, ptr(b.sorted), ptr(b.route_pos), ptr(b.tiles),
-                 ptr(b.ntiles), st)
+            if b.bucket_ws is not None and R >= WIDE_BUCKET_MIN_ROWS:
+                call("dsv2_moe_bucket_wide", ptr(b.ids32), R, b.tile_tokens, ptr(b.sorted), ptr(b.route_pos),
+                     ptr(b.tiles), ptr(b.ntiles), ptr(b.bucket_ws), b.bucket_ws.numel(), st)
+            else:
+                call("dsv2_moe_bucket", ptr(b.ids32), R, b.tile_tokens, ptr(b.sorted), ptr(b.route_pos),
+                     ptr(b.tiles), ptr(b.ntiles), st)
             if shared_in_grouped(R, b.tile_tokens):
                 # the shared experts' two halves ride in the grouped launches as extra tiles
                 call("dsv2_moe_grouped_gateup_shared", ptr(b.xn), R, ptr(b.sorted), ptr(b.tiles), ptr(b.ntiles),

@@ -67,6 +67,8 @@ _SIGS = {
     "dsv2_moe_route_gateup": ([_p, _i32, _p, _p, _p, _i32, _p, _p], _i32),
     "dsv2_moe_route_down": ([_p, _i32, _p, _p, _p, _p, _i32, _i32, _p, _p, _p, _p], _i32),
     "dsv2_moe_bucket": ([_p, _i32, _i32, _p, _p, _p, _p, _p], _i32),
+    "dsv2_moe_bucket_workspace_size": ([_i32], _i64),
+    "dsv2_moe_bucket_wide": ([_p, _i32, _i32, _p, _p, _p, _p, _p, _i64, _p], _i32),
     "dsv2_moe_grouped_gateup": ([_p, _p, _p, _p, _i32, _i32, _p, _i32, _p, _p], _i32),
     "dsv2_moe_grouped_gateup_shared": ([_p, _i32, _p, _p, _p, _i32, _i32, _p, _p, _i32, _p, _p, _p], _i32),
     "dsv2_moe_grouped_down": ([_p, _p, _p, _i32, _i32, _p, _i32, _p, _p], _i32),

@@ -361,6 +361,16 @@ int dsv2_moe_route_down_fp8(const void* hbuf, int rows, const int32_t* ids, cons
 int dsv2_moe_bucket(const int32_t* ids, int rows, int tile_tokens, int32_t* sorted_routes, int32_t* route_pos,
                     int32_t* tiles, int32_t* num_tiles, void* stream);
 
+/* dsv2_moe_bucket over many workgroups, for the route counts of prefill chunks: the same
+ * outputs bit for bit, in three launches (per-chunk histograms, the exclusive prefix over
+ * chunks with the tile table, the stable scatter), the per-chunk histograms in the caller's
+ * workspace of dsv2_moe_bucket_workspace_size(rows) bytes (16-byte aligned); rows*6 <= 49152
+ * as for dsv2_moe_bucket.  Replaces _build_route_indices_kernel + _build_route_blocks_kernel
+ * (moe_batch.py:95-148). */
+int64_t dsv2_moe_bucket_workspace_size(int rows);
+int dsv2_moe_bucket_wide(const int32_t* ids, int rows, int tile_tokens, int32_t* sorted_routes, int32_t* route_pos,
+                         int32_t* tiles, int32_t* num_tiles, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* Expert-grouped gate_up + SwiGLU on bf16 MFMA over the tiles of dsv2_moe_bucket:
  *   hsorted[p, :inter] for p in tile = SwiGLU(xn[sorted_routes[p]/6] . W_e^T).
  * tile_tokens 16, 32, 64 or 256 (256: inter % 128 == 0).

@@ -317,6 +317,44 @@ def test_moe_bucket_invariants(rows, tile):
     assert torch.all(covered == 1)
 
 
+@pytest.mark.parametrize("rows,tile", [(1, 16), (37, 32), (1000, 64), (4096, 256), (8192, 256),
+                                       (8192, 64)])
+def test_moe_bucket_wide_equals_one_workgroup(rows, tile):
+    """dsv2_moe_bucket_wide (three launches, workspace histograms) gives dsv2_moe_bucket's
+    outputs bit for bit -- sorted routes, route positions, tile table and count -- at every
+    size up to the 49,152 routes of an 8,192-row prefill chunk, with a hot expert spanning
+    many chunks; a workspace one byte short is rejected."""
+    g = torch.Generator().manual_seed(rows + tile)
+    ids = torch.randint(0, 64, (rows, 6), generator=g, dtype=torch.int32)
+    if rows >= 1000:
+        ids[: rows // 3, 0] = 11
+    d = ids.to(DEV)
+    R = rows * 6
+    max_tiles = math.ceil(R / tile) + 64
+    outs = []
+    for wide in (False, True):
+        sr = torch.full((R,), -1, dtype=torch.int32, device=DEV)
+        rp = torch.full((R,), -1, dtype=torch.int32, device=DEV)
+        tl = torch.full((max_tiles, 4), -1, dtype=torch.int32, device=DEV)
+        nt = torch.full((1,), -1, dtype=torch.int32, device=DEV)
+        if wide:
+            nb = _hip.lib.dsv2_moe_bucket_workspace_size(rows)
+            ws = torch.empty(nb, dtype=torch.uint8, device=DEV)
+            with pytest.raises(_hip.HipKernelError):
+                call("dsv2_moe_bucket_wide", d.data_ptr(), rows, tile, sr.data_ptr(), rp.data_ptr(), tl.data_ptr(),
+                     nt.data_ptr(), ws.data_ptr(), nb - 1, st())
+            call("dsv2_moe_bucket_wide", d.data_ptr(), rows, tile, sr.data_ptr(), rp.data_ptr(), tl.data_ptr(),
+                 nt.data_ptr(), ws.data_ptr(), nb, st())
+        else:
+            call("dsv2_moe_bucket", d.data_ptr(), rows, tile, sr.data_ptr(), rp.data_ptr(), tl.data_ptr(),
+                 nt.data_ptr(), st())
+        n = int(nt.item())
+        outs.append((sr.cpu(), rp.cpu(), tl.cpu()[:n], n))
+    (a_sr, a_rp, a_tl, a_n), (b_sr, b_rp, b_tl, b_n) = outs
+    assert a_n == b_n and torch.equal(a_tl, b_tl)
+    assert torch.equal(a_sr, b_sr) and torch.equal(a_rp, b_rp)
+
+
 def _moe_layer(seed):
     gu = rnd(64, 2 * 1408, 2048, std=0.02, seed=seed)
     dn = rnd(64, 2048, 1408, std=0.02, seed=seed + 1)
