@@ -128,14 +128,20 @@ __device__ __forceinline__ void att_finish(AttTok (&ta)[kAttTB], AttTok (&tb)[kA
   R.l = 0.f;
 #pragma unroll
   for (int i = 0; i < 32; ++i) R.o[i] = 0.f;
-  // every load is issued unconditionally (past the end the rows are clamped and masked), so
-  // the same loads are pending at every loop entry and each wait is for one batch
-  for (int t0 = 0; t0 < n; t0 += 2 * kAttStep) {
-    att_consume(R, ta, qc, qr, t0 + tw + rg, n, scale_log2);
-    att_load(ta, crow0, t0 + 2 * kAttStep, n_ld, wv, li, rg);
-    if (t0 + kAttStep < n) att_consume(R, tb, qc, qr, t0 + kAttStep + tw + rg, n, scale_log2);
-    att_load(tb, crow0, t0 + 3 * kAttStep, n_ld, wv, li, rg);
-  }
+  // inside the loop every load is issued unconditionally (past the end the rows are clamped
+  // and masked), so the same loads are pending at every loop entry and each wait is for one
+  // batch; the last pass leaves before loading batches no pass would consume
+  if (n > 0)
+    for (int t0 = 0;; t0 += 2 * kAttStep) {
+      att_consume(R, ta, qc, qr, t0 + tw + rg, n, scale_log2);
+      if (t0 + 2 * kAttStep >= n) {
+        if (t0 + kAttStep < n) att_consume(R, tb, qc, qr, t0 + kAttStep + tw + rg, n, scale_log2);
+        break;
+      }
+      att_load(ta, crow0, t0 + 2 * kAttStep, n_ld, wv, li, rg);
+      att_consume(R, tb, qc, qr, t0 + kAttStep + tw + rg, n, scale_log2);
+      att_load(tb, crow0, t0 + 3 * kAttStep, n_ld, wv, li, rg);
+    }
   if (xt && wv == 0 && rg == 0) {  // the extra token, in row 0
     AttTok t;
 #pragma unroll
