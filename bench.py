@@ -106,6 +106,19 @@ def time_dominant_kernel(eng, family: str, reps: int = 4) -> dict:
         def launch(L):
             call("dsv2_moe_route_gateup", ptr(b.xn), B, ptr(b.ids32), ptr(L.w_gu), ptr(L.sh_gu), c.moe_inter,
                  ptr(b.hbuf), stream_ptr())
+    elif eng.expert_dtype == "fp8":
+        sym = {32: "gemm_f8_kernel<true, 16, 4>", 64: "gemm_f8_kernel<true, 32, 4>"}[b.tile_tokens]
+        n_exp = int(torch.unique(b.ids32[:B]).numel())
+        # e4m3 weights (1 B) + one fp32 scale per weight row, routed and shared; bf16 outputs
+        bytes_per = (n_exp * 2 * c.moe_inter + 2 * c.shared_inter) * (c.hidden + 4) + (B * 6 * c.moe_inter
+                                                                                      + B * c.shared_inter) * 2
+        name = (f"{sym} via dsv2_moe_grouped_gateup_shared_fp8 (expert-grouped gate_up+SwiGLU on e4m3 weights, "
+                f"{b.tile_tokens}-token tiles, + the 2 shared-expert halves)")
+
+        def launch(L):
+            call("dsv2_moe_grouped_gateup_shared_fp8", ptr(b.xn), B, ptr(b.sorted), ptr(b.tiles), ptr(b.ntiles),
+                 b.max_tiles, b.tile_tokens, ptr(L.w_gu8), ptr(L.gu_scale), ptr(L.sh_gu8), ptr(L.sh_gu_scale),
+                 c.moe_inter, ptr(b.hs), ptr(b.shmid), stream_ptr())
     else:
         from dsv2lite.engine import shared_in_grouped
 
@@ -241,21 +254,27 @@ def time_other_kernels(eng, family: str, ctx_rows: list[int]) -> dict:
         return out
     n_exp = int(torch.unique(b.ids32[:B]).numel())
     R = B * c.top_k
-    shared = shared_in_grouped(B, b.tile_tokens)
+    fp8 = eng.expert_dtype == "fp8"
+    shared = fp8 or shared_in_grouped(B, b.tile_tokens)
 
     def down(li):
         L = eng.w.layers[li]
-        if shared:
+        if fp8:
+            call("dsv2_moe_grouped_down_shared_fp8", ptr(b.hs), B, ptr(b.tiles), ptr(b.ntiles), b.max_tiles,
+                 b.tile_tokens, ptr(L.w_down8), ptr(L.down_scale), ptr(b.shmid), ptr(L.sh_down8),
+                 ptr(L.sh_down_scale), c.moe_inter, ptr(b.ys), ptr(b.shparts), stream_ptr())
+        elif shared:
             call("dsv2_moe_grouped_down_shared", ptr(b.hs), B, ptr(b.tiles), ptr(b.ntiles), b.max_tiles,
                  b.tile_tokens, ptr(L.w_down), ptr(b.shmid), ptr(L.sh_down), c.moe_inter, ptr(b.ys), ptr(b.shparts),
                  stream_ptr())
         else:
             call("dsv2_moe_grouped_down", ptr(b.hs), ptr(b.tiles), ptr(b.ntiles), b.max_tiles, b.tile_tokens,
                  ptr(L.w_down), c.moe_inter, ptr(b.ys), stream_ptr())
-    nb = n_exp * 2048 * 1408 * 2 + R * 1408 * 2 + R * 2048 * 2
+    wb = 1 if fp8 else 2  # bytes per weight (e4m3 rows add one fp32 scale each)
+    nb = n_exp * 2048 * (1408 * wb + (4 if fp8 else 0)) + R * 1408 * 2 + R * 2048 * 2
     if shared:
-        nb += 2048 * c.shared_inter * 2 + B * c.shared_inter * 2 + 2 * B * 2048 * 4
-    entry("expert-grouped down" + (" + the 2 shared-expert halves" if shared else "")
+        nb += 2048 * (c.shared_inter * wb + (4 if fp8 else 0)) + B * c.shared_inter * 2 + 2 * B * 2048 * 4
+    entry("expert-grouped down" + (" on e4m3 weights" if fp8 else "") + (" + the 2 shared-expert halves" if shared else "")
           + f" ({b.tile_tokens}-token tiles)", down, moe, nb)
 
     if b.max_splits == 1:
@@ -574,6 +593,60 @@ def bench_mla_micro(args) -> dict:
     return out
 
 
+def device_copy_gbps(dev, nbytes: int = 2**30, reps: int = 10) -> dict:
+    """Measured device copy bandwidth (a plain HBM-to-HBM tensor copy, read + write bytes per
+    second), the practical ceiling the step fractions are also quoted against: a graph of
+    `reps` copies of `nbytes` between HIP events, best of three replays."""
+    src = torch.empty(nbytes // 2, dtype=torch.float16, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            dst.copy_(src)
+    g.replay()
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(3):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        best = min(best, e0.elapsed_time(e1) / 1e3)
+    del src, dst, g
+    torch.cuda.empty_cache()
+    return {"GBps": 2 * nbytes * reps / best / 1e9, "bytes_per_copy": nbytes, "copies": reps,
+            "how": "torch tensor copy (read + write bytes), graph of 10 x 1 GiB, best of 3"}
+
+
+def in_step_timing(profile: str, kernel: str) -> dict | None:
+    """The dominant kernel's average duration inside the graph-replayed step, from the
+    committed rocprofv3 step trace (its one-step section), with the source sha the trace was
+    recorded on -- beside the live isolated-graph timing of `roofline.avg_us`."""
+    path = os.path.join(ROOT, "profiles", profile)
+    if not os.path.exists(path):
+        return None
+    sym = kernel.split(" via ")[0].split(" (")[0].strip()
+    in_step = False
+    for ln in open(path):
+        if ln.startswith("## One decode step"):
+            in_step = True
+        elif ln.startswith("## "):
+            in_step = False
+        elif in_step and ln.startswith(f"| `{sym}` |"):  # | kernel | calls/step | us/step |
+            cells = [c.strip() for c in ln.strip().strip("|").split("|")]
+            try:
+                calls, us = int(cells[1]), float(cells[2])
+            except (IndexError, ValueError):
+                return None
+            return {"avg_us": us / calls, "launches_per_step": calls, "profile": f"profiles/{profile}"}
+    return None
+
+
 def _copy_calibration(out: dict, dev) -> None:
     """Three plain 512 MiB device copies at the end of the run: the PMC byte counters of a
     copy of known size scale the dominant kernel's (--pmc-traffic)."""
@@ -631,6 +704,12 @@ def cpu_baseline(max_seconds: float = 30.0) -> dict:
                        f"t_dense={t_dense * 1e3:.1f} ms, t_head={t_head * 1e3:.1f} ms; oracle bf16-rounded fp32 math")}
 
 
+# committed rocprofv3 step traces per config (bench.py --summarize-trace)
+STEP_PROFILES = {1: "decode_step_c1_small_bsz1.md", 2: "decode_step_c2_batch_bsz64.md",
+                 3: "decode_step_c3_batch_bsz256.md", "r64": "decode_step_r64_reference_workload_bsz64.md",
+                 "r256": "decode_step_r256_reference_workload_bsz256.md"}
+
+
 def _log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -686,6 +765,11 @@ def run_config(key, w, args, cfg, dev, expert_dtype: str = "bf16") -> dict:
     _log(f"config {key}: timed {steps} graph replays: {ms:.3f} ms/step, {value:.1f} tok/s")
     roof = time_dominant_kernel(eng, family)
     roof["traffic"], roof["traffic_source"] = measured_traffic(key, roof["kernel"])
+    prof = STEP_PROFILES.get(key) if expert_dtype == "bf16" else None
+    ins = in_step_timing(prof, roof["kernel"]) if prof else None
+    if ins:  # the same kernel inside the replayed step (committed trace) beside the live isolated timing
+        ins["frac"] = roof["bytes_per_launch"] / (ins["avg_us"] * 1e-6) / HBM_PEAK
+        roof["in_step"] = ins
     pos_now = eng.cache.pos.cpu().tolist()
     others = time_other_kernels(eng, family, [p + 1 for p in pos_now])
     res = {"workload": spec["workload"] + (", e4m3 expert weights" if expert_dtype == "fp8" else ""),
@@ -714,7 +798,7 @@ def main() -> None:
                          "'configs'; N: that config alone")
     ap.add_argument("--family", choices=("small", "batch"), default=None)
     ap.add_argument("--expert-dtype", choices=("bf16", "fp8"), default="bf16",
-                    help="one config: MoE expert weights in bf16 or e4m3 (small family); 'all' runs C1 both ways")
+                    help="one config: MoE expert weights in bf16 or e4m3; 'all' runs C1-C3 both ways")
     ap.add_argument("--mla-path", choices=("fused", "spread", "split", "absorb"), default="absorb",
                     help="small family: the absorption in the q|kv_a projection + one attention launch "
                          "(absorb), prepare + spread attention (two launches), one fused MLA kernel per "
@@ -788,15 +872,31 @@ def main() -> None:
     if args.config == "all":
         # the metric's other two batch sizes, timed in the same run on the same weights
         out["configs"] = {}
-        for key in (2, 3):
+        # the metric's other two batch sizes, then the reference's own published workload (one
+        # prompt replicated over the batch; vs_published_a100 = tok/s / the published A100 figure)
+        for key, name in ((2, "C2"), (3, "C3"), ("r64", "r64"), ("r256", "r256")):
             rk = run_config(key, w, args, cfg, dev)
-            out["configs"][f"C{key}"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in rk.items()}
-        # config 1 again with the MoE expert weights in e4m3 (per-row power-of-two scales);
-        # quantizing rewrites the bf16 experts with their dequantized values, so it runs last
+            out["configs"][name] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in rk.items()}
+        # benchmark config 4, the isolated absorbed-MLA decode microbenchmark (its own inputs)
+        a4 = argparse.Namespace(**vars(args))
+        a4.no_cpu_baseline, a4.copy_calibration = True, False
+        c4 = bench_mla_micro(a4)
+        out["configs"]["C4"] = {k: c4[k] for k in ("metric", "value", "unit", "ms_per_step", "config", "roofline")}
+        # configs 1-3 again with the MoE expert weights in e4m3 (per-row power-of-two scales);
+        # quantizing rewrites the bf16 experts with their dequantized values, so they run last
         _log("quantizing expert weights to e4m3")
         dsv2lite.quantize_experts_fp8(w)
-        rk = run_config(1, w, args, cfg, dev, expert_dtype="fp8")
-        out["configs"]["C1_fp8"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in rk.items()}
+        for key in (1, 2, 3):
+            rk = run_config(key, w, args, cfg, dev, expert_dtype="fp8")
+            out["configs"][f"C{key}_fp8"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in rk.items()}
+    # the measured device copy bandwidth and each step's fraction of it (beside the 8 TB/s peak)
+    cp = device_copy_gbps(dev)
+    out["copy_GBps"] = round(cp["GBps"], 1)
+    out["copy"] = cp
+    for r in [out] + list(out.get("configs", {}).values()):
+        sr = r.get("step_roofline")
+        if sr:
+            sr["frac_of_copy"] = sr["achieved_GBps"] / cp["GBps"]
     if args.copy_calibration:
         _copy_calibration(out, dev)
     if not args.no_cpu_baseline:

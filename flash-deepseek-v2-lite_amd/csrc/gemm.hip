@@ -28,6 +28,7 @@ struct GemmArgs {
   void* Y;
   int64_t ys, yg;
   bool out_f32;
+  bool exact_f32;  // out_f32 without the bf16 round of the accumulator (router logits)
   // grouped launches: the shared-expert halves (a token tile of the launch's size per chunk
   // of `rows` and half, ahead of the table's tiles): half h reads token t at
   // X2 + h*x2g + t*x2s, its (gate) weight rows at W2 + h*w2g with row stride w2ld (SwiGLU:
@@ -40,7 +41,17 @@ struct GemmArgs {
   int w2ld, w2up, s_tiles;
   void* Y2;
   int64_t y2s, y2g;
+  // e4m3 weights (gemm_f8_kernel: W / W2 then hold e4m3 bytes): fp32 power-of-two scale of
+  // weight row R of group g at S[g * sg + R] (shared half h: S2[h * s2g + R])
+  const float* S;
+  int64_t sg;
+  const float* S2;
+  int64_t s2g;
 };
+
+// A plain (non-SwiGLU) output before its residual add / store: the bf16 round of the fp32
+// accumulator, or the accumulator itself for an exact fp32 output.
+__device__ __forceinline__ float acc_out(const GemmArgs& a, float acc) { return a.exact_f32 ? acc : rbf(acc); }
 
 template <int TB, bool SWIGLU, int NW, int U>
 __global__ __launch_bounds__(NW * 64) void gemm_kernel(const GemmArgs a) {
@@ -126,7 +137,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_kernel(const GemmArgs a) {
     const int n = n0 + 4 * kg;
     float v[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = SWIGLU ? swiglu_bf(sum[0][e], sum[R - 1][e]) : rbf(sum[0][e]);
+    for (int e = 0; e < 4; ++e) v[e] = SWIGLU ? swiglu_bf(sum[0][e], sum[R - 1][e]) : acc_out(a, sum[0][e]);
     if (a.res) {
       const uint2 r2 = *reinterpret_cast<const uint2*>(a.res + slot * a.rs + n);
       v[0] = rbf(__uint_as_float(r2.x << 16) + v[0]);
@@ -350,7 +361,7 @@ __global__ __launch_bounds__(512) void gemm_xlds_kernel(const GemmArgs a) {
     const int n = f0 + 4 * kg;
     float v[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = SWIGLU ? swiglu_bf(acc[0][tb][e], acc[R - 1][tb][e]) : rbf(acc[0][tb][e]);
+    for (int e = 0; e < 4; ++e) v[e] = SWIGLU ? swiglu_bf(acc[0][tb][e], acc[R - 1][tb][e]) : acc_out(a, acc[0][tb][e]);
     if (shared) {  // SwiGLU: bf16 row of the half's output; plain: the fp32 partial sum
       if (SWIGLU) {
         uint2 o;
@@ -654,7 +665,7 @@ __global__ __launch_bounds__(RWV * 128) void gemm_dma_kernel(const GemmArgs a, c
           }
           float v[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = rbf(acc[x][y][e]);
+          for (int e = 0; e < 4; ++e) v[e] = acc_out(a, acc[x][y][e]);
           gemm_store4(a, g, t0 + wt + 16 * y + li, f0 + wa + 16 * x + 4 * kg, v);
         }
     }
@@ -693,6 +704,277 @@ static void launch_dma(const GemmArgs& a, bool swiglu, hipStream_t st, int max_t
   }
   if (swiglu) hipLaunchKernelGGL(gemm_dma_kernel<true>, dim3(sh.nwg), dim3(256), kDmaStages * 16384, st, a, sh);
   else hipLaunchKernelGGL(gemm_dma_kernel<false>, dim3(sh.nwg), dim3(256), kDmaStages * 16384, st, a, sh);
+}
+
+// ---------------------------------------------------------------------------
+// Expert-grouped MoE GEMMs on e4m3 weights (per-row power-of-two scales), bf16 activations.
+// The shape of gemm_dma_kernel's decode form -- 4 waves, 64 weight rows x 2 WN tokens per
+// workgroup, direct-to-LDS rings, resident workgroups looping over the live (tile, feature
+// block) items, the shared-expert halves as extra tiles -- with the weight rows carried as
+// e4m3 bytes (a K chunk of a row takes KC bytes of LDS instead of 2 KC) in a ring of their own
+// (SW stages) beside the token ring (ST stages).
+// A lane reads 16 e4m3 weights of one row per 64-wide half chunk (ds_read_b128: bytes
+// 64 h + 16 kg .. + 15) and decodes them to two bf16 MFMA fragments (v_cvt_pk_f32_fp8, exact:
+// e4m3 values are bf16 values), one per 32-wide MFMA step: step s takes K {64 h + 16 kg + 8 s
+// .. + 7}, and the token fragments read the same K from their LDS rows.  The row's scale
+// multiplies the fp32 accumulator in the epilogue (a power of two: the products are those of
+// the dequantized bf16 weights).  The weight reads are native vector loads: as struct-typed
+// uint4 loads they carried no TBAA tag, and the compiler then made every one of them wait for
+// all ring loads in flight (vmcnt(0) each chunk: C3 gate_up 178 -> 128 us once fixed).
+// LDS weight rows of 64 B: piece p (16 B) of row r at slot p ^ ((r >> 1) & 3); of 128 B:
+// p ^ (r & 7) -- a 16-byte LDS read is served 8 lanes at a time over 32 four-byte banks, and
+// the 8 rows such a group reads then fill all 8 sixteen-byte bank groups (slot p ^ ((r >> 2)
+// & 3) left two rows on each: 9.7 M conflict cycles per launch at C3).
+// Ring shapes per tile size (measured on MI355X, gate_up + shared halves, 26 layers' weights):
+// 32-token tiles: 128-wide K chunks (8 KB of weights per stage), 3 weight + 3 token stages, 768
+// resident workgroups (3 per CU) -- 256 rows 105.6 us, 64 rows 76.5 us, against 114.5 / 92.8 us
+// with 64-wide chunks in 8 + 4 stages (2 per CU) and 152 / 131 us for the bf16 launches;
+// 64-token tiles: 64-wide chunks, 8 + 4 stages, 512 workgroups (256 rows 125.9 us; 128-wide
+// chunks need 96 KB of LDS there, one workgroup per CU, 160 us).
+constexpr int kF8Wgs32 = 768, kF8Wgs64 = 512;
+
+__device__ __forceinline__ uint32_t pack_hi16(float lo, float hi) {
+  // the bf16 of an fp32 holding an e4m3 value is its upper half (no rounding needed)
+  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+__device__ __forceinline__ bf16x8_t fp8x8_to_bf16x8(uint32_t w0, uint32_t w1) {
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  const f32x2_t a = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w0), false);
+  const f32x2_t b = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w0), true);
+  const f32x2_t c = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w1), false);
+  const f32x2_t d = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w1), true);
+  return as_bf16x8(make_uint4(pack_hi16(a[0], a[1]), pack_hi16(b[0], b[1]), pack_hi16(c[0], c[1]),
+                              pack_hi16(d[0], d[1])));
+}
+
+template <bool SWIGLU, int WN, int KC, int SW, int ST>
+__global__ __launch_bounds__(256) void gemm_f8_kernel(const GemmArgs a, const DmaShape sh) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, li = lane & 15, kg = lane >> 4;
+  constexpr int NW = 4, TM = 64, TN = 2 * WN;   // waves; weight rows, tokens per workgroup
+  constexpr int RW = KC, RB = 2 * KC;           // bytes per weight / token row per chunk (K = KC)
+  constexpr int WSB = TM * RW, TSB = TN * RB;   // weight / token stage bytes
+  constexpr int RLW = 1024 / RW, RLT = 1024 / RB;  // rows per 1 KB ring load: weights, tokens
+  constexpr int LW = TM / (RLW * NW), LT = TN / (RLT * NW);  // ring loads per wave per chunk
+  constexpr int LL = LW + LT;
+  constexpr int XM = 2, XN = WN / 16;           // MFMA blocks per wave (32 rows x WN tokens)
+  constexpr int FPW = SWIGLU ? TM / 2 : TM;     // output features per workgroup
+  static_assert((KC == 64 || KC == 128) && LW >= 1 && LW <= 2 && LT >= 1 && LT <= 4 && XN >= 1 && XN <= 4 &&
+                    SW % ST == 0, "shape");
+  // weight slot swizzle: 64-B rows p ^ ((r >> 1) & 3), 128-B rows p ^ (r & 7) (8 distinct per 8 rows)
+  auto wswz = [](int r) { return KC == 64 ? ((r >> 1) & 3) : (r & 7); };
+  const uint8_t* const W8 = reinterpret_cast<const uint8_t*>(a.W);
+  const uint8_t* const W28 = reinterpret_cast<const uint8_t*>(a.W2);
+  const int ns = a.W2 ? 2 * a.s_tiles : 0;
+  const int live = ns + min(a.ntiles[0], sh.tiles);
+  for (int it = 0;; ++it) {
+    const int j = blockIdx.x + it * gridDim.x;
+    if (j >= live * sh.nfb) break;
+    const int tile = j / sh.nfb, fb = j % sh.nfb;
+    int g, t0, count;
+    const bool shared = tile < ns;
+    if (shared) {  // a shared-expert half's tile of tokens
+      g = tile / a.s_tiles;
+      t0 = (tile % a.s_tiles) * TN;
+      count = min(TN, a.rows - t0);
+    } else {
+      const int4 tt = reinterpret_cast<const int4*>(a.tiles)[tile - ns];
+      g = tt.x;
+      t0 = tt.y;
+      count = tt.z;
+    }
+    const int f0 = fb * FPW;
+    const int K = a.K, nch = K / KC;
+    const uint8_t* const wbase = shared ? W28 + g * a.w2g : W8 + g * a.wg;
+    const int64_t wld = shared ? a.w2ld : K;
+    const int upoff = shared ? a.w2up : a.N;
+    const float* const sbase = shared ? a.S2 + g * a.s2g : a.S + g * a.sg;
+    // weight row of tile row r (SwiGLU: per 16 features 16 gate rows then the 16 up rows)
+    auto wrow = [&](int r) {
+      return SWIGLU ? f0 + (r >> 5) * 16 + ((r >> 4) & 1) * upoff + (r & 15) : min(f0 + r, a.N - 1);
+    };
+    // the epilogue's scales (rows wa + 16 x + 4 kg + e), requested before the stream
+    const int wa = (wv & 1) * 32, wt = (wv >> 1) * WN;
+    float sc[2][4];  // literal sizes: the host stub of the template is kept
+#pragma unroll
+    for (int x = 0; x < XM; ++x)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sc[x][e] = sbase[wrow(wa + 16 * x + 4 * kg + e)];
+    // ring loads: one of 16 weight rows x 64 B (lane -> row 16 wv + lane / 4, slot lane & 3),
+    // LT of 8 token rows x 128 B
+    // weight ring loads: LW of RLW rows x RW bytes (lane -> row, slot lane % (RW / 16))
+    const uint8_t* wsrc[2];
+#pragma unroll
+    for (int q = 0; q < LW; ++q) {
+      const int r = (TM / NW) * wv + RLW * q + lane / (RW / 16), slot = lane % (RW / 16);
+      wsrc[q] = wbase + (int64_t)wrow(r) * wld + (slot ^ wswz(r)) * 16;
+    }
+    const int wdst = (TM / NW) * wv * RW;
+    const uint8_t* tsrc[4];
+#pragma unroll
+    for (int q = 0; q < LT; ++q) {
+      const int r = (TN / NW) * wv + RLT * q + lane / (RB / 16), pc = (lane % (RB / 16)) ^ (r & 7);
+      const int slot = t0 + (r < count ? r : 0);  // rows past the tile: the tile's first row
+      const bf16_t* x;
+      if (shared) {
+        x = a.X2 + g * a.x2g + (int64_t)slot * a.x2s;
+      } else {
+        const int row = a.slot_row ? a.slot_row[slot] / a.slot_div : slot;
+        x = a.X + (int64_t)row * a.xs;
+      }
+      tsrc[q] = reinterpret_cast<const uint8_t*>(x + pc * 8);
+    }
+    const int tdst = ((TN / NW) * wv) * RB;
+#pragma unroll
+    for (int x = 0; x < XM; ++x)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pin(__float_as_uint(sc[x][e]));
+    // K chunks start at a rotation per (expert or half, feature block), as gemm_dma_kernel
+    const int rot = (int)((unsigned)(fb * 7 + g * 13 + (shared ? 3 : 0)) % (unsigned)nch);
+    auto chunk_of = [&](int c) {  // past the last chunk: repeat it (never multiplied)
+      int cc = min(c, nch - 1) + rot;
+      return cc >= nch ? cc - nch : cc;
+    };
+    auto issue_w = [&](int c, int stage) {
+      // (the chunk index in a local: with the call inside the builtin's argument hipcc drops
+      // the kernel's host launch stub)
+      const int cc = chunk_of(c);
+#pragma unroll
+      for (int q = 0; q < LW; ++q)
+        __builtin_amdgcn_global_load_lds(wsrc[q] + cc * RW,
+                                         (__attribute__((address_space(3))) void*)(lds + stage * WSB + wdst +
+                                                                                   RLW * q * RW),
+                                         16, 0, 0);
+    };
+    auto issue_t = [&](int c, int stage) {
+      const int cc = chunk_of(c);
+#pragma unroll
+      for (int q = 0; q < LT; ++q)
+        __builtin_amdgcn_global_load_lds(tsrc[q] + cc * RB,
+                                         (__attribute__((address_space(3))) void*)(lds + SW * WSB + stage * TSB + tdst +
+                                                                                   RLT * q * RB),
+                                         16, 0, 0);
+    };
+    floatx4_t acc[2][4];
+#pragma unroll
+    for (int x = 0; x < XM; ++x)
+#pragma unroll
+      for (int y = 0; y < XN; ++y) acc[x][y] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+    // iteration c issues W(c + SW - 1), then T(c + ST - 1); the prologue runs the iterations
+    // -(SW - 1) .. -1 of that schedule (a token chunk only from index 0), so before chunk c
+    // every wave has exactly (ST - 2) iterations of loads issued after T(c), and T(c) landing
+    // means W(c), issued before it, landed too (loads complete in issue order)
+#pragma unroll
+    for (int k = -(SW - 1); k < 0; ++k) {
+      issue_w(k + SW - 1, k + SW - 1);
+      if (k + ST - 1 >= 0) issue_t(k + ST - 1, k + ST - 1);
+    }
+    for (int c0 = 0; c0 < nch; c0 += SW) {
+#pragma unroll
+      for (int i = 0; i < SW; ++i) {
+        const int c = c0 + i;
+        if (c >= nch) break;
+        __builtin_amdgcn_s_waitcnt(vmcnt_only((ST - 2) * LL));
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        issue_w(c + SW - 1, (i + SW - 1) % SW);
+        issue_t(c + ST - 1, (i + ST - 1) % ST);
+        const uint8_t* ws = lds + i * WSB;
+        const uint8_t* ts = lds + SW * WSB + (i % ST) * TSB;
+#pragma unroll
+        for (int h = 0; h < KC / 64; ++h) {  // 64-wide halves of the chunk: one weight read, two MFMA steps
+          bf16x8_t af[2][2];
+#pragma unroll
+          for (int x = 0; x < XM; ++x) {
+            const int r = wa + 16 * x + li;
+            // a native vector load: it keeps its TBAA tag, which lets the compiler tell it apart
+            // from the ring loads in flight (as a struct-typed uint4 it waited for all of them)
+            const u32x4_t w = *reinterpret_cast<const u32x4_t*>(ws + r * RW + (((4 * h + kg) ^ wswz(r)) * 16));
+            af[0][x] = fp8x8_to_bf16x8(w[0], w[1]);
+            af[1][x] = fp8x8_to_bf16x8(w[2], w[3]);
+          }
+#pragma unroll
+          for (int s2 = 0; s2 < 2; ++s2) {
+            bf16x8_t bfr[4];
+#pragma unroll
+            for (int y = 0; y < XN; ++y) {
+              const int t = wt + 16 * y + li;
+              bfr[y] = *reinterpret_cast<const bf16x8_t*>(ts + t * RB + (((8 * h + 2 * kg + s2) ^ (t & 7)) * 16));
+            }
+#pragma unroll
+            for (int x = 0; x < XM; ++x)
+#pragma unroll
+              for (int y = 0; y < XN; ++y) acc[x][y] = mfma16x16x32(af[s2][x], bfr[y], acc[x][y]);
+          }
+        }
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+#pragma unroll
+    for (int x = 0; x < XM; ++x)
+#pragma unroll
+      for (int y = 0; y < XN; ++y)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[x][y][e] *= sc[x][e];
+    if (SWIGLU) {  // row block 0 of the wave holds 16 features' gate rows, block 1 their up rows
+#pragma unroll
+      for (int y = 0; y < XN; ++y) {
+        if (wt + 16 * y + li >= count) continue;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = swiglu_bf(acc[0][y][e], acc[1][y][e]);
+        const int n = f0 + (wa >> 1) + 4 * kg;
+        if (shared) {
+          uint2 o;
+          o.x = pack2(v[0], v[1]);
+          o.y = pack2(v[2], v[3]);
+          *reinterpret_cast<uint2*>(reinterpret_cast<bf16_t*>(a.Y2) + g * a.y2g + (int64_t)(t0 + wt + 16 * y + li) * a.y2s +
+                                    n) = o;
+        } else {
+          gemm_store4(a, g, t0 + wt + 16 * y + li, n, v);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int x = 0; x < XM; ++x)
+#pragma unroll
+        for (int y = 0; y < XN; ++y) {
+          if (wt + 16 * y + li >= count || f0 + wa + 16 * x >= a.N) continue;
+          if (shared) {  // fp32 partial of one half (the halves are summed by the consumer)
+            float* yp = reinterpret_cast<float*>(a.Y2) + g * a.y2g + (int64_t)(t0 + wt + 16 * y + li) * a.y2s + f0 +
+                        wa + 16 * x + 4 * kg;
+            *reinterpret_cast<float4*>(yp) = make_float4(acc[x][y][0], acc[x][y][1], acc[x][y][2], acc[x][y][3]);
+            continue;
+          }
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = rbf(acc[x][y][e]);
+          gemm_store4(a, g, t0 + wt + 16 * y + li, f0 + wa + 16 * x + 4 * kg, v);
+        }
+    }
+    __syncthreads();  // every wave is done with the rings before the next item refills them
+  }
+}
+
+// grouped e4m3 launch: 32- or 64-token tiles (WN 16 / 32), resident workgroups over the items
+static void launch_f8(const GemmArgs& a, bool swiglu, int tile_tokens, int max_tiles, hipStream_t st) {
+  DmaShape sh{};
+  sh.nfb = swiglu ? a.N / 32 : (a.N + 63) / 64;
+  sh.tiles = max_tiles;
+  if (tile_tokens == 64) {
+    constexpr int KC = 64, SW = 8, ST = 4;
+    sh.nwg = kF8Wgs64;
+    const int lds = SW * 64 * KC + ST * 64 * 2 * KC;
+    if (swiglu) hipLaunchKernelGGL((gemm_f8_kernel<true, 32, KC, SW, ST>), dim3(sh.nwg), dim3(256), lds, st, a, sh);
+    else hipLaunchKernelGGL((gemm_f8_kernel<false, 32, KC, SW, ST>), dim3(sh.nwg), dim3(256), lds, st, a, sh);
+  } else {
+    constexpr int KC = 128, SW = 3, ST = 3;
+    sh.nwg = kF8Wgs32;
+    const int lds = SW * 64 * KC + ST * 32 * 2 * KC;
+    if (swiglu) hipLaunchKernelGGL((gemm_f8_kernel<true, 16, KC, SW, ST>), dim3(sh.nwg), dim3(256), lds, st, a, sh);
+    else hipLaunchKernelGGL((gemm_f8_kernel<false, 16, KC, SW, ST>), dim3(sh.nwg), dim3(256), lds, st, a, sh);
+  }
 }
 
 // One-shot shape for dense weights and few tokens (the row blocks alone cannot fill the
@@ -817,7 +1099,7 @@ __global__ __launch_bounds__(1024) void gemm_os_kernel(const GemmArgs a, const O
     }
     float v[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = SWIGLU ? swiglu_bf(sum[0][e], sum[R - 1][e]) : rbf(sum[0][e]);
+    for (int e = 0; e < 4; ++e) v[e] = SWIGLU ? swiglu_bf(sum[0][e], sum[R - 1][e]) : acc_out(a, sum[0][e]);
     gemm_store4(a, g, start + tb * 16 + li, (rblk * sh.rbw + urb) * 16 + 4 * kg, v);
   }
 }
@@ -1004,9 +1286,12 @@ extern "C" int dsv2_gemm_bf16(const void* x, int64_t x_stride, int64_t x_gstride
   DSV2_REQUIRE(x && W && y, DSV2_E_NULL, "gemm: null pointer");
   DSV2_REQUIRE(rows >= 0 && K > 0 && K % 64 == 0 && N > 0 && N % 16 == 0 && n_groups >= 1, DSV2_E_SHAPE,
                "gemm: bad shape rows=%d K=%d N=%d groups=%d (K%%64, N%%16 required)", rows, K, N, n_groups);
-  DSV2_REQUIRE((flags & ~(DSV2_LINEAR_SWIGLU | DSV2_LINEAR_OUT_F32)) == 0, DSV2_E_FLAGS, "gemm: unknown flags");
+  DSV2_REQUIRE((flags & ~(DSV2_LINEAR_SWIGLU | DSV2_LINEAR_OUT_F32 | DSV2_LINEAR_OUT_F32_EXACT)) == 0, DSV2_E_FLAGS,
+               "gemm: unknown flags");
   DSV2_REQUIRE(!(residual && ((flags & DSV2_LINEAR_SWIGLU) || n_groups != 1)), DSV2_E_FLAGS,
                "gemm: residual needs a plain single-group GEMM");
+  DSV2_REQUIRE(!((flags & DSV2_LINEAR_OUT_F32_EXACT) && ((flags & DSV2_LINEAR_SWIGLU) || residual)), DSV2_E_FLAGS,
+               "gemm: the exact fp32 output takes no SwiGLU and no residual");
   DSV2_REQUIRE(dsv2_aligned16(x) && dsv2_aligned16(W) && x_stride % 8 == 0 && x_gstride % 8 == 0 &&
                    w_gstride % 8 == 0 && y_stride % 4 == 0 && y_gstride % 4 == 0 &&
                    (!residual || res_stride % 4 == 0),
@@ -1032,7 +1317,8 @@ extern "C" int dsv2_gemm_bf16(const void* x, int64_t x_stride, int64_t x_gstride
   a.Y = y;
   a.ys = y_stride;
   a.yg = y_gstride;
-  a.out_f32 = flags & DSV2_LINEAR_OUT_F32;
+  a.out_f32 = flags & (DSV2_LINEAR_OUT_F32 | DSV2_LINEAR_OUT_F32_EXACT);
+  a.exact_f32 = flags & DSV2_LINEAR_OUT_F32_EXACT;
   const bool swiglu = flags & DSV2_LINEAR_SWIGLU;
   if (launch_dense_os(a, n_groups, swiglu, (hipStream_t)stream)) return dsv2_launch_status("gemm");
   const int64_t grid_y = (int64_t)a.tiles_per_group * n_groups;
@@ -1199,4 +1485,99 @@ extern "C" int dsv2_moe_grouped_down(const void* hsorted, const int32_t* tiles, 
     return dsv2_launch_status("moe_grouped_down");
   }
   return launch_gemm(a, tile_tb(tile_tokens), false, max_tiles, (hipStream_t)stream);
+}
+
+// ---- e4m3 expert weights (batch family) ------------------------------------------------
+extern "C" int dsv2_moe_grouped_gateup_shared_fp8(const void* xn, int rows, const int32_t* sorted_routes,
+                                                  const int32_t* tiles, const int32_t* num_tiles, int max_tiles,
+                                                  int tile_tokens, const void* w_gate_up8, const float* gu_scale,
+                                                  const void* sh_gate_up8, const float* sh_gu_scale, int inter,
+                                                  void* hsorted, void* shared_out, void* stream) {
+  DSV2_REQUIRE(xn && sorted_routes && tiles && num_tiles && w_gate_up8 && gu_scale && sh_gate_up8 && sh_gu_scale &&
+                   hsorted && shared_out,
+               DSV2_E_NULL, "moe_grouped_gateup_shared_fp8: null pointer");
+  DSV2_REQUIRE(rows >= 0 && max_tiles >= 0 && max_tiles <= 65535 && inter > 0 && inter % 64 == 0 &&
+                   (tile_tokens == 32 || tile_tokens == 64),
+               DSV2_E_SHAPE, "moe_grouped_gateup_shared_fp8: bad shape (inter %% 64, tile_tokens in {32,64})");
+  DSV2_REQUIRE(dsv2_aligned16(xn) && dsv2_aligned16(w_gate_up8) && dsv2_aligned16(sh_gate_up8) &&
+                   dsv2_aligned16(tiles) && dsv2_aligned16(shared_out) && dsv2_aligned16(hsorted),
+               DSV2_E_ALIGN, "moe_grouped_gateup_shared_fp8: alignment");
+  if (rows == 0) return DSV2_OK;
+  GemmArgs a{};
+  a.X = (const bf16_t*)xn;
+  a.xs = 2048;
+  a.slot_row = sorted_routes;
+  a.slot_div = 6;
+  a.tiles = tiles;
+  a.ntiles = num_tiles;
+  a.rows = rows;
+  a.W = (const bf16_t*)w_gate_up8;  // e4m3 bytes: group and row strides below count bytes
+  a.wg = (int64_t)2 * inter * 2048;
+  a.N = inter;
+  a.K = 2048;
+  a.Y = hsorted;
+  a.ys = inter;
+  a.X2 = (const bf16_t*)xn;
+  a.x2s = 2048;
+  a.W2 = (const bf16_t*)sh_gate_up8;
+  a.w2g = (int64_t)inter * 2048;
+  a.w2ld = 2048;
+  a.w2up = 2 * inter;
+  a.s_tiles = (rows + tile_tokens - 1) / tile_tokens;
+  a.Y2 = shared_out;
+  a.y2s = 2 * inter;
+  a.y2g = inter;
+  a.S = gu_scale;
+  a.sg = 2 * inter;
+  a.S2 = sh_gu_scale;
+  a.s2g = inter;
+  launch_f8(a, true, tile_tokens, max_tiles, (hipStream_t)stream);
+  return dsv2_launch_status("moe_grouped_gateup_shared_fp8");
+}
+
+extern "C" int dsv2_moe_grouped_down_shared_fp8(const void* hsorted, int rows, const int32_t* tiles,
+                                                const int32_t* num_tiles, int max_tiles, int tile_tokens,
+                                                const void* w_down8, const float* down_scale, const void* shared_mid,
+                                                const void* sh_down8, const float* sh_down_scale, int inter,
+                                                void* ysorted, float* shared_parts, void* stream) {
+  DSV2_REQUIRE(hsorted && tiles && num_tiles && w_down8 && down_scale && shared_mid && sh_down8 && sh_down_scale &&
+                   ysorted && shared_parts,
+               DSV2_E_NULL, "moe_grouped_down_shared_fp8: null pointer");
+  DSV2_REQUIRE(rows >= 0 && max_tiles >= 0 && max_tiles <= 65535 && inter > 0 && inter % 64 == 0 &&
+                   (tile_tokens == 32 || tile_tokens == 64),
+               DSV2_E_SHAPE, "moe_grouped_down_shared_fp8: bad shape (inter %% 64, tile_tokens in {32,64})");
+  DSV2_REQUIRE(dsv2_aligned16(hsorted) && dsv2_aligned16(w_down8) && dsv2_aligned16(shared_mid) &&
+                   dsv2_aligned16(sh_down8) && dsv2_aligned16(tiles) && dsv2_aligned16(ysorted) &&
+                   dsv2_aligned16(shared_parts),
+               DSV2_E_ALIGN, "moe_grouped_down_shared_fp8: alignment");
+  if (rows == 0) return DSV2_OK;
+  GemmArgs a{};
+  a.X = (const bf16_t*)hsorted;
+  a.xs = inter;
+  a.slot_div = 1;
+  a.tiles = tiles;
+  a.ntiles = num_tiles;
+  a.rows = rows;
+  a.W = (const bf16_t*)w_down8;
+  a.wg = (int64_t)2048 * inter;
+  a.N = 2048;
+  a.K = inter;
+  a.Y = ysorted;
+  a.ys = 2048;
+  a.X2 = (const bf16_t*)shared_mid;
+  a.x2s = 2 * inter;
+  a.x2g = inter;
+  a.W2 = (const bf16_t*)sh_down8;
+  a.w2g = inter;
+  a.w2ld = 2 * inter;
+  a.s_tiles = (rows + tile_tokens - 1) / tile_tokens;
+  a.Y2 = shared_parts;
+  a.y2s = 2048;
+  a.y2g = (int64_t)rows * 2048;
+  a.S = down_scale;
+  a.sg = 2048;
+  a.S2 = sh_down_scale;
+  a.s2g = 0;  // the two halves split K: the same output rows, the same scales
+  launch_f8(a, false, tile_tokens, max_tiles, (hipStream_t)stream);
+  return dsv2_launch_status("moe_grouped_down_shared_fp8");
 }

@@ -260,15 +260,12 @@ __global__ __launch_bounds__(256, 2) void mla_decode_kernel(const bf16_t* __rest
     }
   };
 
-  // each workgroup walks its tiles from a rotated start (wrapping around): the ~256 rows
-  // streamed at once then read different phases of their cache instead of the same offset
-  // of rows laid out at one stride, which for some strides lands them on the same HBM
-  // channels (C3 at a 2,099-token capacity: 145 vs 100 us per layer).  Order does not
-  // matter to the softmax; every tile holds at least one live token.
-  const int rot = (int)((unsigned)(b * 7 + s * 3) % (unsigned)ntiles);
-  auto tile_t0 = [&](int it) {  // first token of the it-th tile walked; past the end: the last
-    it = min(it, ntiles - 1) + rot;
-    return t_begin + (it >= ntiles ? it - ntiles : it) * kTile;
+  // every workgroup walks its tiles in token order, whatever its row: the online softmax's
+  // rounding depends on the order, and rows holding the same sequence must give the same
+  // bits.  (Rows streamed together at one cache stride can camp on the same HBM channels;
+  // CompressedKVCache staggers the rows' bases against that.)
+  auto tile_t0 = [&](int it) {  // first token of tile it; past the end: the last tile
+    return t_begin + min(it, ntiles - 1) * kTile;
   };
   load_tile(0, tile_t0(0));
   load_tile(1, tile_t0(1));

@@ -1,7 +1,7 @@
 """Compressed MLA KV cache in HBM.
 
 Layout: one bf16 tensor [n_layers, total_tokens, 576]; sequence b owns rows
-[base[b], base[b] + capacity[b]) of every layer.  A row is the kv-normalised
+[base[b], base[b] + capacity[b]) of every layer (row starts staggered, see STAGGER_*).  A row is the kv-normalised
 512-d latent followed by the 64-d rotated k_pe (1,152 bytes per token per
 layer, vs. 10,240 for the reference's expanded K/V cache, src/run.py:81-99).
 
@@ -23,17 +23,32 @@ import torch
 
 DEVERR_CACHE_FULL = 1  # DSV2_DEVERR_CACHE_FULL of include/dsv2lite.h
 
+# Staggered row starts: the split-KV decode streams every row's cache tile by tile in token
+# order, all rows at once; with every row at one stride some strides put the rows' concurrent
+# reads on the same HBM channels (MI355X, bsz=256 x 2,049 cached tokens: a 2,099-token stride
+# 158 us per layer against 99-102 us for 2,081 / 2,089 / 2,112 / 2,158).  Row b therefore
+# starts (7 b mod 8) tiles of 32 tokens into a slot of capacity + 7 tiles (2,099 with the
+# stagger: 101 us; every stride measured stays at 99-102 us).  Caches of short rows skip it.
+STAGGER_TILE = 32
+STAGGER_PHASES = 8
+STAGGER_MIN_CAPACITY = 512
+
 
 class CompressedKVCache:
-    def __init__(self, n_layers: int, capacities: list[int], device="cuda", row: int = 576):
+    def __init__(self, n_layers: int, capacities: list[int], device="cuda", row: int = 576,
+                 stagger: bool | None = None):
         if not capacities or min(capacities) <= 0:
             raise ValueError("capacities must be positive")
         self.n_layers = n_layers
         self.capacities = list(int(c) for c in capacities)
-        bases = [0]
-        for c in self.capacities[:-1]:
-            bases.append(bases[-1] + c)
-        self.total = bases[-1] + self.capacities[-1]
+        if stagger is None:
+            stagger = max(self.capacities) >= STAGGER_MIN_CAPACITY
+        pad = (STAGGER_PHASES - 1) * STAGGER_TILE if stagger else 0
+        bases, start = [], 0
+        for b, c in enumerate(self.capacities):
+            bases.append(start + (((7 * b) % STAGGER_PHASES) * STAGGER_TILE if stagger else 0))
+            start += c + pad
+        self.total = start
         self.row = row
         self.data = torch.zeros(n_layers, self.total, row, dtype=torch.bfloat16, device=device)
         self.base = torch.tensor(bases, dtype=torch.int64, device=device)

@@ -26,7 +26,7 @@ import math
 import torch
 
 from triton_kernels import _hip
-from triton_kernels._hip import LINEAR_OUT_F32, LINEAR_SWIGLU, call, ptr
+from triton_kernels._hip import LINEAR_OUT_F32, LINEAR_OUT_F32_EXACT, LINEAR_SWIGLU, call, ptr
 from triton_kernels.attention_decode_batch import plan_splits
 
 from .cache import CompressedKVCache
@@ -93,31 +93,64 @@ def routing_load(ids: torch.Tensor, n_experts: int = 64) -> float:
 
 
 class PrefillPlan:
-    """One prefill chunk's attention work: the query tiles (<= 128 consecutive rows of one
-    sequence each: first row, rows, first position, the sequence's cache base) and the cache
-    rows [exp_lo, exp_lo + exp_rows) whose keys / values the chunk expands."""
+    """One prefill chunk's attention work, in groups of sequences: each group's query tiles
+    (<= 128 consecutive rows of one sequence each: first row, rows, first position, the
+    sequence's cache base) and the cache rows [exp_lo, exp_lo + exp_rows) whose keys / values
+    the group expands into kexp / vexp."""
 
-    def __init__(self, tiles: torch.Tensor, exp_lo: int, exp_rows: int, kexp: torch.Tensor, vexp: torch.Tensor):
-        self.tiles, self.n_tiles = tiles, int(tiles.shape[0])
-        self.exp_lo, self.exp_rows = exp_lo, exp_rows
+    def __init__(self, groups: list[tuple[torch.Tensor, int, int]], kexp: torch.Tensor, vexp: torch.Tensor):
+        self.groups = [(t, int(t.shape[0]), lo, n) for t, lo, n in groups]
         self.kexp, self.vexp = kexp, vexp
 
 
-def prefill_tiles(seq: torch.Tensor, posv: torch.Tensor, bases: list[int], tile: int = 128) -> tuple[torch.Tensor, int, int]:
-    """Query tiles of one chunk (seq[r]: sequence of chunk row r, posv[r]: its position;
-    rows of a sequence are consecutive with consecutive positions) and the cache row range
-    its attention reads: from the lowest sequence base to the last position of any row."""
+def _segments(seq: torch.Tensor) -> list[tuple[int, int, int]]:
+    """(first chunk row, rows, sequence) of each run of one sequence's rows in a chunk."""
     vals, counts = torch.unique_consecutive(seq, return_counts=True)
-    out, lo, hi, r = [], None, None, 0
+    out, r = [], 0
     for s, cnt in zip(vals.tolist(), counts.tolist()):
+        out.append((r, cnt, s))
+        r += cnt
+    return out
+
+
+def _group_tiles(segs, posv: torch.Tensor, bases: list[int], tile: int) -> tuple[torch.Tensor, int, int]:
+    out, lo, hi = [], None, None
+    for r, cnt, s in segs:
         p_first = int(posv[r])
         for a in range(0, cnt, tile):
             out.append((r + a, min(tile, cnt - a), p_first + a, bases[s]))
         lo = bases[s] if lo is None else min(lo, bases[s])
         last = bases[s] + p_first + cnt
         hi = last if hi is None else max(hi, last)
-        r += cnt
     return torch.tensor(out, dtype=torch.int32).reshape(-1, 4), int(lo), int(hi - lo)
+
+
+def prefill_tiles(seq: torch.Tensor, posv: torch.Tensor, bases: list[int], tile: int = 128) -> tuple[torch.Tensor, int, int]:
+    """Query tiles of one chunk (seq[r]: sequence of chunk row r, posv[r]: its position;
+    rows of a sequence are consecutive with consecutive positions) and the cache row range
+    its attention reads: from the lowest sequence base to the last position of any row."""
+    return _group_tiles(_segments(seq), posv, bases, tile)
+
+
+def prefill_groups(seq: torch.Tensor, posv: torch.Tensor, bases: list[int], tile: int = 128,
+                   slack: int = 4096) -> list[tuple[torch.Tensor, int, int]]:
+    """prefill_tiles in groups of consecutive sequences whose expanded cache range stays within
+    twice the rows they attend (plus `slack`): with slots far apart (capacities much larger
+    than the prompts) one range over the whole chunk would expand every slot's unused
+    capacity in between.  Each group: (tiles, exp_lo, exp_rows)."""
+    groups, cur, lo, hi, used = [], [], 0, 0, 0
+    for r, cnt, s in _segments(seq):
+        need = int(posv[r]) + cnt
+        a, e = bases[s], bases[s] + need
+        if cur and max(hi, e) - min(lo, a) <= 2 * (used + need) + slack:
+            cur.append((r, cnt, s))
+            lo, hi, used = min(lo, a), max(hi, e), used + need
+            continue
+        if cur:
+            groups.append(cur)
+        cur, lo, hi, used = [(r, cnt, s)], a, e, need
+    groups.append(cur)
+    return [_group_tiles(g, posv, bases, tile) for g in groups]
 
 
 class RowBuffers:
@@ -177,15 +210,28 @@ class RowBuffers:
 
 
 def _graph_node_count(g: torch.cuda.CUDAGraph) -> int:
-    """Nodes of a captured (kept, not yet instantiated) graph, by hipGraphGetNodes."""
+    """Nodes of a captured (kept, not yet instantiated) graph, by hipGraphGetNodes of the HIP
+    runtime torch loaded (whichever of its sonames resolves); -1 when none does or the call
+    fails -- the count is a report, never a reason to fail a capture."""
     import ctypes
 
-    hip = ctypes.CDLL("libamdhip64.so.7")
+    loaded = []  # the runtime already mapped into this process (torch's), never a second copy
+    try:
+        with open("/proc/self/maps") as f:
+            loaded = sorted({ln.split()[-1] for ln in f if "libamdhip64.so" in ln})
+    except OSError:
+        pass
+    for name in loaded + ["libamdhip64.so.7", "libamdhip64.so.6"]:
+        try:
+            hip = ctypes.CDLL(name)
+            break
+        except OSError:
+            continue
+    else:
+        return -1
     n = ctypes.c_size_t(0)
     rc = hip.hipGraphGetNodes(ctypes.c_void_p(g.raw_cuda_graph()), None, ctypes.byref(n))
-    if rc != 0:
-        raise RuntimeError(f"hipGraphGetNodes failed with {rc}")
-    return int(n.value)
+    return int(n.value) if rc == 0 else -1
 
 
 class DecodeEngine:
@@ -195,16 +241,16 @@ class DecodeEngine:
         """capacities: cache tokens of each row (slot).  moe_tile (batch family): fix the
         grouped MoE token tile (16, 32, 64 or 256) instead of choosing it from the routing of one
         eager step at capture -- for a serving loop whose batch changes under one graph.
-        expert_dtype "fp8" (small family): the decode step reads the e4m3 expert weights of
-        quantize_experts_fp8 (prefill keeps the bf16 kernels on the dequantized weights)."""
+        expert_dtype "fp8": the decode step reads the e4m3 expert weights of
+        quantize_experts_fp8 (small family: the route kernels; batch family: the grouped
+        launches, 32- or 64-token tiles); prefill keeps the bf16 kernels on the dequantized
+        weights."""
         if family not in FAMILIES:
             raise ValueError(f"Unknown kernel family: {family}")
         if mla_path not in ("split", "fused", "spread", "absorb"):
             raise ValueError(f"Unknown MLA path: {mla_path}")
         if expert_dtype not in ("bf16", "fp8"):
             raise ValueError(f"Unknown expert dtype: {expert_dtype}")
-        if expert_dtype == "fp8" and family != "small":
-            raise NotImplementedError("fp8 expert weights: small kernel family only")
         if expert_dtype == "fp8" and not weights.fp8_experts:
             raise ValueError("fp8 expert weights: run dsv2lite.quantize_experts_fp8(weights) first")
         cfg = weights.cfg
@@ -223,8 +269,10 @@ class DecodeEngine:
         self.logits = torch.empty(self.B, cfg.vocab, dtype=torch.float32, device=device)
         self.buf = RowBuffers(cfg, self.B, family, self.max_pos, device)
         if family == "batch" and moe_tile is not None:
-            self.buf.set_tile_tokens(moe_tile)
+            self.buf.set_tile_tokens(self._fit_tile(moe_tile))
             self._moe_tiles_tuned = True
+        elif family == "batch":
+            self.buf.set_tile_tokens(self._fit_tile(self.buf.tile_tokens))
         self._amax = torch.empty(max(0, _hip.lib.dsv2_lm_head_argmax_workspace_size(min(self.B, 8))),
                                  dtype=torch.uint8, device=device)
         # small family: one fused workgroup per (row, head) while contexts are short; the
@@ -243,6 +291,17 @@ class DecodeEngine:
         self.kernels_per_step = 0  # set by capture()
         self._host_pos = [0] * self.B  # host mirror of cache.pos, for capacity checks only
         self._free: set[int] = set()  # retired slots (continuous batching)
+
+    def _fit_tile(self, tile: int, load: float | None = None) -> int:
+        """The decode step's grouped MoE token tile: the e4m3 launches take 32- or 64-token
+        tiles (the bf16 ones 16, 32, 64 or 256) -- 32 up to 32 routes per expert (measured on
+        MI355X, gate_up + shared halves: 256 rows of uniform routing 105.6 us with 32-token tiles
+        against 125.9 us with 64), 64 above."""
+        if self.expert_dtype != "fp8":
+            return tile
+        if load is not None:
+            return 32 if load <= 32 else 64
+        return min(64, max(32, tile))
 
     # ------------------------------------------------------------------ layers
     def _attention(self, L, li: int, b: RowBuffers, R: int, pos, base, cap, family: str, st: int,
@@ -331,16 +390,17 @@ class DecodeEngine:
              c.qkva_dim, 0, 0, st)
         call("dsv2_mla_prepare", ptr(b.qkva), c.qkva_dim, R, ptr(pos), ptr(base), ptr(cap), ptr(L.kv_norm), c.eps,
              ptr(self.cos), ptr(self.sin), self.max_pos, None, ptr(cache), ptr(b.q), ptr(self.cache.status), st)
-        crow = cache.data_ptr() + pf.exp_lo * c.cache_row * cache.element_size()
-        # W_UK / W_UV [16, 128, 512] are the [2048, 512] weights of one dense GEMM whose output
-        # row is [16, 128] (the heads side by side): the prefill-size ring tiles, not 16 groups
-        # of 128 features (C3 prefill: 73 -> ~25 us per expansion)
-        for w, out, n in ((L.w_uk, pf.kexp, nh * c.qk_nope), (L.w_uv, pf.vexp, nh * c.v_dim)):
-            call("dsv2_gemm_bf16", crow, c.cache_row, 0, pf.exp_rows, c.kv_rank, ptr(w), 0, n, 1, None, 0, ptr(out), n,
-                 0, 0, st)
-        call("dsv2_mla_prefill_attention", ptr(b.qkva), c.qkva_dim, ptr(b.q), nh * c.cache_row, R, ptr(cache),
-             cache.shape[0], ptr(pf.kexp), ptr(pf.vexp), pf.exp_lo, pf.exp_rows, ptr(pf.tiles), pf.n_tiles,
-             self.scale, ptr(b.attn), H, st)
+        for tiles, n_tiles, exp_lo, exp_rows in pf.groups:
+            crow = cache.data_ptr() + exp_lo * c.cache_row * cache.element_size()
+            # W_UK / W_UV [16, 128, 512] are the [2048, 512] weights of one dense GEMM whose
+            # output row is [16, 128] (the heads side by side): the prefill-size ring tiles, not
+            # 16 groups of 128 features (C3 prefill: 73 -> ~25 us per expansion)
+            for w, out, n in ((L.w_uk, pf.kexp, nh * c.qk_nope), (L.w_uv, pf.vexp, nh * c.v_dim)):
+                call("dsv2_gemm_bf16", crow, c.cache_row, 0, exp_rows, c.kv_rank, ptr(w), 0, n, 1, None, 0, ptr(out),
+                     n, 0, 0, st)
+            call("dsv2_mla_prefill_attention", ptr(b.qkva), c.qkva_dim, ptr(b.q), nh * c.cache_row, R, ptr(cache),
+                 cache.shape[0], ptr(pf.kexp), ptr(pf.vexp), exp_lo, exp_rows, ptr(tiles), n_tiles, self.scale,
+                 ptr(b.attn), H, st)
         call("dsv2_gemm_bf16", ptr(b.attn), H, 0, R, H, ptr(L.w_o), 0, H, 1, ptr(b.h), H, ptr(b.h), H, 0, 0, st)
 
     def _mlp(self, L, li: int, b: RowBuffers, R: int, family: str, next_norm, st: int) -> None:
@@ -370,10 +430,11 @@ class DecodeEngine:
             return
         if L.moe:
             if R >= GEMM_ROUTER_MIN_ROWS:
-                # prefill chunks: the norm, the logits as an MFMA GEMM, then the top-6
+                # prefill chunks: the norm, the logits as an MFMA GEMM (unrounded fp32, as the
+                # other routers), then the top-6
                 call("dsv2_rmsnorm_bf16", ptr(b.h), H, ptr(L.ln_post), ptr(b.xn), H, R, H, c.eps, st)
                 call("dsv2_gemm_bf16", ptr(b.xn), H, 0, R, H, ptr(L.w_router), 0, c.n_experts, 1, None, 0,
-                     ptr(b.router_logits), c.n_experts, 0, LINEAR_OUT_F32, st)
+                     ptr(b.router_logits), c.n_experts, 0, LINEAR_OUT_F32_EXACT, st)
                 call("dsv2_router_topk6_from_logits", ptr(b.router_logits), R, c.routed_scaling, ptr(b.ids32), None,
                      ptr(b.wts), st)
             elif R <= SPLIT_ROUTER_MAX_ROWS:
@@ -390,7 +451,17 @@ class DecodeEngine:
             else:
                 call("dsv2_moe_bucket", ptr(b.ids32), R, b.tile_tokens, ptr(b.sorted), ptr(b.route_pos),
                      ptr(b.tiles), ptr(b.ntiles), st)
-            if shared_in_grouped(R, b.tile_tokens):
+            if self.expert_dtype == "fp8" and b is self.buf:
+                # e4m3 routed and shared experts, the shared halves in the grouped launches
+                call("dsv2_moe_grouped_gateup_shared_fp8", ptr(b.xn), R, ptr(b.sorted), ptr(b.tiles), ptr(b.ntiles),
+                     b.max_tiles, b.tile_tokens, ptr(L.w_gu8), ptr(L.gu_scale), ptr(L.sh_gu8), ptr(L.sh_gu_scale),
+                     c.moe_inter, ptr(b.hs), ptr(b.shmid), st)
+                call("dsv2_moe_grouped_down_shared_fp8", ptr(b.hs), R, ptr(b.tiles), ptr(b.ntiles), b.max_tiles,
+                     b.tile_tokens, ptr(L.w_down8), ptr(L.down_scale), ptr(b.shmid), ptr(L.sh_down8),
+                     ptr(L.sh_down_scale), c.moe_inter, ptr(b.ys), ptr(b.shparts), st)
+                call("dsv2_moe_combine_parts", ptr(b.ys), ptr(b.route_pos), ptr(b.wts), R, ptr(b.shparts),
+                     ptr(b.h), ptr(b.h), ptr(next_norm), c.eps, ptr(b.xn), st)
+            elif shared_in_grouped(R, b.tile_tokens):
                 # the shared experts' two halves ride in the grouped launches as extra tiles
                 call("dsv2_moe_grouped_gateup_shared", ptr(b.xn), R, ptr(b.sorted), ptr(b.tiles), ptr(b.ntiles),
                      b.max_tiles, b.tile_tokens, ptr(L.w_gu), ptr(L.sh_gu), c.moe_inter, ptr(b.hs), ptr(b.shmid),
@@ -536,8 +607,8 @@ class DecodeEngine:
         max_rows = min(self.max_prefill_rows, total)
         pb = RowBuffers(self.cfg, max_rows, "batch", self.max_pos, dev, prefill=True)
         bases = [int(x) for x in self.cache.base.cpu()[slot_t]]
-        plans = [prefill_tiles(seq[s:s + max_rows], posv[s:s + max_rows], bases) for s in range(0, total, max_rows)]
-        n_exp = max(p[2] for p in plans)
+        plans = [prefill_groups(seq[s:s + max_rows], posv[s:s + max_rows], bases) for s in range(0, total, max_rows)]
+        n_exp = max(g[2] for p in plans for g in p)
         nh, dk = self.cfg.n_heads, self.cfg.qk_nope
         kexp = torch.empty(n_exp, nh, dk, dtype=BF16, device=dev)
         vexp = torch.empty(n_exp, nh, self.cfg.v_dim, dtype=BF16, device=dev)
@@ -557,8 +628,7 @@ class DecodeEngine:
             rows_d = rows.to(dev)
             which = seq[s:e][rows].to(dev)
             crec = [] if record is not None else None
-            t, lo, n = plans[s // max_rows]
-            pf = PrefillPlan(t.to(dev), lo, n, kexp, vexp)
+            pf = PrefillPlan([(t.to(dev), lo, n) for t, lo, n in plans[s // max_rows]], kexp, vexp)
             self._layers(pb, R, ids_c, pos_c, base_c, cap_c, "batch", st, crec, rows_d, pf)
             for r in crec or ():
                 for j, t in enumerate(r[2:]):  # scatter the last-token rows to their sequences
@@ -613,7 +683,9 @@ class DecodeEngine:
         self.step(record=rec)
         self.restore(snap)
         loads = sorted(routing_load(r[2], self.cfg.n_experts) for r in rec if r[0] == "router")
-        tile = tile_tokens_for_load(loads[len(loads) // 2], self.buf._routes) if loads else self.buf.tile_tokens
+        load = loads[len(loads) // 2] if loads else None
+        tile = tile_tokens_for_load(load, self.buf._routes) if loads else self.buf.tile_tokens
+        tile = self._fit_tile(tile, load)
         self.buf.set_tile_tokens(tile)
         self._moe_tiles_tuned = True
         return tile

@@ -19,6 +19,7 @@ ABI_VERSION = 2
 
 LINEAR_SWIGLU = 1
 LINEAR_OUT_F32 = 2
+LINEAR_OUT_F32_EXACT = 4
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int
@@ -74,6 +75,8 @@ _SIGS = {
     "dsv2_moe_grouped_down": ([_p, _p, _p, _i32, _i32, _p, _i32, _p, _p], _i32),
     "dsv2_moe_combine": ([_p, _p, _p, _i32, _p, _p, _p, _p, _f32, _p, _p], _i32),
     "dsv2_moe_grouped_down_shared": ([_p, _i32, _p, _p, _i32, _i32, _p, _p, _p, _i32, _p, _p, _p], _i32),
+    "dsv2_moe_grouped_gateup_shared_fp8": ([_p, _i32, _p, _p, _p, _i32, _i32, _p, _p, _p, _p, _i32, _p, _p, _p], _i32),
+    "dsv2_moe_grouped_down_shared_fp8": ([_p, _i32, _p, _p, _i32, _i32, _p, _p, _p, _p, _p, _i32, _p, _p, _p], _i32),
     "dsv2_moe_combine_parts": ([_p, _p, _p, _i32, _p, _p, _p, _p, _f32, _p, _p], _i32),
 }
 

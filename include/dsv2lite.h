@@ -41,6 +41,8 @@ extern "C" {
 /* flags of dsv2_gemv_bf16 / dsv2_gemm_bf16 */
 #define DSV2_LINEAR_SWIGLU 1  /* W holds [gate; up] (2N rows): y = bf16(silu(bf16 g)) * bf16 u */
 #define DSV2_LINEAR_OUT_F32 2 /* store fp32(bf16(acc)) instead of bf16 (logits)               */
+#define DSV2_LINEAR_OUT_F32_EXACT 4 /* dsv2_gemm_bf16: store the fp32 accumulator unrounded
+                                       (router logits: HF's fp32 gate product); no SwiGLU or residual */
 
 int dsv2_abi_version(void);
 const char* dsv2_last_error_message(void);
@@ -404,6 +406,24 @@ int dsv2_moe_grouped_down(const void* hsorted, const int32_t* tiles, const int32
 int dsv2_moe_grouped_down_shared(const void* hsorted, int rows, const int32_t* tiles, const int32_t* num_tiles,
                                  int max_tiles, int tile_tokens, const void* w_down, const void* shared_mid,
                                  const void* sh_down, int inter, void* ysorted, float* shared_parts, void* stream);
+
+/* dsv2_moe_grouped_gateup_shared / dsv2_moe_grouped_down_shared on e4m3 (OCP float8_e4m3fn)
+ * expert weights with one fp32 power-of-two scale per weight row (gu_scale [E, 2*inter],
+ * sh_gu_scale [2*2816], down_scale [E, 2048], sh_down_scale [2048]; the layouts of
+ * quantize_experts_fp8): every product is that of the dequantized bf16 weight (w8 * scale,
+ * exact), decoded in the kernel (bf16 MFMA on the activations; the scale multiplies the fp32
+ * accumulator).  Same outputs, rounding points and tile table as the bf16 launches; tile_tokens
+ * 32 or 64.  The reference's grouped MoE is bf16 only (moe_batch.py:152-307): these replace
+ * the same functions with half the weight bytes. */
+int dsv2_moe_grouped_gateup_shared_fp8(const void* xn, int rows, const int32_t* sorted_routes, const int32_t* tiles,
+                                       const int32_t* num_tiles, int max_tiles, int tile_tokens,
+                                       const void* w_gate_up8, const float* gu_scale, const void* sh_gate_up8,
+                                       const float* sh_gu_scale, int inter, void* hsorted, void* shared_out,
+                                       void* stream);
+int dsv2_moe_grouped_down_shared_fp8(const void* hsorted, int rows, const int32_t* tiles, const int32_t* num_tiles,
+                                     int max_tiles, int tile_tokens, const void* w_down8, const float* down_scale,
+                                     const void* shared_mid, const void* sh_down8, const float* sh_down_scale, int inter,
+                                     void* ysorted, float* shared_parts, void* stream);
 
 /* Combine: routed = bf16(sum_s w[r,s] ysorted[route_pos[r*6+s]]) (fp32, slot order);
  * y = shared ? bf16(routed + shared[r]) : routed;  out[r] = residual ? bf16(residual[r] + y) : y.

@@ -115,7 +115,7 @@ def _logit_margin(logits: torch.Tensor, k: int) -> float:
     return float(srt[k - 1] - srt[k])
 
 
-def router_flips(om: Pair, record, trace, row, what) -> list[int]:
+def router_flips(om: Pair, record, trace, row, what, stats: list | None = None) -> list[int]:
     """Router checks of one kernel row of a recorded step (or prefill) against the oracle.
 
     1. The router is exact on its own input: the kernel's expert set equals the oracle
@@ -124,7 +124,8 @@ def router_flips(om: Pair, record, trace, row, what) -> list[int]:
     2. A kernel set that differs from the oracle's (a flip) must be explained by the
        difference of the two inputs: the oracle's top-6 logit margin is at most twice the
        largest router-logit difference between the kernel's and the oracle's input.
-    Returns the layers with a flip."""
+    Returns the layers with a flip; with `stats`, appends (layer, oracle top-6 logit margin,
+    router-logit difference of the two inputs) for every flip."""
     h_attn = {r[1]: r[2][row] for r in record if r[0] == "attn"}
     k = om.om.d.top_k
     flips = []
@@ -139,18 +140,24 @@ def router_flips(om: Pair, record, trace, row, what) -> list[int]:
             err = float((lk - lo).abs().max())
             assert _logit_margin(lo, k) <= 2 * err, (what, li, "unexplained flip", _logit_margin(lo, k), err)
             flips.append(li)
+            if stats is not None:
+                stats.append((li, _logit_margin(lo, k), err))
     return flips
 
 
-def check_trace(om: Pair, record, trace, row, what, res, errs: list | None = None) -> tuple[int, bool]:
+def check_trace(om: Pair, record, trace, row, what, res, errs: list | None = None,
+                per_layer: dict | None = None, flip_stats: list | None = None) -> tuple[int, bool]:
     """Per-layer hidden states and router ids of one kernel row of a recorded step vs the
     oracle trace.  Returns (MoE layers checked, whether any layer's expert set differs from
-    the oracle's)."""
-    flips = router_flips(om, record, trace, row, what)
+    the oracle's).  per_layer: layer -> list receiving that layer's close() error tuples."""
+    flips = router_flips(om, record, trace, row, what, flip_stats)
     first = min(flips) if flips else 1 << 30
     for (_, li, h) in (r for r in record if r[0] == "layer"):
+        e = per_layer.setdefault(li, []) if per_layer is not None else None
         close(h[row].float().cpu(), trace[li]["h_out"], res["fp32"]["layer_out"][li][-1], li >= first, (what, li),
-              errs)
+              errs if e is None else e)
+        if e is not None and errs is not None:
+            errs.append(e[-1])
     return sum(1 for r in record if r[0] == "router"), bool(flips)
 
 
@@ -172,3 +179,67 @@ def oracle_step(om: Pair, cache, toks, start, last_logits_only=False):
     for i, tr in enumerate(trace):
         tr["h_out"] = res["layer_out"][i][-1]
     return res, trace
+
+
+class StreamedOracle:
+    """The oracle pair (HF bf16 rounding points and exact fp32 math) for a model whose fp32
+    host copy would not fit comfortably in host memory (27 layers: about 62 GB).  Every pass
+    streams the layers from the device one at a time (hf_layer(i) -> fp32 host tensors), runs
+    that layer for every tracked sequence in both modes with the oracle's own layer_forward,
+    and frees it.  Only the last token's states are kept.  `self.om` exposes the small
+    per-layer tensors (router weights, post-attention norms) the router checks read."""
+
+    def __init__(self, w, max_pos: int):
+        from types import SimpleNamespace
+
+        self.w = w
+        self.d = O.Dims(n_layers=len(w.layers))
+        self.rb = {"bf16": O._rounder("bf16"), "fp32": O._rounder("fp32")}
+        self.tables = {m: O.yarn_cos_sin(self.d, max_pos, m) for m in self.rb}
+        self.embed = w.embed.float().cpu()
+        self.norm = w.norm.float().cpu()
+        self.lm_head = w.lm_head.float().cpu()
+        small = []
+        for L in w.layers:
+            small.append({"post_attention_layernorm": L.ln_post.float().cpu(),
+                          "gate": L.w_router.float().cpu() if L.w_router is not None else None})
+        self.om = SimpleNamespace(w={"layers": small}, d=self.d, rb=self.rb["bf16"])
+
+    def new_cache(self) -> dict:
+        return {m: [O.SeqCache() for _ in self.w.layers] for m in self.rb}
+
+    def run(self, seqs: list, progress=None) -> list:
+        """seqs: (cache, token ids [T], start position) per sequence.  Returns per sequence
+        (res, trace) in oracle_step's format, holding the last token only: res["logits"] /
+        res["fp32"]["logits"] [1, V], res["layer_out"] / res["fp32"]["layer_out"] per layer
+        [1, H]; trace[li] with h_attn, router_ids, router_w ([1, ...]) and h_out."""
+        h = {(j, m): self.embed[toks] for j, (_, toks, _) in enumerate(seqs) for m in self.rb}
+        outs = {k: [] for k in h}
+        traces = [[] for _ in seqs]
+        for li in range(len(self.w.layers)):
+            lw = {k: v.float().cpu() for k, v in self.w.hf_layer(li).items()}
+            for j, (cache, toks, start) in enumerate(seqs):
+                positions = torch.arange(start, start + toks.numel())
+                for m, rb in self.rb.items():
+                    cos, sin = self.tables[m]
+                    tr = {} if m == "bf16" else None
+                    h[j, m] = O.layer_forward(lw, self.d, li, h[j, m], cache[m][li], positions, cos, sin, rb,
+                                              trace=tr)
+                    outs[j, m].append(h[j, m][-1:].clone())
+                    if tr is not None:
+                        keep = {k: tr[k][-1:].clone() for k in ("h_attn", "router_ids", "router_w") if k in tr}
+                        keep["h_out"] = h[j, m][-1]
+                        traces[j].append(keep)
+            del lw
+            if progress is not None:
+                progress(li)
+        res = []
+        for j in range(len(seqs)):
+            r = {}
+            for m, rb in self.rb.items():
+                xn = O.rmsnorm(h[j, m][-1:], self.norm, self.d.eps, rb)
+                r[m] = {"logits": O.linear(xn, self.lm_head, rb).to(torch.float32), "layer_out": outs[j, m]}
+            out = r["bf16"]
+            out["fp32"] = r["fp32"]
+            res.append((out, traces[j]))
+        return res

@@ -112,6 +112,11 @@ def test_moe_tile_choice_and_cache_layout():
     assert not shared_in_grouped(256, 32) and not shared_in_grouped(256, 16) and shared_in_grouped(100, 32)
     c = CompressedKVCache(2, [5, 7, 3], device="cpu")
     assert c.base.tolist() == [0, 5, 12] and c.total == 15 and c.data.shape == (2, 15, 576)
+    # long rows: starts staggered by (7 b mod 8) 32-token tiles inside slots of capacity + 224
+    s = CompressedKVCache(1, [600, 700, 600], device="cpu")
+    assert s.base.tolist() == [0, 824 + 224, 824 + 924 + 192] and s.total == 824 + 924 + 824
+    ends = [int(b) + c for b, c in zip(s.base.tolist(), s.capacities)]
+    assert ends[0] <= s.base[1] and ends[1] <= s.base[2] and ends[2] <= s.total
     c.pos.copy_(torch.tensor([1, 2, 3], dtype=torch.int32))
     snap = c.snapshot()
     c.pos.add_(4)
@@ -347,3 +352,39 @@ def test_prefill_tiles_cover_every_row_once():
         assert lo <= sb and sb + p0 + nr <= lo + n  # every key of the tile's rows is expanded
     assert torch.all(seen == 1)
     assert lo == 0 and lo + n == 500 + 70
+
+
+def test_prefill_groups_bound_the_expansion_by_the_rows_attended():
+    """Slots far apart (capacity 32768, 100-token prompts): the chunk's attention is planned in
+    groups whose expanded cache range is at most twice the rows they attend plus the slack,
+    instead of one range over every slot's unused capacity (64 x 32768 rows); the groups
+    together cover every chunk row exactly once.  Slots packed closely stay one group."""
+    from dsv2lite.engine import prefill_groups, prefill_tiles
+
+    def plan(lens, caps, slack=4096):
+        bases = [0]
+        for c in caps[:-1]:
+            bases.append(bases[-1] + c)
+        seq = torch.cat([torch.full((n,), b, dtype=torch.int64) for b, n in enumerate(lens)])
+        posv = torch.cat([torch.arange(n, dtype=torch.int32) for n in lens])
+        return seq, posv, bases, prefill_groups(seq, posv, bases, slack=slack)
+
+    lens = [100] * 64
+    seq, posv, bases, groups = plan(lens, [32768] * 64)
+    seen = torch.zeros(seq.numel(), dtype=torch.int32)
+    total_exp = 0
+    for tiles, lo, n in groups:
+        used = 0
+        for r0, nr, p0, sb in tiles.tolist():
+            seen[r0:r0 + nr] += 1
+            assert lo <= sb and sb + p0 + nr <= lo + n  # every key of the tile's rows is expanded
+            used += nr
+        assert n <= 2 * used + 4096
+        total_exp += n
+    assert torch.all(seen == 1)
+    assert total_exp <= 64 * 100 + 64 * 4096 and total_exp < 64 * 32768 // 4
+    # bench-like capacities (prompt + a few tokens): one group, the same plan as prefill_tiles
+    seq, posv, bases, groups = plan([2048] * 4, [2081] * 4)
+    assert len(groups) == 1
+    t, lo, n = prefill_tiles(seq, posv, bases)
+    assert torch.equal(groups[0][0], t) and groups[0][1:] == (lo, n)

@@ -109,9 +109,8 @@ def test_engine_rejects_fp8_before_allocating():
     import dsv2lite
 
     w = types.SimpleNamespace(fp8_experts=False)
-    with pytest.raises(NotImplementedError):
-        dsv2lite.DecodeEngine(w, [8], family="batch", expert_dtype="fp8")
-    with pytest.raises(ValueError, match="quantize_experts_fp8"):
-        dsv2lite.DecodeEngine(w, [8], family="small", expert_dtype="fp8")
+    for family in ("small", "batch"):
+        with pytest.raises(ValueError, match="quantize_experts_fp8"):
+            dsv2lite.DecodeEngine(w, [8], family=family, expert_dtype="fp8")
     with pytest.raises(ValueError):
         dsv2lite.DecodeEngine(w, [8], family="small", expert_dtype="int4")

@@ -144,3 +144,56 @@ def test_prefill_crosses_a_chunk_boundary(model):
     the short prompt and the long one's first 924 tokens, the second chunk's queries attend
     keys the first chunk cached."""
     _parity(model, "batch", [100, 1300], seed=6, rows=[0, 1], chunk=1024)
+
+
+def test_prefill_with_capacities_far_above_the_prompts(model):
+    """Slots of capacity 32,768 holding 37..120-token prompts: the prefill plans its attention
+    in per-sequence groups (prefill_groups) instead of expanding every slot's unused capacity
+    in between, and gives the first tokens and logits of an engine whose capacities just fit
+    the prompts (logits within 1e-2; tokens equal or a near-tie)."""
+    import dsv2lite
+
+    from golden_utils import rel_err
+
+    cfg, w, _ = model
+    lens = [100, 37, 120, 64]
+    P = [p.cuda() for p in prompts(lens, seed=8)]
+    big = dsv2lite.DecodeEngine(w, [32768] * 4, family="batch")
+    tight = dsv2lite.DecodeEngine(w, [n + 8 for n in lens], family="batch")
+    ib = big.prefill(P).cpu().clone()
+    it = tight.prefill(P).cpu().clone()
+    torch.cuda.synchronize()
+    for b in range(4):
+        assert rel_err(big.logits[b].cpu(), tight.logits[b].cpu()) < 1e-2, b
+        agree(int(ib[b]), tight.logits[b].cpu(), big.logits[b].cpu(), ("capacity", b))
+    # one decode step on the same input tokens
+    big.ids.copy_(tight.ids)
+    big.step()
+    tight.step()
+    torch.cuda.synchronize()
+    for b in range(4):
+        assert rel_err(big.logits[b].cpu(), tight.logits[b].cpu()) < 2e-2, b
+
+
+@pytest.mark.parametrize("B", [64, 256])
+def test_replicated_prompt_rows_stay_bitwise_identical(model, B):
+    """The reference's published workload replicates one prompt over the batch
+    (src/run.py:733-741): every row then holds the same sequence and must produce the same
+    bits -- the split-KV decode walks every row's tiles in token order (4 splits per row at
+    bsz=64, one 600-token split at bsz=256), the cache rows start staggered, and every sum
+    has a fixed order -- through the prefill and several graph replays."""
+    import dsv2lite
+
+    cfg, w, _ = model
+    p = prompts([600], seed=4)[0].cuda()
+    eng = dsv2lite.DecodeEngine(w, [600 + 16] * B, family="batch")
+    eng.prefill([p] * B)
+    torch.cuda.synchronize()
+    assert torch.equal(eng.logits, eng.logits[:1].expand_as(eng.logits))
+    eng.capture()
+    for s in range(4):
+        eng.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(eng.logits, eng.logits[:1].expand_as(eng.logits)), s
+        assert torch.equal(eng.ids, eng.ids[:1].expand_as(eng.ids)), s
+    eng.check_errors()

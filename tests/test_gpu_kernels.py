@@ -287,6 +287,56 @@ def test_router_from_logits_ties():
     assert torch.allclose(w.cpu(), 2.0 * ref.gather(1, ids.cpu()), rtol=1e-5)
 
 
+@pytest.mark.parametrize("rows", [1024, 8192])
+def test_gemm_router_logits_exact_fp32(rows):
+    """The prefill router (RMSNorm, the logits as an MFMA GEMM with DSV2_LINEAR_OUT_F32_EXACT,
+    then the top-6) keeps the logits in unrounded fp32 like the decode routers: the logits
+    are the fp32 sums of the exact bf16 products (|error| <= 1e-5, where a bf16 round would
+    move them by ~2e-4), and the ids and weights equal dsv2_router_topk6's on the same input
+    wherever the top-6 logit margin exceeds 1e-4 (the two sum the products in different
+    orders)."""
+    from triton_kernels._hip import LINEAR_OUT_F32_EXACT
+
+    h, nw, wr = _router_case(rows, 77)
+    xn = torch.empty_like(h)
+    call("dsv2_rmsnorm_bf16", h.data_ptr(), 2048, nw.data_ptr(), xn.data_ptr(), 2048, rows, 2048, 1e-6, st())
+    lg = torch.empty(rows, 64, dtype=torch.float32, device=DEV)
+    call("dsv2_gemm_bf16", xn.data_ptr(), 2048, 0, rows, 2048, wr.data_ptr(), 0, 64, 1, None, 0, lg.data_ptr(), 64, 0,
+         LINEAR_OUT_F32_EXACT, st())
+    ids = torch.empty(rows, 6, dtype=torch.int32, device=DEV)
+    w = torch.empty(rows, 6, dtype=torch.float32, device=DEV)
+    call("dsv2_router_topk6_from_logits", lg.data_ptr(), rows, 1.0, ids.data_ptr(), None, w.data_ptr(), st())
+    xn2 = torch.empty_like(h)
+    ids2 = torch.empty_like(ids)
+    w2 = torch.empty_like(w)
+    call("dsv2_router_topk6", h.data_ptr(), 2048, nw.data_ptr(), 1e-6, wr.data_ptr(), 1.0, rows, xn2.data_ptr(),
+         ids2.data_ptr(), None, w2.data_ptr(), st())
+    torch.cuda.synchronize()
+    exact = xn.double() @ wr.double().t()
+    assert float((lg.double() - exact).abs().max()) <= 1e-5
+    assert float((rb(exact.float()).double() - exact).abs().max()) > 1e-4  # a bf16 round would show
+    srt = torch.sort(exact, dim=-1, descending=True).values
+    ok = (srt[:, 5] - srt[:, 6]) > 1e-4
+    assert ok.float().mean() > 0.9
+    # sets compared in id order (two of the six may hold logits within fp32 rounding)
+    def by_id(i, wt):
+        o = torch.argsort(i.long(), dim=1)
+        return i.gather(1, o), wt.gather(1, o)
+
+    top = torch.sort(exact, dim=-1, descending=True, stable=True).indices[:, :6].to(torch.int32)
+    ref_w = torch.softmax(exact, dim=-1).gather(1, top.long()).float()
+    (i1, w1), (i0, w0) = by_id(ids, w), by_id(top, ref_w)
+    assert torch.equal(i1[ok], i0[ok])
+    assert torch.allclose(w1[ok], w0[ok], rtol=1e-5, atol=1e-7)
+    # the decode router on the same hidden states: same ids and weights wherever its own
+    # normalised input is bitwise the same (its norm sums in another order)
+    same = (xn == xn2).all(dim=1) & ok
+    assert same.float().mean() > 0.5
+    i2, w2s = by_id(ids2, w2)
+    assert torch.equal(i1[same], i2[same])
+    assert torch.allclose(w1[same], w2s[same], rtol=1e-5, atol=1e-7)
+
+
 @pytest.mark.parametrize("rows,tile", [(1, 16), (64, 16), (256, 64), (1024, 64), (5, 32)])
 def test_moe_bucket_invariants(rows, tile):
     g = torch.Generator().manual_seed(rows)
