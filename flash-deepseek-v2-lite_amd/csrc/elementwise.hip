@@ -297,5 +297,38 @@ extern "C" int dsv2_argmax_f32(const float* logits, int rows, int vocab, int64_t
   return dsv2_launch_status("argmax");
 }
 
+// ---------------------------------------------------------------------------
+// Device copy (a measurement reference, not a step kernel): every thread moves 4 x 16 B per
+// pass, all four loads in flight before the stores, a grid of a few resident waves per SIMD
+// striding over the buffer; non-temporal loads and stores (the bytes are touched once).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void stream_copy_kernel(const uint4* __restrict__ src, uint4* __restrict__ dst,
+                                                          int64_t n16) {
+  const int64_t stride = (int64_t)gridDim.x * 256 * 4;
+  for (int64_t i = (int64_t)blockIdx.x * 256 * 4 + threadIdx.x; i < n16; i += stride) {
+    u32x4_t v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int64_t j = min(i + k * 256, n16 - 1);  // past the end: the last unit (not stored)
+      v[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(src + j));
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (i + k * 256 < n16) __builtin_nontemporal_store(v[k], reinterpret_cast<u32x4_t*>(dst + i + k * 256));
+  }
+}
+
+extern "C" int dsv2_stream_copy(const void* src, void* dst, int64_t nbytes, void* stream) {
+  DSV2_REQUIRE(src && dst, DSV2_E_NULL, "stream_copy: null pointer");
+  DSV2_REQUIRE(nbytes >= 0 && nbytes % 16 == 0, DSV2_E_SHAPE, "stream_copy: nbytes %% 16 required");
+  DSV2_REQUIRE(dsv2_aligned16(src) && dsv2_aligned16(dst), DSV2_E_ALIGN, "stream_copy: alignment");
+  if (nbytes == 0) return DSV2_OK;
+  const int64_t n16 = nbytes / 16;
+  const int64_t wgs = min((int64_t)256 * 8, (n16 + 1023) / 1024);
+  hipLaunchKernelGGL(stream_copy_kernel, dim3((unsigned)wgs), dim3(256), 0, (hipStream_t)stream, (const uint4*)src,
+                     (uint4*)dst, n16);
+  return dsv2_launch_status("stream_copy");
+}
+
 extern "C" int dsv2_abi_version(void) { return DSV2_ABI_VERSION; }
 extern "C" const char* dsv2_last_error_message(void) { return g_err; }

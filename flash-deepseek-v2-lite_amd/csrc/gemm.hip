@@ -714,8 +714,8 @@ static void launch_dma(const GemmArgs& a, bool swiglu, hipStream_t st, int max_t
 // e4m3 bytes (a K chunk of a row takes KC bytes of LDS instead of 2 KC) in a ring of their own
 // (SW stages) beside the token ring (ST stages).
 // A lane reads 16 e4m3 weights of one row per 64-wide half chunk (ds_read_b128: bytes
-// 64 h + 16 kg .. + 15) and decodes them to two bf16 MFMA fragments (v_cvt_pk_f32_fp8, exact:
-// e4m3 values are bf16 values), one per 32-wide MFMA step: step s takes K {64 h + 16 kg + 8 s
+// 64 h + 16 kg .. + 15) and decodes them to two bf16 MFMA fragments (v_cvt_scalef32_pk_bf16_fp8,
+// exact: e4m3 values are bf16 values), one per 32-wide MFMA step: step s takes K {64 h + 16 kg + 8 s
 // .. + 7}, and the token fragments read the same K from their LDS rows.  The row's scale
 // multiplies the fp32 accumulator in the epilogue (a power of two: the products are those of
 // the dequantized bf16 weights).  The weight reads are native vector loads: as struct-typed
@@ -733,18 +733,16 @@ static void launch_dma(const GemmArgs& a, bool swiglu, hipStream_t st, int max_t
 // chunks need 96 KB of LDS there, one workgroup per CU, 160 us).
 constexpr int kF8Wgs32 = 768, kF8Wgs64 = 512;
 
-__device__ __forceinline__ uint32_t pack_hi16(float lo, float hi) {
-  // the bf16 of an fp32 holding an e4m3 value is its upper half (no rounding needed)
-  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
-}
+// 8 e4m3 bytes -> 8 bf16 by v_cvt_scalef32_pk_bf16_fp8 (two per instruction, scale 1: an e4m3
+// value is a bf16 value, so the conversion is exact; the row scale is applied in fp32 later)
 __device__ __forceinline__ bf16x8_t fp8x8_to_bf16x8(uint32_t w0, uint32_t w1) {
-  typedef float f32x2_t __attribute__((ext_vector_type(2)));
-  const f32x2_t a = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w0), false);
-  const f32x2_t b = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w0), true);
-  const f32x2_t c = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w1), false);
-  const f32x2_t d = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w1), true);
-  return as_bf16x8(make_uint4(pack_hi16(a[0], a[1]), pack_hi16(b[0], b[1]), pack_hi16(c[0], c[1]),
-                              pack_hi16(d[0], d[1])));
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false);
+  const bf16x2_t b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true);
+  const bf16x2_t c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false);
+  const bf16x2_t d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true);
+  return as_bf16x8(make_uint4(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+                              __builtin_bit_cast(uint32_t, c), __builtin_bit_cast(uint32_t, d)));
 }
 
 template <bool SWIGLU, int WN, int KC, int SW, int ST>

@@ -98,6 +98,11 @@ int dsv2_embed_gather_bf16(const int64_t* ids, const void* table, int hidden, vo
 int dsv2_argmax_f32(const float* logits, int rows, int vocab, int64_t* next_ids, int32_t* pos,
                     void* stream);
 
+/* dst[0, nbytes) = src[0, nbytes): a streaming device copy (16-byte aligned, nbytes % 16 == 0).
+ * No reference counterpart: the measured copy bandwidth the benchmark quotes each step's
+ * byte rate against, beside the HBM peak. */
+int dsv2_stream_copy(const void* src, void* dst, int64_t nbytes, void* stream);
+
 /* ---- linears -------------------------------------------------------------- */
 
 /* y[r, n] = bf16( x'[r,:] . W[n,:] ) for r < rows, n < N, fp32 accumulation, where

@@ -1086,3 +1086,16 @@ def test_mla_prefill_attention_vs_fp32(lens, start):
         ref[r] = torch.einsum("hn,nhd->hd", torch.softmax(s, -1), ve[rows - lo])
     assert torch.isfinite(c(out)).all()
     assert rel_err(c(out).view(R, 16, 128), ref) < 1e-2
+
+
+@pytest.mark.parametrize("nbytes", [16, 4096 * 16 + 48, 64 * 2**20 + 16])
+def test_stream_copy_exact(nbytes):
+    """dsv2_stream_copy (the copy the benchmark measures its copy bandwidth with) moves every
+    byte and nothing past the end, also for sizes that are not a multiple of its 16 KB pass."""
+    g = torch.Generator(device=DEV).manual_seed(nbytes % 1000)
+    src = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device=DEV, generator=g)
+    dst = torch.full((nbytes + 64,), 7, dtype=torch.uint8, device=DEV)
+    call("dsv2_stream_copy", src.data_ptr(), dst.data_ptr(), nbytes, st())
+    torch.cuda.synchronize()
+    assert torch.equal(dst[:nbytes], src)
+    assert torch.all(dst[nbytes:] == 7)
