@@ -1,6 +1,7 @@
 """Decode-throughput benchmark of the HIP DeepSeek-V2-Lite decode step on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config all|1|2|3|4|r64|r256] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config all|1|2|3|4|r64|r256|s8|s64]
+                    [--expert-dtype bf16|fp8] [--no-cpu-baseline]
 
 Every config: full 27-layer random-init DeepSeek-V2-Lite bf16 (N(0,0.02), seed 0), eager
 prefill of uniform random prompt ids, then K greedy decode steps, the whole step replayed
@@ -12,7 +13,10 @@ from seed 1, small kernel family); the metric's other two batch sizes ride along
 token prompts, batch family) -- timed in the same run on the same weights, each with its
 tok/s, ms/step, step roofline and dominant-kernel roofline.  --config N runs one config
 alone; r64|r256 are the reference's own published workload (one 24-token prompt replicated
-over the batch), whose vs_baseline is value / the published A100 batch-family TPS for it.
+over the batch), whose vs_baseline is value / the published A100 batch-family TPS for it,
+and s8|s64 the same workload on the small (GEMV) family, against the published A100
+small-GEMV TPS.  The default line carries all of them under "configs", with the isolated
+MLA microbenchmark (C4) and configs 1-3 again on e4m3 expert weights (C1_fp8..C3_fp8).
 --config 4 is the isolated absorbed-MLA decode microbenchmark (bsz=128, KV lengths
 U[256,8192]); its value is compressed-cache GB/s.
 
@@ -67,6 +71,13 @@ CONFIGS = {
     "r256": dict(batch=256, family="batch", prompt=lambda g: [24] * 256, seed=4, replicate=True, published=11428.26,
                  workload="reference workload: bsz=256, one 24-token random prompt replicated, batch family, "
                           "hipGraph"),
+    # the same workload on the small (GEMV) family above bsz=1; published: the A100 "forced
+    # small-GEMV" column of docs/third_party_baselines.md:90-100
+    "s8": dict(batch=8, family="small", prompt=lambda g: [24] * 8, seed=4, replicate=True, published=614.82,
+               workload="reference workload: bsz=8, one 24-token random prompt replicated, small family, hipGraph"),
+    "s64": dict(batch=64, family="small", prompt=lambda g: [24] * 64, seed=4, replicate=True, published=1006.51,
+                workload="reference workload: bsz=64, one 24-token random prompt replicated, small family, "
+                         "hipGraph"),
 }
 
 
@@ -91,9 +102,12 @@ def time_dominant_kernel(eng, family: str, reps: int = 4) -> dict:
     c, b = eng.cfg, eng.buf
     moe_layers = [L for L in eng.w.layers if L.moe]
     B = eng.B
+    # small family: each distinct routed expert's and the 2 shared halves' weights once (at
+    # bsz=1 every one of the row's 8 routes), the 8 SwiGLU outputs of every row
+    n_small = int(torch.unique(b.ids32[:B]).numel()) + 2 if family == "small" else 0
     if family == "small" and eng.expert_dtype == "fp8":
         name = "route_gateup_fp8_kernel<4> (small-family MoE gate_up+SwiGLU on e4m3 weights, 6 routed + 2 shared halves)"
-        bytes_per = B * 8 * 2 * c.moe_inter * (c.hidden + 4) + B * 8 * c.moe_inter * 2
+        bytes_per = n_small * 2 * c.moe_inter * (c.hidden + 4) + B * 8 * c.moe_inter * 2
 
         def launch(L):
             call("dsv2_moe_route_gateup_logits_fp8", ptr(b.xn), B, ptr(b.router_logits), c.routed_scaling,
@@ -101,7 +115,7 @@ def time_dominant_kernel(eng, family: str, reps: int = 4) -> dict:
                  c.moe_inter, ptr(b.hbuf), stream_ptr())
     elif family == "small":
         name = "route_gateup_kernel<2> (small-family MoE gate_up+SwiGLU, 6 routed + 2 shared halves)"
-        bytes_per = B * 8 * 2 * c.moe_inter * c.hidden * 2 + B * 8 * c.moe_inter * 2
+        bytes_per = n_small * 2 * c.moe_inter * c.hidden * 2 + B * 8 * c.moe_inter * 2
 
         def launch(L):
             call("dsv2_moe_route_gateup", ptr(b.xn), B, ptr(b.ids32), ptr(L.w_gu), ptr(L.sh_gu), c.moe_inter,
@@ -231,7 +245,7 @@ def time_other_kernels(eng, family: str, ctx_rows: list[int]) -> dict:
                  stream_ptr())
         if eng.absorb_mla:
             entry("qkva_absorb_kernel (q|kv_a projection + W_UK absorption in 8 partial sums per head)",
-                  qkva_absorb, moe, B * 3648 * 2048 * 2 + 2 * 16 * 128 * 512 + B * 16 * 8 * 512 * 4)
+                  qkva_absorb, moe, 3648 * 2048 * 2 + 2 * 16 * 128 * 512 + B * 16 * 8 * 512 * 4)
             entry("mla_quad_kernel<true> (new row + attention + W_UV from the partial absorbed queries)",
                   attend_parts, moe, 2 * 16 * 128 * 512 + kv + B * 16 * 8 * 512 * 4 + B * 2048 * 2)
 
@@ -245,12 +259,13 @@ def time_other_kernels(eng, family: str, ctx_rows: list[int]) -> dict:
             call("dsv2_moe_route_down_fp8", ptr(b.hbuf), B, ptr(b.ids32), ptr(b.wts), ptr(L.w_down8),
                  ptr(L.down_scale), ptr(L.sh_down8), ptr(L.sh_down_scale), c.moe_inter, c.top_k + 2, ptr(b.h),
                  ptr(b.attn), stream_ptr())
+        n_small = int(torch.unique(b.ids32[:B]).numel()) + 2  # distinct routed experts + 2 shared halves
         if eng.expert_dtype == "fp8":
             entry("route_down_fp8_kernel (6 routed + 2 shared-half down projections on e4m3 weights + combine)",
-                  down8, moe, B * 8 * 2048 * (1408 + 4))
+                  down8, moe, n_small * 2048 * (1408 + 4))
         else:
             entry("route_down_kernel (6 routed + 2 shared-half down projections + combine)", down, moe,
-                  B * 8 * 2048 * 1408 * 2)
+                  n_small * 2048 * 1408 * 2)
         return out
     n_exp = int(torch.unique(b.ids32[:B]).numel())
     R = B * c.top_k
@@ -880,11 +895,12 @@ def main() -> None:
         "setup_s": dict(r["setup_s"], init_weights=round(t_init, 2)),
     }
     if args.config == "all":
-        # the metric's other two batch sizes, timed in the same run on the same weights
-        out["configs"] = {}
         # the metric's other two batch sizes, then the reference's own published workload (one
-        # prompt replicated over the batch; vs_published_a100 = tok/s / the published A100 figure)
-        for key, name in ((2, "C2"), (3, "C3"), ("r64", "r64"), ("r256", "r256")):
+        # prompt replicated over the batch) on the batch family at bsz 64 / 256 and on the small
+        # family at bsz 8 / 64 (vs_published_a100 = tok/s / the published A100 figure), timed in
+        # the same run on the same weights
+        out["configs"] = {}
+        for key, name in ((2, "C2"), (3, "C3"), ("r64", "r64"), ("r256", "r256"), ("s8", "s8"), ("s64", "s64")):
             rk = run_config(key, w, args, cfg, dev)
             out["configs"][name] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in rk.items()}
         # benchmark config 4, the isolated absorbed-MLA decode microbenchmark (its own inputs)

@@ -197,3 +197,17 @@ def test_replicated_prompt_rows_stay_bitwise_identical(model, B):
         assert torch.equal(eng.logits, eng.logits[:1].expand_as(eng.logits)), s
         assert torch.equal(eng.ids, eng.ids[:1].expand_as(eng.ids)), s
     eng.check_errors()
+
+
+@pytest.mark.parametrize("bsz", [8, 64])
+def test_small_family_at_larger_batches(model, bsz):
+    """The small (GEMV) family above bsz=3, as the reference runs it up to bsz=256
+    (attention_decode_small.py:932-1070, moe_small_gemv.py:430-514): ragged prompts, the
+    absorbed q|kv_a projection, the one-launch attention and the route-local MoE with 8 and
+    64 rows (the lm_head GEMV + argmax above 8 rows).  Two sampled rows (the shortest and the
+    longest prompt) against the oracle, teacher-forced for 3 steps; graph == eager for the
+    whole batch."""
+    g = torch.Generator().manual_seed(20 + bsz)
+    lens = torch.randint(24, 600, (bsz,), generator=g).tolist()
+    eng = _parity(model, "small", lens, seed=20 + bsz, rows=_sample(lens, 20 + bsz)[:2])
+    assert eng.mla_path == "absorb"
