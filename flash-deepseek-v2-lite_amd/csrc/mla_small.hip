@@ -15,7 +15,7 @@ constexpr int kAbsBlocks = 8;  // q_nope rows of a head in blocks of 16: partial
 // instruction: q.k by v_dot2_f32_bf16 on the packed bf16 pairs, a 16-lane DPP sum, an online
 // softmax per 16-lane row, p.v by v_dot2_f32_bf16 over the row's two tokens with p rounded
 // to bf16 (the reference also rounds its softmax weights to bf16 before p.v).  Each wave
-// takes 8 consecutive tokens per batch (2 per row), two batches in flight.  The 32 row
+// takes 8 consecutive tokens per batch (2 per row), three batches in flight.  The 32 row
 // states of the workgroup merge in LDS.
 //   mla_attend_kernel: after mla_prepare (absorbed, rotated q and the new cache row written).
 //   mla_quad_kernel (dsv2_mla_fused): the whole MLA in one launch -- each of a head's four
@@ -42,8 +42,9 @@ struct AttTok {
   uint4 c[4];  // latent chunks li + 16j
   uint2 r;     // rope elements 4li .. 4li+3
 };
-struct AttLds {
+struct __attribute__((aligned(16))) AttLds {
   float wo[kAttRows][kLat];
+  bf16_t wuv[kAttRows][kLat];  // the workgroup's 32 W_UV rows (wave wv: rows 4 wv .. 4 wv + 3)
   float wm[kAttRows], wl[kAttRows];
   float olat[kLat];
 };
@@ -113,14 +114,15 @@ __device__ __forceinline__ void att_consume(AttRow& R, const AttTok (&S)[kAttTB]
   }
 }
 
-// The attention of one (row, head, W_UV quarter): cached rows [0, n) of crow0 (first two
-// batches already requested into ta / tb), plus -- when xt != null, in the workgroup's
+// The attention of one (row, head, W_UV quarter): cached rows [0, n) of crow0 (first three
+// batches already requested into ta / tb / tc), plus -- when xt != null, in the workgroup's
 // 16-lane row 0 -- one more token whose bf16 row xt[576] is in LDS; the 32 row states merged
-// in LDS, then y = W_UV rows (this lane's 16 bytes of 4 rows per wave in wuv) . o_lat,
+// in LDS, then y = W_UV rows (wave wv's 4 rows in sh.wuv, stored by att_stash_wuv) . o_lat,
 // stored as bf16 at outp[wv*4 .. +3].
-__device__ __forceinline__ void att_finish(AttTok (&ta)[kAttTB], AttTok (&tb)[kAttTB], const bf16_t* crow0, int n,
-                                           int n_ld, const uint4 (&qc)[4], uint2 qr, const bf16_t* xt,
-                                           const uint4 (&wuv)[4], float scale_log2, AttLds& sh, bf16_t* outp) {
+__device__ __forceinline__ void att_finish(AttTok (&ta)[kAttTB], AttTok (&tb)[kAttTB], AttTok (&tc)[kAttTB],
+                                           const bf16_t* crow0, int n, int n_ld, const uint4 (&qc)[4], uint2 qr,
+                                           const bf16_t* xt, float scale_log2, AttLds& sh,
+                                           bf16_t* outp) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, li = lane & 15, rg = lane >> 4;
   const int tw = wv * 4 * kAttTB;
   AttRow R;
@@ -128,19 +130,25 @@ __device__ __forceinline__ void att_finish(AttTok (&ta)[kAttTB], AttTok (&tb)[kA
   R.l = 0.f;
 #pragma unroll
   for (int i = 0; i < 32; ++i) R.o[i] = 0.f;
-  // inside the loop every load is issued unconditionally (past the end the rows are clamped
-  // and masked), so the same loads are pending at every loop entry and each wait is for one
-  // batch; the last pass leaves before loading batches no pass would consume
+  // a ring of three batches (192 tokens requested at entry: the bsz=1 contexts of a few
+  // hundred tokens wait for one load round trip, not one per batch pair).  Each pass but the
+  // last consumes its three batches and refills each slot unconditionally (past the end the
+  // rows are clamped and masked), so the same loads are pending at every loop entry and each
+  // wait is for one batch; the last pass -- its batches already in flight -- loads nothing
   if (n > 0)
-    for (int t0 = 0;; t0 += 2 * kAttStep) {
-      att_consume(R, ta, qc, qr, t0 + tw + rg, n, scale_log2);
-      if (t0 + 2 * kAttStep >= n) {
+    for (int t0 = 0;; t0 += 3 * kAttStep) {
+      if (t0 + 3 * kAttStep >= n) {
+        att_consume(R, ta, qc, qr, t0 + tw + rg, n, scale_log2);
         if (t0 + kAttStep < n) att_consume(R, tb, qc, qr, t0 + kAttStep + tw + rg, n, scale_log2);
+        if (t0 + 2 * kAttStep < n) att_consume(R, tc, qc, qr, t0 + 2 * kAttStep + tw + rg, n, scale_log2);
         break;
       }
-      att_load(ta, crow0, t0 + 2 * kAttStep, n_ld, wv, li, rg);
+      att_consume(R, ta, qc, qr, t0 + tw + rg, n, scale_log2);
+      att_load(ta, crow0, t0 + 3 * kAttStep, n_ld, wv, li, rg);
       att_consume(R, tb, qc, qr, t0 + kAttStep + tw + rg, n, scale_log2);
-      att_load(tb, crow0, t0 + 3 * kAttStep, n_ld, wv, li, rg);
+      att_load(tb, crow0, t0 + 4 * kAttStep, n_ld, wv, li, rg);
+      att_consume(R, tc, qc, qr, t0 + 2 * kAttStep + tw + rg, n, scale_log2);
+      att_load(tc, crow0, t0 + 5 * kAttStep, n_ld, wv, li, rg);
     }
   if (xt && wv == 0 && rg == 0) {  // the extra token, in row 0
     AttTok t;
@@ -166,10 +174,23 @@ __device__ __forceinline__ void att_finish(AttTok (&ta)[kAttTB], AttTok (&tb)[kA
     sh.wm[row] = R.m;
     sh.wl[row] = R.l;
   }
+  // the row state as 16-byte LDS writes: lane li's 8 latent elements (li + 16j) * 8 .. + 7 are
+  // one 32-byte chunk, and lanes li with bit 2 set write its second half first, so the 8 lanes
+  // a write serves at once cover all 32 banks (element-wise writes put the 64 lanes of a wave
+  // on 4 banks: 1.8 us of the workgroup's 8 us at bsz=1, MI355X)
+  const int hs = (li >> 2) & 1;
 #pragma unroll
   for (int j = 0; j < 4; ++j)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) sh.wo[row][(li + 16 * j) * 8 + i] = R.o[8 * j + i];
+    for (int k = 0; k < 2; ++k) {
+      const int hh = k ^ hs;
+      floatx4_t v;
+      v[0] = hh ? R.o[8 * j + 4] : R.o[8 * j];
+      v[1] = hh ? R.o[8 * j + 5] : R.o[8 * j + 1];
+      v[2] = hh ? R.o[8 * j + 6] : R.o[8 * j + 2];
+      v[3] = hh ? R.o[8 * j + 7] : R.o[8 * j + 3];
+      *reinterpret_cast<floatx4_t*>(&sh.wo[row][(li + 16 * j) * 8 + 4 * hh]) = v;
+    }
   __syncthreads();
   // merge the rows: wave 0 turns the 32 row maxima into weights 2^(m_w - M) / L once (a row
   // that saw no token carries m = -inf: weight 0; row 0 always sees a token -- token 0, or
@@ -198,7 +219,10 @@ __device__ __forceinline__ void att_finish(AttTok (&ta)[kAttTB], AttTok (&tb)[kA
   for (int i = 0; i < 8; ++i) xo[i] = sh.olat[lane * 8 + i];
   float yr[4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) yr[r] = wave_sum_dpp(dot8(wuv[r], xo));
+  for (int r = 0; r < 4; ++r) {
+    const u32x4_t w4 = *reinterpret_cast<const u32x4_t*>(&sh.wuv[wv * 4 + r][lane * 8]);
+    yr[r] = wave_sum_dpp(dot8(make_uint4(w4[0], w4[1], w4[2], w4[3]), xo));
+  }
   if (lane == 0) {
     uint2 w;
     w.x = pack2(yr[0], yr[1]);
@@ -207,10 +231,18 @@ __device__ __forceinline__ void att_finish(AttTok (&ta)[kAttTB], AttTok (&tb)[kA
   }
 }
 
+// wave wv's 4 of the workgroup's 32 W_UV rows (h's output rows qq*32 + wv*4 ..), this lane's
+// 16 bytes of each, requested at entry and parked in LDS (att_stash_wuv) before the attention
+// so that no registers are held across it
 __device__ __forceinline__ void att_load_wuv(uint4 (&wuv)[4], const bf16_t* w_uv, int h, int qq, int wv, int lane) {
   const bf16_t* wp = w_uv + ((int64_t)h * 128 + qq * 32 + wv * 4) * kLat + lane * 8;
 #pragma unroll
   for (int r = 0; r < 4; ++r) wuv[r] = ldg16(wp + (int64_t)r * kLat);
+}
+__device__ __forceinline__ void att_stash_wuv(AttLds& sh, const uint4 (&wuv)[4], int wv, int lane) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    *reinterpret_cast<u32x4_t*>(&sh.wuv[wv * 4 + r][lane * 8]) = u32x4_t{wuv[r].x, wuv[r].y, wuv[r].z, wuv[r].w};
 }
 }  // namespace
 
@@ -236,10 +268,13 @@ __global__ __launch_bounds__(512) void mla_attend_kernel(const bf16_t* __restric
   const uint2 qr = *reinterpret_cast<const uint2*>(qh + kLat + 4 * li);
   uint4 wuv[4];
   att_load_wuv(wuv, w_uv, h, qq, wv, lane);
-  AttTok ta[kAttTB], tb[kAttTB];
+  AttTok ta[kAttTB], tb[kAttTB], tc[kAttTB];
   att_load(ta, crow0, 0, n, wv, li, rg);
   att_load(tb, crow0, kAttStep, n, wv, li, rg);
-  att_finish(ta, tb, crow0, n, n, qc, qr, nullptr, wuv, scale_log2, sh, out + (int64_t)b * os + h * 128 + qq * 32);
+  att_load(tc, crow0, 2 * kAttStep, n, wv, li, rg);
+  att_stash_wuv(sh, wuv, wv, lane);
+  att_finish(ta, tb, tc, crow0, n, n, qc, qr, nullptr, scale_log2, sh,
+             out + (int64_t)b * os + h * 128 + qq * 32);
 }
 
 // PARTS: q_lat is the sum of qkva_absorb_kernel's 8 fp32 partial products per head
@@ -276,7 +311,7 @@ __global__ __launch_bounds__(512) void mla_quad_kernel(const bf16_t* __restrict_
   const int pc = p >= max_pos ? max_pos - 1 : p;
   const bf16_t* crow0 = cache + base[b] * kRow;
 
-  // ---- entry loads: W_UK^T_h, q_nope_h, the W_UV rows, the new row's inputs, two batches --
+  // ---- entry loads: W_UK^T_h, q_nope_h, the W_UV rows, the new row's inputs, 3 batches ----
   // absorption: thread (gi = tid / 16, k = tid % 16) owns latent rows gi + 32u, K slice k
   const int gi = tid >> 4, k = tid & 15;
   uint4 qn4 = {0u, 0u, 0u, 0u};
@@ -295,27 +330,35 @@ __global__ __launch_bounds__(512) void mla_quad_kernel(const bf16_t* __restrict_
   }
   uint4 wuv[4];
   att_load_wuv(wuv, w_uv, h, qq, wv, lane);
-  uint4 kv4 = {0u, 0u, 0u, 0u}, kw4 = {0u, 0u, 0u, 0u};
-  float re = 0.f, ro = 0.f, c0 = 0.f, c1 = 0.f, s0 = 0.f, s1 = 0.f;
-  if (wv <= 1) {
-    if (wv == 0) {
-      kv4 = ldg16(q + 3072 + lane * 8);
-      kw4 = ldg16(kvw + lane * 8);
-    }
-    if (lane < 32) {
-      const bf16_t* rp = wv == 0 ? q + 3584 : q + h * 192 + 128;
-      re = bf2f(rp[2 * lane]);
-      ro = bf2f(rp[2 * lane + 1]);
-      c0 = bf2f(cosT[(int64_t)pc * 64 + lane]);
-      c1 = bf2f(cosT[(int64_t)pc * 64 + 32 + lane]);
-      s0 = bf2f(sinT[(int64_t)pc * 64 + lane]);
-      s1 = bf2f(sinT[(int64_t)pc * 64 + 32 + lane]);
-    }
+  // the new row's inputs (used by waves 0 and 1), requested by every wave without a branch and
+  // turned into floats only after the token batches are requested: unpacked inside a branch
+  // they made waves 0 and 1 wait for every load so far first (one more load round trip)
+  const uint4 kv4 = ldg16(q + 3072 + lane * 8);
+  const uint4 kw4 = ldg16(kvw + lane * 8);
+  uint32_t rr[6];  // RoPE pair (k_pe: wave 0, q_pe: the other waves), cos pair, sin pair
+  {
+    const int l32 = lane & 31;
+    const bf16_t* rp = wv == 0 ? q + 3584 : q + h * 192 + 128;
+    rr[0] = rp[2 * l32];
+    rr[1] = rp[2 * l32 + 1];
+    rr[2] = cosT[(int64_t)pc * 64 + l32];
+    rr[3] = cosT[(int64_t)pc * 64 + 32 + l32];
+    rr[4] = sinT[(int64_t)pc * 64 + l32];
+    rr[5] = sinT[(int64_t)pc * 64 + 32 + l32];
   }
   const int n_ld = max(p, 1);
-  AttTok ta[kAttTB], tb[kAttTB];
+  AttTok ta[kAttTB], tb[kAttTB], tc[kAttTB];
   att_load(ta, crow0, 0, n_ld, wv, li, rg);
   att_load(tb, crow0, kAttStep, n_ld, wv, li, rg);
+  att_load(tc, crow0, 2 * kAttStep, n_ld, wv, li, rg);
+  float rf[6];
+#pragma unroll
+  for (int i = 0; i < 6; ++i) {
+    uint32_t u = rr[i];
+    asm volatile("" : "+v"(u));
+    rf[i] = __uint_as_float(u << 16);
+  }
+  const float re = rf[0], ro = rf[1], c0 = rf[2], c1 = rf[3], s0 = rf[4], s1 = rf[5];
 
   // ---- absorption: q_lat[c] = bf16(W_UK^T_h[c, :] . q_nope_h) ------------------------------
   if (PARTS) {
@@ -360,12 +403,14 @@ __global__ __launch_bounds__(512) void mla_quad_kernel(const bf16_t* __restrict_
     qv[kLat + lane] = f2bf(re * c0 - ro * s0);
     qv[kLat + 32 + lane] = f2bf(ro * c1 + re * s1);
   }
+  att_stash_wuv(sh, wuv, wv, lane);
   __syncthreads();
   uint4 qc[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) qc[j] = *reinterpret_cast<const uint4*>(qv + (li + 16 * j) * 8);
   const uint2 qr = *reinterpret_cast<const uint2*>(qv + kLat + 4 * li);
-  att_finish(ta, tb, crow0, p, n_ld, qc, qr, nrow, wuv, scale_log2, sh, out + (int64_t)b * os + h * 128 + qq * 32);
+  att_finish(ta, tb, tc, crow0, p, n_ld, qc, qr, nrow, scale_log2, sh,
+             out + (int64_t)b * os + h * 128 + qq * 32);
 }
 
 // ---------------------------------------------------------------------------------------

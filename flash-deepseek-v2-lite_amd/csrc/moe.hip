@@ -216,15 +216,15 @@ __device__ __forceinline__ int routed_expert(float x, int s) {
   return max(__ffsll(__ballot(rank == s)) - 1, 0);  // no lane holds rank s only when logits are NaN
 }
 
-// Expert of routed slot s of row b (wave 0 of the route's workgroups): from the row's ids, or
-// ranked from its fp32 router logits (the route's first workgroup then publishes the row's
-// ids and softmax weights).  Slots s >= 6 (shared halves) return 0.
-__device__ __forceinline__ int route_expert(const RouteGateupArgs& a, int b, int s, int bx, int lane) {
+// Expert of routed slot s of row b (every wave of the route's workgroups): from the row's ids,
+// or ranked from its fp32 router logits (wave 0 of the route's first workgroup then publishes
+// the row's ids and softmax weights: `publish`).  Slots s >= 6 (shared halves) return 0.
+__device__ __forceinline__ int route_expert(const RouteGateupArgs& a, int b, int s, bool publish, int lane) {
   int e = 0;
   if (s < kTopK && a.logits) {
     const float x = a.logits[(int64_t)b * kE + lane];
     e = routed_expert(x, s);
-    if (bx == 0 && s == 0) {
+    if (publish) {
       int rank = 0;
       for (int j = 0; j < kE; ++j) {
         const float xj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), j));
@@ -244,33 +244,21 @@ __device__ __forceinline__ int route_expert(const RouteGateupArgs& a, int b, int
   return e;
 }
 
-// 6 waves per SIMD: all 1408 workgroups of a bsz=1 launch (8 routes x 176) resident together
+// 6 waves per SIMD: all 1408 workgroups of a bsz=1 launch (8 routes x 176) resident together.
+// Every wave finds its route's expert itself and requests its weight rows at once -- the
+// shared halves' workgroups at entry -- and only then stages x and meets the other waves: a
+// wave-0 ranking handed over through LDS held every weight request of the workgroup behind
+// the x load and the barrier (the launch's first ~2 us without HBM traffic).
 template <int RPW>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) void route_gateup_kernel(
     const RouteGateupArgs a) {
   __shared__ float xs[kH];
-  __shared__ int eid;
   const int bx = blockIdx.x % a.gu_blocks, route = blockIdx.x / a.gu_blocks;
   const int b = route / a.nr, s = route % a.nr;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int i0 = (bx * 4 + wv) * RPW;
-  // x first (it does not depend on the routing), then the logits
-  const uint4 x4 = ldg16(a.xn + (int64_t)b * kH + tid * 8);
-  if (wv == 0) {
-    // one wave per workgroup ranks the logits
-    const int e = route_expert(a, b, s, bx, lane);
-    if (lane == 0) eid = e;
-  }
-  {
-    float f[8];
-    unpack8(x4, f);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) xs[tid * 8 + i] = f[i];
-  }
-  __syncthreads();
-  const int e = eid;
   const bool live = i0 < a.inter;  // inter % RPW == 0: a live wave owns RPW whole rows
-  if (!live) return;
+  const int e = route_expert(a, b, s, bx == 0 && s == 0 && wv == 0, lane);
   const bf16_t *gp, *up;
   if (s < kTopK) {
     gp = a.wgu + (int64_t)e * 2 * a.inter * kH;
@@ -280,8 +268,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) voi
     gp = a.shgu + (int64_t)half * a.inter * kH;
     up = a.shgu + (int64_t)(2 * a.inter + half * a.inter) * kH;
   }
-  gp += (int64_t)i0 * kH;
-  up += (int64_t)i0 * kH;
+  const int ir = live ? i0 : 0;  // a dead wave's rows: in bounds, never used
+  gp += (int64_t)ir * kH;
+  up += (int64_t)ir * kH;
   uint4 wg[RPW][4], wu[RPW][4];
 #pragma unroll
   for (int r = 0; r < RPW; ++r)
@@ -290,6 +279,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) voi
       wg[r][j] = ldg16_nt(gp + (int64_t)r * kH + (lane + 64 * j) * 8);
       wu[r][j] = ldg16_nt(up + (int64_t)r * kH + (lane + 64 * j) * 8);
     }
+  // x after the weight requests (its registers are not held while they are formed), staged
+  // once they are all out
+  const uint4 x4 = ldg16(a.xn + (int64_t)b * kH + tid * 8);
+  asm volatile("" ::: "memory");
+  {
+    float f[8];
+    unpack8(x4, f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xs[tid * 8 + i] = f[i];
+  }
+  __syncthreads();
+  if (!live) return;
   float ag[RPW], au[RPW];
 #pragma unroll
   for (int r = 0; r < RPW; ++r) ag[r] = au[r] = 0.f;
@@ -320,28 +321,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) voi
 // 2 loads per lane per row, 4 rows of gate and 4 of up per wave) and the row's fp32 scale
 // applied to the fp32 dot product before the SwiGLU.
 template <int RPW>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) void route_gateup_fp8_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void route_gateup_fp8_kernel(
     const RouteGateupArgs a) {
   __shared__ float xs[kH];
-  __shared__ int eid;
   const int bx = blockIdx.x % a.gu_blocks, route = blockIdx.x / a.gu_blocks;
   const int b = route / a.nr, s = route % a.nr;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int i0 = (bx * 4 + wv) * RPW;
+  const bool live = i0 < a.inter;  // inter % RPW == 0: a live wave owns RPW whole rows
   const uint4 x4 = ldg16(a.xn + (int64_t)b * kH + tid * 8);
-  if (wv == 0) {
-    const int e = route_expert(a, b, s, bx, lane);
-    if (lane == 0) eid = e;
-  }
-  {
-    float f[8];
-    unpack8(x4, f);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) xs[tid * 8 + i] = f[i];
-  }
-  __syncthreads();
-  const int e = eid;
-  if (i0 >= a.inter) return;  // inter % RPW == 0: a live wave owns RPW whole rows
+  const int e = route_expert(a, b, s, bx == 0 && s == 0 && wv == 0, lane);
   const uint8_t *gp, *up;
   const float *gs, *us;
   if (s < kTopK) {
@@ -356,14 +345,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) voi
     gs = a.sshgu + half * a.inter;
     us = a.sshgu + 2 * a.inter + half * a.inter;
   }
+  const int ir = live ? i0 : 0;  // a dead wave's rows: in bounds, never used
   float sg[RPW], su[RPW];
 #pragma unroll
   for (int r = 0; r < RPW; ++r) {
-    sg[r] = gs[i0 + r];
-    su[r] = us[i0 + r];
+    sg[r] = gs[ir + r];
+    su[r] = us[ir + r];
   }
-  gp += (int64_t)i0 * kH;
-  up += (int64_t)i0 * kH;
+  gp += (int64_t)ir * kH;
+  up += (int64_t)ir * kH;
   uint4 wg[RPW][2], wu[RPW][2];
 #pragma unroll
   for (int r = 0; r < RPW; ++r)
@@ -372,6 +362,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) voi
       wg[r][j] = ldg16_nt(gp + (int64_t)r * kH + (lane + 64 * j) * 16);
       wu[r][j] = ldg16_nt(up + (int64_t)r * kH + (lane + 64 * j) * 16);
     }
+  asm volatile("" ::: "memory");  // every weight request goes out before x is staged
+  {
+    float f[8];
+    unpack8(x4, f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xs[tid * 8 + i] = f[i];
+  }
+  __syncthreads();
+  if (!live) return;
   float ag[RPW], au[RPW];
 #pragma unroll
   for (int r = 0; r < RPW; ++r) ag[r] = au[r] = 0.f;
