@@ -330,38 +330,5 @@ extern "C" int dsv2_stream_copy(const void* src, void* dst, int64_t nbytes, void
   return dsv2_launch_status("stream_copy");
 }
 
-// ---------------------------------------------------------------------------
-// Cache warm-up read: `wgs` workgroups stride over [src, src + nbytes) with 8 loads of 16 B
-// per lane in flight and keep nothing (the loaded words are folded into one value that is
-// stored only when `sink` is non-null), so the bytes pass through the memory-side Infinity
-// Cache on their way to the CUs -- run beside latency-bound launches, it moves weights a later
-// launch reads from HBM into that cache while HBM would otherwise idle.
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void warm_read_kernel(const uint4* __restrict__ src, int64_t n16,
-                                                        uint32_t* __restrict__ sink) {
-  constexpr int U = 8;
-  const int64_t stride = (int64_t)gridDim.x * 256 * U;
-  uint32_t acc = 0;
-  for (int64_t i = (int64_t)blockIdx.x * 256 * U + threadIdx.x; i < n16; i += stride) {
-    u32x4_t v[U];
-#pragma unroll
-    for (int k = 0; k < U; ++k) v[k] = *reinterpret_cast<const u32x4_t*>(src + min(i + k * 256, n16 - 1));
-#pragma unroll
-    for (int k = 0; k < U; ++k) acc ^= v[k][0] ^ v[k][1] ^ v[k][2] ^ v[k][3];
-  }
-  if (sink) sink[(int64_t)blockIdx.x * 256 + threadIdx.x] = acc;
-}
-
-extern "C" int dsv2_warm_read(const void* src, int64_t nbytes, int wgs, void* sink, void* stream) {
-  DSV2_REQUIRE(src, DSV2_E_NULL, "warm_read: null pointer");
-  DSV2_REQUIRE(nbytes >= 0 && nbytes % 16 == 0 && wgs > 0 && wgs <= 4096, DSV2_E_SHAPE,
-               "warm_read: nbytes %% 16 and 1..4096 workgroups required");
-  DSV2_REQUIRE(dsv2_aligned16(src), DSV2_E_ALIGN, "warm_read: alignment");
-  if (nbytes == 0) return DSV2_OK;
-  hipLaunchKernelGGL(warm_read_kernel, dim3((unsigned)wgs), dim3(256), 0, (hipStream_t)stream, (const uint4*)src,
-                     nbytes / 16, (uint32_t*)sink);
-  return dsv2_launch_status("warm_read");
-}
-
 extern "C" int dsv2_abi_version(void) { return DSV2_ABI_VERSION; }
 extern "C" const char* dsv2_last_error_message(void) { return g_err; }

@@ -38,7 +38,6 @@ _SIGS = {
     "dsv2_fill_positions": ([_p, _p, _p, _p, _i64, _i32, _p], _i32),
     "dsv2_embed_gather_bf16": ([_p, _p, _i32, _p, _i32, _p], _i32),
     "dsv2_stream_copy": ([_p, _p, _i64, _p], _i32),
-    "dsv2_warm_read": ([_p, _i64, _i32, _p, _p], _i32),
     "dsv2_argmax_f32": ([_p, _i32, _i32, _p, _p, _p], _i32),
     "dsv2_gemv_bf16": ([_p, _i64, _i32, _i32, _p, _i32, _p, _f32, _p, _i64, _p, _i64, _i32, _p], _i32),
     "dsv2_lm_head_argmax_workspace_size": ([_i32], _i64),

@@ -103,12 +103,6 @@ int dsv2_argmax_f32(const float* logits, int rows, int vocab, int64_t* next_ids,
  * byte rate against, beside the HBM peak. */
 int dsv2_stream_copy(const void* src, void* dst, int64_t nbytes, void* stream);
 
-/* Read [src, src + nbytes) with `wgs` workgroups and keep nothing (sink: null, or a buffer
- * of wgs * 256 uint32 that receives a fold of the words read).  No reference counterpart:
- * run on a second captured stream beside latency-bound launches, it pulls weights a later
- * launch of the step reads into the memory-side Infinity Cache. */
-int dsv2_warm_read(const void* src, int64_t nbytes, int wgs, void* sink, void* stream);
-
 /* ---- linears -------------------------------------------------------------- */
 
 /* y[r, n] = bf16( x'[r,:] . W[n,:] ) for r < rows, n < N, fp32 accumulation, where
