@@ -245,19 +245,18 @@ __device__ __forceinline__ int route_expert(const RouteGateupArgs& a, int b, int
 }
 
 // 6 waves per SIMD: all 1408 workgroups of a bsz=1 launch (8 routes x 176) resident together.
-// Every wave finds its route's expert itself and requests its weight rows at once -- the
-// shared halves' workgroups at entry -- and only then stages x and meets the other waves: a
-// wave-0 ranking handed over through LDS held every weight request of the workgroup behind
-// the x load and the barrier (the launch's first ~2 us without HBM traffic).
+// Every wave finds its route's expert itself and requests its weight rows at once (the shared
+// halves' workgroups at entry), then each lane reads x for its own K chunks (as bf16, from L2
+// / L1) instead of a copy staged in LDS: no LDS and no barrier, so nothing holds a wave's
+// weight requests behind the other waves.
 template <int RPW>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) void route_gateup_kernel(
     const RouteGateupArgs a) {
-  __shared__ float xs[kH];
   const int bx = blockIdx.x % a.gu_blocks, route = blockIdx.x / a.gu_blocks;
   const int b = route / a.nr, s = route % a.nr;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int i0 = (bx * 4 + wv) * RPW;
-  const bool live = i0 < a.inter;  // inter % RPW == 0: a live wave owns RPW whole rows
+  if (i0 >= a.inter) return;  // inter % RPW == 0: a live wave owns RPW whole rows
   const int e = route_expert(a, b, s, bx == 0 && s == 0 && wv == 0, lane);
   const bf16_t *gp, *up;
   if (s < kTopK) {
@@ -268,9 +267,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) voi
     gp = a.shgu + (int64_t)half * a.inter * kH;
     up = a.shgu + (int64_t)(2 * a.inter + half * a.inter) * kH;
   }
-  const int ir = live ? i0 : 0;  // a dead wave's rows: in bounds, never used
-  gp += (int64_t)ir * kH;
-  up += (int64_t)ir * kH;
+  gp += (int64_t)i0 * kH;
+  up += (int64_t)i0 * kH;
   uint4 wg[RPW][4], wu[RPW][4];
 #pragma unroll
   for (int r = 0; r < RPW; ++r)
@@ -279,24 +277,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) voi
       wg[r][j] = ldg16_nt(gp + (int64_t)r * kH + (lane + 64 * j) * 8);
       wu[r][j] = ldg16_nt(up + (int64_t)r * kH + (lane + 64 * j) * 8);
     }
-  // x after the weight requests (its registers are not held while they are formed), staged
-  // once they are all out
-  const uint4 x4 = ldg16(a.xn + (int64_t)b * kH + tid * 8);
-  asm volatile("" ::: "memory");
-  {
-    float f[8];
-    unpack8(x4, f);
+  // x after the weight requests (held across them it would not fit the 80 registers that
+  // keep all 1408 workgroups resident)
+  uint4 xr[4];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) xs[tid * 8 + i] = f[i];
-  }
-  __syncthreads();
-  if (!live) return;
+  for (int j = 0; j < 4; ++j) xr[j] = ldg16(a.xn + (int64_t)b * kH + (lane + 64 * j) * 8);
   float ag[RPW], au[RPW];
 #pragma unroll
   for (int r = 0; r < RPW; ++r) ag[r] = au[r] = 0.f;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const float* xl = &xs[(lane + 64 * j) * 8];
+    float xl[8];
+    unpack8(xr[j], xl);
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
       ag[r] += dot8(wg[r][j], xl);
