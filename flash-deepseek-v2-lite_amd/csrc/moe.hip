@@ -244,6 +244,12 @@ __device__ __forceinline__ int route_expert(const RouteGateupArgs& a, int b, int
   return e;
 }
 
+// Slot of a row's route r (grid order): with the shared halves (nr = 8) they come first, so
+// their workgroups -- which need no routing -- are dispatched first and stream their weights
+// while the routed ones still wait for the router logits (a launch's workgroups are dispatched
+// over ~1.7 us at bsz=1).
+__device__ __forceinline__ int route_slot(int r, int nr) { return nr > kTopK ? (r + kTopK) % nr : r; }
+
 // 6 waves per SIMD: all 1408 workgroups of a bsz=1 launch (8 routes x 176) resident together.
 // Every wave finds its route's expert itself and requests its weight rows at once (the shared
 // halves' workgroups at entry), then each lane reads x for its own K chunks (as bf16, from L2
@@ -253,7 +259,7 @@ template <int RPW>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) void route_gateup_kernel(
     const RouteGateupArgs a) {
   const int bx = blockIdx.x % a.gu_blocks, route = blockIdx.x / a.gu_blocks;
-  const int b = route / a.nr, s = route % a.nr;
+  const int b = route / a.nr, s = route_slot(route % a.nr, a.nr);
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int i0 = (bx * 4 + wv) * RPW;
   if (i0 >= a.inter) return;  // inter % RPW == 0: a live wave owns RPW whole rows
@@ -317,7 +323,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     const RouteGateupArgs a) {
   __shared__ float xs[kH];
   const int bx = blockIdx.x % a.gu_blocks, route = blockIdx.x / a.gu_blocks;
-  const int b = route / a.nr, s = route % a.nr;
+  const int b = route / a.nr, s = route_slot(route % a.nr, a.nr);
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int i0 = (bx * 4 + wv) * RPW;
   const bool live = i0 < a.inter;  // inter % RPW == 0: a live wave owns RPW whole rows
