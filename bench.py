@@ -114,7 +114,7 @@ def time_dominant_kernel(eng, family: str, reps: int = 4) -> dict:
                  ptr(b.ids32), ptr(b.wts), ptr(L.w_gu8), ptr(L.gu_scale), ptr(L.sh_gu8), ptr(L.sh_gu_scale),
                  c.moe_inter, ptr(b.hbuf), stream_ptr())
     elif family == "small":
-        name = "route_gateup_kernel<2> (small-family MoE gate_up+SwiGLU, 6 routed + 2 shared halves)"
+        name = "route_gateup_kernel<2, 2> (small-family MoE gate_up+SwiGLU, 6 routed + 2 shared halves)"
         bytes_per = n_small * 2 * c.moe_inter * c.hidden * 2 + B * 8 * c.moe_inter * 2
 
         def launch(L):

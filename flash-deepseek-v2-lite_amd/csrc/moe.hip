@@ -250,18 +250,18 @@ __device__ __forceinline__ int route_expert(const RouteGateupArgs& a, int b, int
 // over ~1.7 us at bsz=1).
 __device__ __forceinline__ int route_slot(int r, int nr) { return nr > kTopK ? (r + kTopK) % nr : r; }
 
-// 6 waves per SIMD: all 1408 workgroups of a bsz=1 launch (8 routes x 176) resident together.
+// 6 waves per SIMD: all workgroups of a bsz=1 launch (8 routes x 1408 / (2 NWV)) resident together.
 // Every wave finds its route's expert itself and requests its weight rows at once (the shared
 // halves' workgroups at entry), then each lane reads x for its own K chunks (as bf16, from L2
 // / L1) instead of a copy staged in LDS: no LDS and no barrier, so nothing holds a wave's
 // weight requests behind the other waves.
-template <int RPW>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) void route_gateup_kernel(
+template <int RPW, int NWV>
+__global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(6, 8))) void route_gateup_kernel(
     const RouteGateupArgs a) {
   const int bx = blockIdx.x % a.gu_blocks, route = blockIdx.x / a.gu_blocks;
   const int b = route / a.nr, s = route_slot(route % a.nr, a.nr);
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int i0 = (bx * 4 + wv) * RPW;
+  const int i0 = (bx * NWV + wv) * RPW;
   if (i0 >= a.inter) return;  // inter % RPW == 0: a live wave owns RPW whole rows
   const int e = route_expert(a, b, s, bx == 0 && s == 0 && wv == 0, lane);
   const bf16_t *gp, *up;
@@ -284,7 +284,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) voi
       wu[r][j] = ldg16_nt(up + (int64_t)r * kH + (lane + 64 * j) * 8);
     }
   // x after the weight requests (held across them it would not fit the 80 registers that
-  // keep all 1408 workgroups resident)
+  // keep every workgroup of the launch resident)
   uint4 xr[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) xr[j] = ldg16(a.xn + (int64_t)b * kH + (lane + 64 * j) * 8);
@@ -398,10 +398,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 static int launch_route_gateup(RouteGateupArgs& a, int rows, hipStream_t st, const char* what) {
   constexpr int RPW = kGateRPW;
   DSV2_REQUIRE(a.inter % RPW == 0, DSV2_E_SHAPE, "%s: inter %% %d required", what, RPW);
-  a.gu_blocks = (a.inter + 4 * RPW - 1) / (4 * RPW);
+  // 2-wave workgroups (2,816 at bsz=1; MI355X, C1 step: 1.3629 -> 1.3568 ms against 4 waves,
+  // 1.401 with 8, 1.459 with 16, 1.400 with 1)
+  constexpr int NWV = 2;
+  a.gu_blocks = (a.inter + NWV * RPW - 1) / (NWV * RPW);
   const int64_t grid = (int64_t)rows * a.nr * a.gu_blocks;
   DSV2_REQUIRE(grid <= 0x7fffffff, DSV2_E_SHAPE, "%s: too many rows", what);
-  hipLaunchKernelGGL(route_gateup_kernel<RPW>, dim3((unsigned)grid), dim3(256), 0, st, a);
+  hipLaunchKernelGGL((route_gateup_kernel<RPW, NWV>), dim3((unsigned)grid), dim3(64 * NWV), 0, st, a);
   return dsv2_launch_status(what);
 }
 
