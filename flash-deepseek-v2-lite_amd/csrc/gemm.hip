@@ -11,6 +11,7 @@
 // (or the MoE tile table).  Groups are experts (MoE), heads (MLA absorption) or one
 // dense matrix.
 #include "common.h"
+#include "mla_rows.h"
 
 struct GemmArgs {
   const bf16_t* X;
@@ -988,17 +989,18 @@ struct OsShape {
   int rbw, kw, row_blocks, tiles, groups, nwg;
 };
 
+// bid: the workgroup's index in the launch's gemm_os part (blockIdx.x for gemm_os_kernel)
 template <int TB, bool SWIGLU, int J>
-__global__ __launch_bounds__(1024) void gemm_os_kernel(const GemmArgs a, const OsShape sh) {
+__device__ __forceinline__ void gemm_os_body(const GemmArgs& a, const OsShape& sh, int bid) {
   constexpr int R = SWIGLU ? 2 : 1;
   constexpr int AROW = 136;  // LDS tile row (128 k + 8 pad), elements
   // dynamic LDS, os_lds_bytes(): per wave a 16 x AROW tile, reused for the partial tiles
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int li = lane & 15, kg = lane >> 4;
-  // XCD-aware work index: XCD x = blockIdx.x % 8 takes work items [x*per, (x+1)*per)
+  // XCD-aware work index: XCD x = bid % 8 takes work items [x*per, (x+1)*per)
   const int per = sh.nwg / 8;
-  const int w = (blockIdx.x % 8) * per + blockIdx.x / 8;
+  const int w = (bid % 8) * per + bid / 8;
   const int total = sh.row_blocks * sh.tiles * sh.groups;
   if (w >= total) return;
   const int tile = w % sh.tiles, rbg = w / sh.tiles;  // tiles of one row block are adjacent
@@ -1100,6 +1102,11 @@ __global__ __launch_bounds__(1024) void gemm_os_kernel(const GemmArgs a, const O
     for (int e = 0; e < 4; ++e) v[e] = SWIGLU ? swiglu_bf(sum[0][e], sum[R - 1][e]) : acc_out(a, sum[0][e]);
     gemm_store4(a, g, start + tb * 16 + li, (rblk * sh.rbw + urb) * 16 + 4 * kg, v);
   }
+}
+
+template <int TB, bool SWIGLU, int J>
+__global__ __launch_bounds__(1024) void gemm_os_kernel(const GemmArgs a, const OsShape sh) {
+  gemm_os_body<TB, SWIGLU, J>(a, sh, blockIdx.x);
 }
 
 // Shape of a one-shot launch for an implicit-tile GEMM, or rbw = 0 if it does not apply.
@@ -1322,6 +1329,69 @@ extern "C" int dsv2_gemm_bf16(const void* x, int64_t x_stride, int64_t x_gstride
   const int64_t grid_y = (int64_t)a.tiles_per_group * n_groups;
   DSV2_REQUIRE(grid_y <= 65535, DSV2_E_SHAPE, "gemm: too many row tiles (%lld)", (long long)grid_y);
   return launch_gemm(a, tb, swiglu, (int)grid_y, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------
+// Batch-family decode preparation in one launch: the absorbed queries
+// q_lat[r, h, :512] = W_UK_h^T q_nope[r, h] (16 head groups, K = 128, N = 512: the one-shot
+// GEMM's workgroups, with the shape and arithmetic dsv2_gemm_bf16 gives this product) and
+// mla_prepare's per-row work (RoPE(q_pe), the token's new cache row), two rows per workgroup,
+// after them.  Both parts only read qkva and write disjoint columns of q_out (and the cache),
+// so they need no ordering: one launch instead of two dependent ones.
+// ---------------------------------------------------------------------------
+template <int TB>
+__global__ __launch_bounds__(512) void mla_prepare_qlat_kernel(const GemmArgs a, const OsShape sh,
+                                                               const MlaRowArgs m) {
+  if ((int)blockIdx.x < sh.nwg) {
+    gemm_os_body<TB, false, 1>(a, sh, blockIdx.x);
+    return;
+  }
+  const int b = ((int)blockIdx.x - sh.nwg) * 2 + (int)(threadIdx.x >> 8);
+  if (b < a.rows) mla_prepare_row(m, b, threadIdx.x & 255);
+}
+
+extern "C" int dsv2_mla_prepare_qlat(const void* qkva, int64_t qkva_stride, int rows, const int32_t* pos,
+                                     const int64_t* base, const int32_t* cap, const void* kv_norm_w, float eps,
+                                     const void* rope_cos, const void* rope_sin, int max_pos, const void* w_ukt,
+                                     void* cache, void* q_out, int32_t* status, void* stream) {
+  DSV2_REQUIRE(qkva && pos && base && cap && kv_norm_w && rope_cos && rope_sin && w_ukt && cache && q_out,
+               DSV2_E_NULL, "mla_prepare_qlat: null pointer");
+  DSV2_REQUIRE(rows >= 0 && rows <= 65535 && max_pos > 0 && qkva_stride >= 3648, DSV2_E_SHAPE,
+               "mla_prepare_qlat: bad shape");
+  DSV2_REQUIRE(dsv2_aligned16(qkva) && qkva_stride % 8 == 0 && dsv2_aligned16(kv_norm_w) && dsv2_aligned16(cache) &&
+                   dsv2_aligned16(q_out) && dsv2_aligned16(w_ukt),
+               DSV2_E_ALIGN, "mla_prepare_qlat: alignment");
+  if (rows == 0) return DSV2_OK;
+  constexpr int kHeadsQ = 16, kRowQ = 576, kLatQ = 512, kNopeQ = 128;
+  GemmArgs a{};
+  a.X = (const bf16_t*)qkva;  // q_nope of head g: columns 192 g .. 192 g + 127
+  a.xs = qkva_stride;
+  a.xg = 192;
+  a.slot_div = 1;
+  a.rows = rows;
+  const int tb = rows <= 64 ? 1 : 2;  // dsv2_gemm_bf16's token tile for K <= 512
+  a.tiles_per_group = (rows + 16 * tb - 1) / (16 * tb);
+  a.W = (const bf16_t*)w_ukt;  // [16][512][128]
+  a.wg = (int64_t)kLatQ * kNopeQ;
+  a.N = kLatQ;
+  a.K = kNopeQ;
+  a.Y = q_out;
+  a.ys = kHeadsQ * kRowQ;
+  a.yg = kRowQ;
+  int j = 0;
+  const OsShape sh = os_shape(a, tb, false, kHeadsQ, &j, 8);
+  DSV2_REQUIRE(sh.rbw * sh.kw == 8 && j == 1, DSV2_E_SHAPE, "mla_prepare_qlat: unexpected GEMM shape");
+  const MlaRowArgs m{(const bf16_t*)qkva, qkva_stride, pos, base, cap, (const bf16_t*)kv_norm_w, eps,
+                     (const bf16_t*)rope_cos, (const bf16_t*)rope_sin, max_pos, (bf16_t*)cache, (bf16_t*)q_out,
+                     status};
+  const dim3 grid(sh.nwg + (rows + 1) / 2);
+  if (tb == 1)
+    hipLaunchKernelGGL(mla_prepare_qlat_kernel<1>, grid, dim3(512), os_lds_bytes(sh, 1, false), (hipStream_t)stream,
+                       a, sh, m);
+  else
+    hipLaunchKernelGGL(mla_prepare_qlat_kernel<2>, grid, dim3(512), os_lds_bytes(sh, 2, false), (hipStream_t)stream,
+                       a, sh, m);
+  return dsv2_launch_status("mla_prepare_qlat");
 }
 
 static int tile_tb(int tile_tokens) { return tile_tokens == 16 ? 1 : (tile_tokens == 32 ? 2 : 4); }

@@ -9,6 +9,7 @@
 //             dimension), V^T fragments by transposed LDS reads
 //   combine : log-sum-exp merge of the splits, then W_UV (fused GEMV) or bf16 o_lat
 #include "common.h"
+#include "mla_rows.h"
 
 namespace {
 constexpr int kHeads = 16;
@@ -19,14 +20,6 @@ constexpr int kTile = 32;       // tokens per LDS tile
 constexpr int kLdsRow = kRow + 8;  // padded LDS row (elements): 1168 bytes
 constexpr int kTileChunks = kTile * kRow / 8;  // 16-byte chunks per tile = 2304
 }  // namespace
-
-// RoPE on de-interleaved pairs: out[t] = e*cos[t] - o*sin[t], out[32+t] = o*cos[32+t] + e*sin[32+t]
-// (e, o = x[2t], x[2t+1]); lanes 0..31 each produce one pair.  fp32 math, one bf16 round.
-__device__ __forceinline__ void rope_pair(const bf16_t* x, const bf16_t* cs, const bf16_t* sn, bf16_t* out, int t) {
-  const float e = bf2f(x[2 * t]), o = bf2f(x[2 * t + 1]);
-  out[t] = f2bf(e * bf2f(cs[t]) - o * bf2f(sn[t]));
-  out[32 + t] = f2bf(o * bf2f(cs[32 + t]) + e * bf2f(sn[32 + t]));
-}
 
 // Workgroup (x, y) handles rows y*RB .. y*RB+RB-1.  With w_ukt != null workgroups x < 128
 // each compute 64 of the 16*512 absorbed outputs (rows of W_UK_h^T, K = 128 split over 16
@@ -120,39 +113,8 @@ __global__ __launch_bounds__(256) void mla_prepare_kernel(const bf16_t* __restri
     asm volatile("" ::"v"(acc));
     return;
   }
-  for (int r = 0; r < nr; ++r) {
-    const int b = b0 + r;
-    int p = pos[b];
-    p = p < 0 ? 0 : (p >= max_pos ? max_pos - 1 : p);
-    const bf16_t* q = qkva + b * qs;
-    const bf16_t* cs = cosT + (int64_t)p * 64;
-    const bf16_t* sn = sinT + (int64_t)p * 64;
-    // RoPE(q_pe) of the 16 heads: 512 (head, pair) items over 256 threads
-    for (int it = tid; it < kHeads * 32; it += 256) {
-      const int h = it >> 5, t = it & 31;
-      rope_pair(q + h * 192 + 128, cs, sn, qout + ((int64_t)b * kHeads + h) * kRow + kLat, t);
-    }
-    if (wv == 0) {
-      float f[8], g[8];
-      unpack8(ldg16(q + 3072 + lane * 8), f);
-      float ss = 0.f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(f[i], f[i], ss);
-      ss = wave_sum(ss);
-      const float rs = rsqrtf(ss / static_cast<float>(kLat) + eps);
-      unpack8(ldg16(kvw + lane * 8), g);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) f[i] = g[i] * rbf(f[i] * rs);
-      // a position outside [0, cap) would land in another row's slots: skip it and flag
-      if (pos[b] < 0 || pos[b] >= cap[b]) {
-        if (lane == 0 && status) atomicOr(status, DSV2_DEVERR_CACHE_FULL);
-        continue;
-      }
-      bf16_t* crow = cache + (base[b] + pos[b]) * kRow;
-      *reinterpret_cast<uint4*>(crow + lane * 8) = pack8(f);
-      if (lane < 32) rope_pair(q + 3584, cs, sn, crow + kLat, lane);
-    }
-  }
+  const MlaRowArgs m{qkva, qs, pos, base, cap, kvw, eps, cosT, sinT, max_pos, cache, qout, status};
+  for (int r = 0; r < nr; ++r) mla_prepare_row(m, b0 + r, tid);
 }
 
 // mla_prepare with absorption and the W_UV prefetch for mla_attend_kernel (dsv2_mla_spread)

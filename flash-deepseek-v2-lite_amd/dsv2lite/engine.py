@@ -347,13 +347,11 @@ class DecodeEngine:
         else:
             call("dsv2_gemm_bf16", ptr(b.xn), c.hidden, 0, R, c.hidden, ptr(L.w_qkva), 0, c.qkva_dim, 1, None, 0,
                  ptr(b.qkva), c.qkva_dim, 0, 0, st)
-            call("dsv2_mla_prepare", ptr(b.qkva), c.qkva_dim, R, ptr(pos), ptr(base), ptr(cap), ptr(L.kv_norm),
-                 c.eps, ptr(self.cos), ptr(self.sin), self.max_pos, None, ptr(cache), ptr(b.q),
-                 ptr(self.cache.status), st)
-            # q_lat[r, h, :512] = W_UK_h^T q_nope[r, h]: 16 head groups, K = 128
-            call("dsv2_gemm_bf16", ptr(b.qkva), c.qkva_dim, c.q_head, R, c.qk_nope, ptr(L.w_ukt),
-                 c.kv_rank * c.qk_nope, c.kv_rank, c.n_heads, None, 0, ptr(b.q), c.n_heads * c.cache_row,
-                 c.cache_row, 0, st)
+            # kv-norm + RoPE + cache write, and q_lat[r, h, :512] = W_UK_h^T q_nope[r, h] (16 head
+            # groups, K = 128, on MFMA) in one launch
+            call("dsv2_mla_prepare_qlat", ptr(b.qkva), c.qkva_dim, R, ptr(pos), ptr(base), ptr(cap),
+                 ptr(L.kv_norm), c.eps, ptr(self.cos), ptr(self.sin), self.max_pos, ptr(L.w_ukt), ptr(cache),
+                 ptr(b.q), ptr(self.cache.status), st)
         if family == "batch" and b.max_splits == 1:
             # one split per row (~256+ rows fill the GPU): normalised o_lat straight from the decode
             call("dsv2_mla_decode_rows", ptr(b.q), ptr(cache), ptr(base), ptr(pos), ptr(cap), R, self.scale,

@@ -45,6 +45,7 @@ _SIGS = {
     "dsv2_lm_head_argmax_bf16_noalloc": ([_p, _i64, _i32, _p, _i32, _p, _f32, _p, _p, _p, _p], _i32),
     "dsv2_gemm_bf16": ([_p, _i64, _i64, _i32, _i32, _p, _i64, _i32, _i32, _p, _i64, _p, _i64, _i64, _i32, _p], _i32),
     "dsv2_mla_prepare": ([_p, _i64, _i32, _p, _p, _p, _p, _f32, _p, _p, _i32, _p, _p, _p, _p, _p], _i32),
+    "dsv2_mla_prepare_qlat": ([_p, _i64, _i32, _p, _p, _p, _p, _f32, _p, _p, _i32, _p, _p, _p, _p, _p], _i32),
     "dsv2_mla_decode": ([_p, _p, _p, _p, _p, _i32, _i32, _i32, _f32, _p, _p, _p], _i32),
     "dsv2_mla_combine": ([_p, _p, _p, _p, _i32, _i32, _i32, _p, _p, _i64, _p], _i32),
     "dsv2_mla_decode_rows": ([_p, _p, _p, _p, _p, _i32, _f32, _p, _i64, _p], _i32),

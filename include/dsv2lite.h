@@ -163,8 +163,8 @@ int dsv2_gemm_bf16(const void* x, int64_t x_stride, int64_t x_gstride, int rows,
  *   c = RMSNorm(qkva[r, 3072:3584]; kv_norm_w) -> cache[slot, 0:512]
  *   k_pe = RoPE(qkva[r, 3584:3648], pos)      -> cache[slot, 512:576]
  *   q_out[r, h, 512:576] = RoPE(q_pe_h);  q_out[r, h, 0:512] = W_UK_h^T q_nope_h
- *     (only when w_ukt != NULL: W_UK transposed, [16, 512, 128]; the batch family runs the
- *     absorption as a grouped GEMM instead).
+ *     (only when w_ukt != NULL: W_UK transposed, [16, 512, 128], as a per-row GEMV; the batch
+ *     family runs the absorption on MFMA in dsv2_mla_prepare_qlat).
  * RoPE rotates de-interleaved pairs with bf16 cos/sin tables [max_pos, 64].
  * Replaces kv-norm + _batched_build_qkv_rope_kernel + _cache_write_q1_dual_kernel
  * (attention_decode_batch.py:719-813; attention_decode_small.py:141-339). */
@@ -172,6 +172,18 @@ int dsv2_mla_prepare(const void* qkva, int64_t qkva_stride, int rows, const int3
                      const int64_t* base, const int32_t* cap, const void* kv_norm_w, float eps, const void* rope_cos,
                      const void* rope_sin, int max_pos, const void* w_ukt, void* cache, void* q_out,
                      int32_t* status, void* stream);
+
+/* dsv2_mla_prepare with w_ukt (required here) in one launch for the batch family: the same
+ * outputs, bit for bit, as dsv2_mla_prepare(..., w_ukt = NULL, ...) followed by the grouped
+ * absorption dsv2_gemm_bf16(qkva, qkva_stride, 192, rows, 128, w_ukt, 512 * 128, 512, 16,
+ * NULL, 0, q_out, 16 * 576, 576, 0) -- the absorption's MFMA workgroups and the per-row
+ * RoPE / cache workgroups run side by side (they read only qkva and write disjoint outputs).
+ * Replaces the q absorption of attention_decode_batch.py:726-745 together with the kv-norm,
+ * RoPE and cache write of :719-813. */
+int dsv2_mla_prepare_qlat(const void* qkva, int64_t qkva_stride, int rows, const int32_t* pos,
+                          const int64_t* base, const int32_t* cap, const void* kv_norm_w, float eps,
+                          const void* rope_cos, const void* rope_sin, int max_pos, const void* w_ukt, void* cache,
+                          void* q_out, int32_t* status, void* stream);
 
 /* Split-KV absorbed-MLA decode over the compressed cache [*, 576] bf16.
  * Row r attends cache rows base[r] .. base[r]+min(pos[r], cap[r]-1) (inclusive); split s covers

@@ -45,6 +45,8 @@ def test_abi_rejects_bad_arguments_without_launching():
         _hip.call("dsv2_mla_decode", 16, 16, 16, 16, None, 1, 32, 4, 0.1, 16, 16, None)
     with pytest.raises(_hip.HipKernelError, match="null pointer"):
         _hip.call("dsv2_mla_prepare", 16, 3648, 1, 16, 16, None, 16, 1e-6, 16, 16, 64, None, 16, 16, None, None)
+    with pytest.raises(_hip.HipKernelError, match="null pointer"):  # the absorption weights are required
+        _hip.call("dsv2_mla_prepare_qlat", 16, 3648, 1, 16, 16, 16, 16, 1e-6, 16, 16, 64, None, 16, 16, None, None)
     with pytest.raises(_hip.HipKernelError, match="rows\\*6"):
         _hip.call("dsv2_moe_bucket", 16, 8193, 32, 16, 16, 16, 16, None)
 

@@ -755,6 +755,49 @@ def test_mla_prepare_vs_oracle(B):
     assert torch.all(cache.cpu()[mask] == 0)
 
 
+@pytest.mark.parametrize("B", [1, 5, 64, 65, 300])
+def test_mla_prepare_qlat_matches_two_launches(B):
+    """The batch family's one-launch preparation equals, bit for bit, mla_prepare without
+    absorption followed by the 16-group absorption GEMM it replaces (both token tiles: 16
+    rows up to 64, 32 above), including a row whose position is past its capacity (skipped,
+    status flagged) and positions past the RoPE table (clamped)."""
+    from dsv2lite.config import DSV2Config
+    from dsv2lite.rope import cos_sin_tables
+
+    cfg = DSV2Config()
+    qkva = rnd(B, 3648, seed=170)
+    kvw = (rnd(512, seed=171, std=0.1) + 1).to(BF)
+    w_ukt = rnd(16, 512, 128, std=0.05, seed=172)
+    cos, sin = cos_sin_tables(cfg, 1024, device=DEV)
+    g = torch.Generator().manual_seed(B)
+    pos = torch.randint(0, 1200, (B,), generator=g, dtype=torch.int32)
+    cap = torch.full((B,), 1300, dtype=torch.int32)
+    cap[B // 2] = int(pos[B // 2])  # full row: skipped, flagged
+    base = torch.arange(B, dtype=torch.int64) * 1300
+    pos, cap, base = pos.to(DEV), cap.to(DEV), base.to(DEV)
+    outs = []
+    for fused in (False, True):
+        cache = torch.zeros(B * 1300, 576, dtype=BF, device=DEV)
+        q = torch.full((B, 16, 576), float("nan"), dtype=BF, device=DEV)
+        status = torch.zeros(1, dtype=torch.int32, device=DEV)
+        args = (qkva.data_ptr(), 3648, B, pos.data_ptr(), base.data_ptr(), cap.data_ptr(), kvw.data_ptr(), 1e-6,
+                cos.data_ptr(), sin.data_ptr(), 1024)
+        if fused:
+            call("dsv2_mla_prepare_qlat", *args, w_ukt.data_ptr(), cache.data_ptr(), q.data_ptr(),
+                 status.data_ptr(), st())
+        else:
+            call("dsv2_mla_prepare", *args, None, cache.data_ptr(), q.data_ptr(), status.data_ptr(), st())
+            call("dsv2_gemm_bf16", qkva.data_ptr(), 3648, 192, B, 128, w_ukt.data_ptr(), 512 * 128, 512, 16, None, 0,
+                 q.data_ptr(), 16 * 576, 576, 0, st())
+        torch.cuda.synchronize()
+        outs.append((cache, q, status.item()))
+    (c0, q0, s0), (c1, q1, s1) = outs
+    assert s0 == s1 and s0 != 0
+    assert torch.equal(c0, c1)
+    assert not torch.isnan(q1.float()).any()
+    assert torch.equal(q0.view(torch.int16), q1.view(torch.int16))
+
+
 def test_argmax_first_max_and_position_step():
     lg = torch.randn(3, 102400, device=DEV)
     lg[1, 777] = 50.0
