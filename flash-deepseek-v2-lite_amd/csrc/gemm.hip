@@ -1158,7 +1158,9 @@ static int launch_gemm_xlds(const GemmArgs& a, int tb, bool swiglu, int grid_y, 
   // chunks; SwiGLU with 2+ token blocks takes 64 features (4 blocks x 2 k ranges) so each
   // token chunk in LDS serves twice the weight rows (bsz=256 gate_up 178 -> 140 us); with
   // 32-token tiles also non-temporal weight loads and two token chunks in flight (140 ->
-  // 130 us; the same loads measured slower for 16-token tiles and for the down projection).
+  // 130 us; the same loads measured slower for 16-token tiles).  The down projection on
+  // 32-token tiles takes the two token chunks in flight with ordinary weight loads (bsz=64
+  // grouped down + shared halves 72.3 -> 67.8 us; with non-temporal loads 68.2).
   const bool wide = a.N % 64 == 0;
   if (swiglu) {
     if (tb == 1) launch_xlds_variant<1, true, 4, true, 2>(a, grid_y, st);
@@ -1168,7 +1170,7 @@ static int launch_gemm_xlds(const GemmArgs& a, int tb, bool swiglu, int grid_y, 
     else launch_xlds_variant<4, true, 2, false, 2>(a, grid_y, st);
   } else {
     if (tb == 1) launch_xlds_variant<1, false, 4, true, 2>(a, grid_y, st);
-    else if (tb == 2) launch_xlds_variant<2, false, 4, true, 2>(a, grid_y, st);
+    else if (tb == 2) launch_xlds_variant<2, false, 4, true, 2, 4, 2>(a, grid_y, st);
     else if (tb == 4) launch_xlds_variant<4, false, 4, false, 2>(a, grid_y, st);
     else launch_xlds_variant<8, false, 2, false, 2>(a, grid_y, st);
   }
