@@ -49,8 +49,17 @@ def pack_attention_weights(attn: torch.nn.Module) -> AttentionPackedWeights:
                                   attn.o_proj.weight.detach().contiguous())
 
 
+# caches up to this many tokens per row take one split per row: the engine then runs the
+# one-launch decode (dsv2_mla_decode_rows) and no split merge
+ONE_SPLIT_MAX_CTX = 256
+
+
 def plan_splits(rows: int, max_ctx: int, target_wgs: int = 256) -> tuple[int, int]:
-    """(split_tokens, max_splits) for the split-KV decode: about target_wgs workgroups,
+    """(split_tokens, max_splits) for the split-KV decode: one split per row for caches of at
+    most ONE_SPLIT_MAX_CTX tokens (measured on MI355X, whole decode steps, against the
+    multi-split plan below: bsz=64 x 57-token caches 2.809 -> 2.726 ms, bsz=64 x 233 6.958 ->
+    6.901, bsz=128 x 233 7.941 -> 7.832; at 433 tokens one split loses, 7.013 -> 7.101);
+    else about target_wgs workgroups,
     split_tokens a multiple of 32, at most 64 splits per row.  256 = one workgroup per CU;
     each streams its split with two tiles in flight.  Measured on MI355X over the whole
     decode step against 512: bsz=256 x 2048-token prompts 22.72k vs 22.44k tok/s, bsz=64 x
@@ -59,6 +68,8 @@ def plan_splits(rows: int, max_ctx: int, target_wgs: int = 256) -> tuple[int, in
     layer) are slower.  Rows of very unequal lengths want more, shorter splits (bsz=128 x
     U[256,8192]: 512 -> 2048-token splits 132 us, 256 -> 4064-token splits 171 us); capping
     the split at 2048 tokens instead cost the equal-length bsz=256 step 8%."""
+    if max_ctx <= ONE_SPLIT_MAX_CTX:
+        return max(32, math.ceil(max_ctx / 32) * 32), 1
     per_row = max(1, min(64, math.ceil(target_wgs / max(rows, 1))))
     split = max(32, math.ceil(math.ceil(max_ctx / per_row) / 32) * 32)
     split = max(split, math.ceil(max_ctx / 64 / 32) * 32)
