@@ -18,7 +18,6 @@ constexpr int kLat = 512;       // latent part
 constexpr int kQkvA = 3648;     // q (16*192) | latent (512) | k_pe (64)
 constexpr int kTile = 32;       // tokens per LDS tile
 constexpr int kLdsRow = kRow + 8;  // padded LDS row (elements): 1168 bytes
-constexpr int kTileChunks = kTile * kRow / 8;  // 16-byte chunks per tile = 2304
 }  // namespace
 
 // Workgroup (x, y) handles rows y*RB .. y*RB+RB-1.  With w_ukt != null workgroups x < 128
@@ -39,7 +38,7 @@ __global__ __launch_bounds__(256) void mla_prepare_kernel(const bf16_t* __restri
                                                           bf16_t* __restrict__ qout, int32_t* __restrict__ status,
                                                           const bf16_t* __restrict__ w_uv_pf) {
   constexpr int RB = ABSORB ? 8 : 1;  // RoPE/cache only: one row per workgroup
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int tid = threadIdx.x;
   const int b0 = blockIdx.y * RB;
   const int nr = min(RB, rows - b0);
   if (ABSORB && blockIdx.x < 128) {
