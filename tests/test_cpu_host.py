@@ -82,14 +82,16 @@ def test_product_rope_and_scale_match_oracle():
     assert cfg.qkva_dim == 3648 and cfg.cache_row == 576
 
 
-@pytest.mark.parametrize("rows,ctx", [(1, 10), (1, 236), (64, 1130), (256, 2160), (128, 8200), (1024, 2176),
-                                      (3, 100000)])
+@pytest.mark.parametrize("rows,ctx", [(1, 10), (1, 236), (64, 57), (64, 256), (64, 257), (64, 1130), (256, 2160),
+                                      (128, 8200), (1024, 2176), (3, 100000)])
 def test_plan_splits(rows, ctx):
     from dsv2lite.engine import plan_splits
 
     split, ns = plan_splits(rows, ctx)
     assert split % 32 == 0 and 1 <= ns <= 64
     assert split * ns >= ctx and split * (ns - 1) < ctx
+    if ctx <= 256:  # short caches: one split per row (the one-launch decode, no merge)
+        assert ns == 1
 
 
 def test_moe_tile_choice_and_cache_layout():
