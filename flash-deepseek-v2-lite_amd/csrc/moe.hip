@@ -1006,30 +1006,48 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const bf16_t* __restri
                                                           bf16_t* __restrict__ xn) {
   __shared__ float red[4];
   const int b = blockIdx.x, tid = threadIdx.x;
+  // every operand is requested up front -- an absent one reads the start of ys instead and is
+  // not used -- and the six expert rows right after their positions: two dependent round
+  // trips per row instead of one per operand
+  const bf16_t* shp = shared ? shared + (int64_t)b * kH : ys;
+  const float* sp0 = shared_parts ? shared_parts + (int64_t)b * kH : reinterpret_cast<const float*>(ys);
+  const float* sp1 = shared_parts ? shared_parts + ((int64_t)gridDim.x + b) * kH : reinterpret_cast<const float*>(ys);
+  const bf16_t* rsp = res ? res + (int64_t)b * kH : ys;
+  const bf16_t* nwp = nw ? nw : ys;
+  int pr[kTopK];
+  float wr[kTopK];
+#pragma unroll
+  for (int s = 0; s < kTopK; ++s) {
+    pr[s] = route_pos[b * kTopK + s];
+    wr[s] = wts[b * kTopK + s];
+  }
+  const uint4 shq = ldg16(shp + tid * 8);
+  const float4 a0 = reinterpret_cast<const float4*>(sp0 + tid * 8)[0], a1 = reinterpret_cast<const float4*>(sp0 + tid * 8)[1];
+  const float4 b0 = reinterpret_cast<const float4*>(sp1 + tid * 8)[0], b1 = reinterpret_cast<const float4*>(sp1 + tid * 8)[1];
+  const uint4 rq = ldg16(rsp + tid * 8);
+  const uint4 nq = ldg16(nwp + tid * 8);
+  uint4 yq[kTopK];
+#pragma unroll
+  for (int s = 0; s < kTopK; ++s) yq[s] = ldg16(ys + (int64_t)pr[s] * kH + tid * 8);
   float acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.f;
 #pragma unroll
   for (int s = 0; s < kTopK; ++s) {
-    const int p = route_pos[b * kTopK + s];
-    const float w = wts[b * kTopK + s];
     float f[8];
-    unpack8(ldg16(ys + (int64_t)p * kH + tid * 8), f);
+    unpack8(yq[s], f);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] += w * f[i];
+    for (int i = 0; i < 8; ++i) acc[i] += wr[s] * f[i];
   }
   float y[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) y[i] = rbf(acc[i]);
   if (shared) {
     float f[8];
-    unpack8(ldg16(shared + (int64_t)b * kH + tid * 8), f);
+    unpack8(shq, f);
 #pragma unroll
     for (int i = 0; i < 8; ++i) y[i] = rbf(y[i] + f[i]);
   } else if (shared_parts) {  // shared = bf16(half 0 + half 1), the fp32 partials of its down GEMM
-    const float4* p0 = reinterpret_cast<const float4*>(shared_parts + (int64_t)b * kH + tid * 8);
-    const float4* p1 = reinterpret_cast<const float4*>(shared_parts + ((int64_t)gridDim.x + b) * kH + tid * 8);
-    const float4 a0 = p0[0], a1 = p0[1], b0 = p1[0], b1 = p1[1];
     const float sh[8] = {a0.x + b0.x, a0.y + b0.y, a0.z + b0.z, a0.w + b0.w,
                          a1.x + b1.x, a1.y + b1.y, a1.z + b1.z, a1.w + b1.w};
 #pragma unroll
@@ -1037,7 +1055,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const bf16_t* __restri
   }
   if (res) {
     float f[8];
-    unpack8(ldg16(res + (int64_t)b * kH + tid * 8), f);
+    unpack8(rq, f);
 #pragma unroll
     for (int i = 0; i < 8; ++i) y[i] = rbf(f[i] + y[i]);
   }
@@ -1049,7 +1067,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const bf16_t* __restri
     ss = block_sum<4>(ss, red);
     const float rs = rsqrtf(ss / static_cast<float>(kH) + eps);
     float g[8];
-    unpack8(ldg16(nw + tid * 8), g);
+    unpack8(nq, g);
 #pragma unroll
     for (int i = 0; i < 8; ++i) y[i] = g[i] * rbf(y[i] * rs);
     *reinterpret_cast<uint4*>(xn + (int64_t)b * kH + tid * 8) = pack8(y);
