@@ -399,20 +399,25 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(const float* __restric
 #pragma unroll
     for (int r = 0; r < 8; ++r) wr[r] = ldg16(wp + (int64_t)r * kLat);
   }
-  // the first 8 splits' partial outputs are requested before the (m, l) merge; further
-  // splits come 8 loads at a time (split indices clamped into [0, ns), masked where used; a
-  // row with nothing cached, ns = 0, reads its first split's slot and writes zeros)
+  // every split's (m, l) pair (lane = split; wave 0 merges them), then the first 8 splits'
+  // partial outputs, all requested before the merge, so its wait covers the pairs only;
+  // further splits come 8 loads at a time (split indices clamped into [0, ns), masked where
+  // used; a row with nothing cached, ns = 0, reads its first split's slot and writes zeros)
+  const float* pm = part_ml + ((int64_t)b * max_splits * kHeads + h) * 2;
+  float2 ml = *reinterpret_cast<const float2*>(pm + (int64_t)max(min(lane, ns - 1), 0) * kHeads * 2);
   const float* po = part_o + ((int64_t)b * max_splits * kHeads + h) * kLat + 2 * tid;
   float2 pv[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j)
     pv[j] = *reinterpret_cast<const float2*>(po + (int64_t)max(min(j, ns - 1), 0) * kHeads * kLat);
+  // the pair used here, in the entry block: hipcc would otherwise sink its load into wave 0's
+  // branch, behind the partial-output loads
+  asm volatile("" : "+v"(ml.x), "+v"(ml.y));
   if (wv == 0) {
-    const float* pm = part_ml + ((int64_t)b * max_splits * kHeads + h) * 2;
-    const float m = lane < ns ? pm[(int64_t)lane * kHeads * 2] : -INFINITY;
+    const float m = lane < ns ? ml.x : -INFINITY;
     const float M = wave_max(m);
     const float w = lane < ns ? exp2f(m - M) : 0.f;
-    const float l = lane < ns ? pm[(int64_t)lane * kHeads * 2 + 1] : 0.f;
+    const float l = lane < ns ? ml.y : 0.f;
     const float Lsum = wave_sum(w * l);
     wsp[lane] = w / Lsum;
   }
