@@ -5,14 +5,6 @@
 #pragma once
 #include "common.h"
 
-// RoPE on de-interleaved pairs: out[t] = e*cos[t] - o*sin[t], out[32+t] = o*cos[32+t] + e*sin[32+t]
-// (e, o = x[2t], x[2t+1]); lanes 0..31 each produce one pair.  fp32 math, one bf16 round.
-__device__ __forceinline__ void rope_pair(const bf16_t* x, const bf16_t* cs, const bf16_t* sn, bf16_t* out, int t) {
-  const float e = bf2f(x[2 * t]), o = bf2f(x[2 * t + 1]);
-  out[t] = f2bf(e * bf2f(cs[t]) - o * bf2f(sn[t]));
-  out[32 + t] = f2bf(o * bf2f(cs[32 + t]) + e * bf2f(sn[32 + t]));
-}
-
 struct MlaRowArgs {
   const bf16_t* qkva;  // [rows, qs]: q (16 x 192: 128 nope + 64 pe) | latent (512) | k_pe (64)
   int64_t qs;
@@ -31,37 +23,64 @@ struct MlaRowArgs {
 
 // Row b on 256 threads t = 0..255 (t < 64: one whole wave, for the latent's norm).  A position
 // outside [0, cap) would land in another row's cache slots: the row is skipped and the status
-// word flagged.
+// word flagged.  Two dependent load round trips: the position with every operand that does not
+// depend on it, then the cos / sin entries at that position (thread t's two (head, pair) items
+// and, for t < 32, k_pe's pair t share the same four).  RoPE on de-interleaved pairs:
+// out[i] = e cos[i] - o sin[i], out[32 + i] = o cos[32 + i] + e sin[32 + i] with (e, o) =
+// (x[2i], x[2i + 1]), fp32 math, one bf16 round.
 __device__ __forceinline__ void mla_prepare_row(const MlaRowArgs& m, int b, int t) {
   constexpr int kHeadsR = 16, kRowR = 576, kLatR = 512;
-  int p = m.pos[b];
-  p = p < 0 ? 0 : (p >= m.max_pos ? m.max_pos - 1 : p);
+  const int pb = m.pos[b], cb = m.cap[b];
+  const int64_t bb = m.base[b];
   const bf16_t* q = m.qkva + b * m.qs;
+  const int tt = t & 31;
+  // (head, pair) items t and t + 256: heads t >> 5 and 8 + (t >> 5), pair tt
+  uint32_t xq[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k)
+    xq[k] = *reinterpret_cast<const uint32_t*>(q + ((t + 256 * k) >> 5) * 192 + 128 + 2 * tt);
+  uint4 lat = make_uint4(0u, 0u, 0u, 0u), g4 = lat;
+  uint32_t kpe = 0u;
+  if (t < 64) {
+    lat = ldg16(q + 3072 + t * 8);
+    g4 = ldg16(m.kvw + t * 8);
+    kpe = *reinterpret_cast<const uint32_t*>(q + 3584 + 2 * tt);
+  }
+  const int p = pb < 0 ? 0 : (pb >= m.max_pos ? m.max_pos - 1 : pb);
   const bf16_t* cs = m.cosT + (int64_t)p * 64;
   const bf16_t* sn = m.sinT + (int64_t)p * 64;
-  // RoPE(q_pe) of the 16 heads: 512 (head, pair) items over 256 threads
-  for (int it = t; it < kHeadsR * 32; it += 256) {
-    const int h = it >> 5, tt = it & 31;
-    rope_pair(q + h * 192 + 128, cs, sn, m.qout + ((int64_t)b * kHeadsR + h) * kRowR + kLatR, tt);
+  const float c0 = bf2f(cs[tt]), c1 = bf2f(cs[32 + tt]), s0 = bf2f(sn[tt]), s1 = bf2f(sn[32 + tt]);
+  // RoPE(q_pe) of the 16 heads
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int h = (t + 256 * k) >> 5;
+    const float e = __uint_as_float(xq[k] << 16), o = __uint_as_float(xq[k] & 0xffff0000u);
+    bf16_t* out = m.qout + ((int64_t)b * kHeadsR + h) * kRowR + kLatR;
+    out[tt] = f2bf(e * c0 - o * s0);
+    out[32 + tt] = f2bf(o * c1 + e * s1);
   }
   if (t < 64) {
     const int lane = t;
     float f[8], g[8];
-    unpack8(ldg16(q + 3072 + lane * 8), f);
+    unpack8(lat, f);
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(f[i], f[i], ss);
     ss = wave_sum(ss);
     const float rs = rsqrtf(ss / static_cast<float>(kLatR) + m.eps);
-    unpack8(ldg16(m.kvw + lane * 8), g);
+    unpack8(g4, g);
 #pragma unroll
     for (int i = 0; i < 8; ++i) f[i] = g[i] * rbf(f[i] * rs);
-    if (m.pos[b] < 0 || m.pos[b] >= m.cap[b]) {
+    if (pb < 0 || pb >= cb) {
       if (lane == 0 && m.status) atomicOr(m.status, DSV2_DEVERR_CACHE_FULL);
       return;
     }
-    bf16_t* crow = m.cache + (m.base[b] + m.pos[b]) * kRowR;
+    bf16_t* crow = m.cache + (bb + pb) * kRowR;
     *reinterpret_cast<uint4*>(crow + lane * 8) = pack8(f);
-    if (lane < 32) rope_pair(q + 3584, cs, sn, crow + kLatR, lane);
+    if (lane < 32) {
+      const float e = __uint_as_float(kpe << 16), o = __uint_as_float(kpe & 0xffff0000u);
+      crow[kLatR + lane] = f2bf(e * c0 - o * s0);
+      crow[kLatR + 32 + lane] = f2bf(o * c1 + e * s1);
+    }
   }
 }
