@@ -54,6 +54,33 @@ struct GemmArgs {
 // accumulator, or the accumulator itself for an exact fp32 output.
 __device__ __forceinline__ float acc_out(const GemmArgs& a, float acc) { return a.exact_f32 ? acc : rbf(acc); }
 
+// The residual of outputs (slot, n .. n+3), requested by a kernel before its weight stream: a
+// load issued in the epilogue is one more dependent round trip at the end of every workgroup.
+// Without a residual (or where `use` is false) it reads X's first 8 bytes, which are unused.
+__device__ __forceinline__ uint2 gemm_res_load(const GemmArgs& a, bool use, int slot, int n) {
+  return *reinterpret_cast<const uint2*>(use && a.res ? a.res + (int64_t)slot * a.rs + n : a.X);
+}
+
+// Four consecutive outputs (features n..n+3) of token slot `slot`: the residual r2 (loaded by
+// gemm_res_load) added when the GEMM has one, then a bf16 or fp32 store.
+__device__ __forceinline__ void gemm_store4r(const GemmArgs& a, int g, int slot, int n, float* v, uint2 r2) {
+  if (a.res) {
+    v[0] = rbf(__uint_as_float(r2.x << 16) + v[0]);
+    v[1] = rbf(__uint_as_float(r2.x & 0xffff0000u) + v[1]);
+    v[2] = rbf(__uint_as_float(r2.y << 16) + v[2]);
+    v[3] = rbf(__uint_as_float(r2.y & 0xffff0000u) + v[3]);
+  }
+  const int64_t off = g * a.yg + (int64_t)slot * a.ys + n;
+  if (a.out_f32) {
+    *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.Y) + off) = make_float4(v[0], v[1], v[2], v[3]);
+  } else {
+    uint2 o;
+    o.x = pack2(v[0], v[1]);
+    o.y = pack2(v[2], v[3]);
+    *reinterpret_cast<uint2*>(reinterpret_cast<bf16_t*>(a.Y) + off) = o;
+  }
+}
+
 template <int TB, bool SWIGLU, int NW, int U>
 __global__ __launch_bounds__(NW * 64) void gemm_kernel(const GemmArgs a) {
   constexpr int R = SWIGLU ? 2 : 1;  // weight row blocks per tile (gate, up)
@@ -289,12 +316,23 @@ __global__ __launch_bounds__(512) void gemm_xlds_kernel(const GemmArgs a) {
   // loop is unrolled by DEPTH (nch is a multiple of it) so every register buffer index is a
   // constant, and no load sits behind a branch: requests past the last chunk repeat it (L2
   // hits), so the compiler's wait counts stay exact.
+  // the epilogue's residuals (k range 0's waves, token blocks tb) first: the wait for token
+  // chunk 0 before its LDS store then covers them
+  uint2 rpre[TB];
+#pragma unroll
+  for (int tb = 0; tb < TB; ++tb)
+    rpre[tb] = gemm_res_load(a, kq == 0 && !shared && tb * 16 + li < count, start + tb * 16 + li, f0 + 4 * kg);
   uint4 ab[DEPTH][CS][R], xr[XD][UPT];
 #pragma unroll
   for (int x = 0; x < XD; ++x) XL_LOAD_X(min(x, nch - 1), xr[x])
 #pragma unroll
   for (int p = 0; p + 1 < DEPTH; ++p) XL_LOAD_A(min(p, nch - 1), ab[p])
   XL_STORE_X(0, xr[0], 0)
+#pragma unroll
+  for (int tb = 0; tb < TB; ++tb) {
+    pin(rpre[tb].x);
+    pin(rpre[tb].y);
+  }
   __syncthreads();
   for (int c0 = 0; c0 < nch; c0 += DEPTH) {
 #pragma unroll
@@ -375,44 +413,13 @@ __global__ __launch_bounds__(512) void gemm_xlds_kernel(const GemmArgs a) {
       }
       continue;
     }
-    if (a.res) {
-      const uint2 r2 = *reinterpret_cast<const uint2*>(a.res + slot * a.rs + n);
-      v[0] = rbf(__uint_as_float(r2.x << 16) + v[0]);
-      v[1] = rbf(__uint_as_float(r2.x & 0xffff0000u) + v[1]);
-      v[2] = rbf(__uint_as_float(r2.y << 16) + v[2]);
-      v[3] = rbf(__uint_as_float(r2.y & 0xffff0000u) + v[3]);
-    }
-    const int64_t off = g * a.yg + (int64_t)slot * a.ys + n;
-    if (a.out_f32) {
-      *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.Y) + off) = make_float4(v[0], v[1], v[2], v[3]);
-    } else {
-      uint2 o;
-      o.x = pack2(v[0], v[1]);
-      o.y = pack2(v[2], v[3]);
-      *reinterpret_cast<uint2*>(reinterpret_cast<bf16_t*>(a.Y) + off) = o;
-    }
+    gemm_store4r(a, g, slot, n, v, rpre[tb]);
   }
 }
 
-// Four consecutive outputs (features n..n+3) of token slot `slot`: optional residual add,
-// then a bf16 or fp32 store.
+// gemm_store4r with the residual loaded at the store
 __device__ __forceinline__ void gemm_store4(const GemmArgs& a, int g, int slot, int n, float* v) {
-  if (a.res) {
-    const uint2 r2 = *reinterpret_cast<const uint2*>(a.res + slot * a.rs + n);
-    v[0] = rbf(__uint_as_float(r2.x << 16) + v[0]);
-    v[1] = rbf(__uint_as_float(r2.x & 0xffff0000u) + v[1]);
-    v[2] = rbf(__uint_as_float(r2.y << 16) + v[2]);
-    v[3] = rbf(__uint_as_float(r2.y & 0xffff0000u) + v[3]);
-  }
-  const int64_t off = g * a.yg + (int64_t)slot * a.ys + n;
-  if (a.out_f32) {
-    *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.Y) + off) = make_float4(v[0], v[1], v[2], v[3]);
-  } else {
-    uint2 o;
-    o.x = pack2(v[0], v[1]);
-    o.y = pack2(v[2], v[3]);
-    *reinterpret_cast<uint2*>(reinterpret_cast<bf16_t*>(a.Y) + off) = o;
-  }
+  gemm_store4r(a, g, slot, n, v, a.res ? *reinterpret_cast<const uint2*>(a.res + (int64_t)slot * a.rs + n) : uint2{0u, 0u});
 }
 
 // Direct-to-LDS ring shape for dense weights at 128+ tokens (the lm_head from 33) and for the
@@ -1010,6 +1017,11 @@ __device__ __forceinline__ void gemm_os_body(const GemmArgs& a, const OsShape& s
   const int K = a.K, S = K >> 5;
   const int f0 = (rblk * sh.rbw + rb) * 16;
 
+  // the residual of this wave's first output unit (u = wv below), ahead of the weight stream:
+  // the wait for the first weight chunk then covers it
+  const int u0b = wv % sh.rbw, u0t = wv / sh.rbw;
+  const uint2 rpre = gemm_res_load(a, wv < sh.rbw * TB && u0t * 16 + li < count, start + u0t * 16 + li,
+                                   (rblk * sh.rbw + u0b) * 16 + 4 * kg);
   // weight chunks: ab[j][q][r] = rows 4q + (lane >> 4) of block r, k = 128 c_j + (lane & 15) * 8
   uint4 ab[J][4][R];
 #pragma unroll
@@ -1062,6 +1074,10 @@ __device__ __forceinline__ void gemm_os_body(const GemmArgs& a, const OsShape& s
         afr[si][r] = *reinterpret_cast<const bf16x8_t*>(atile + li * AROW + si * 32 + kg * 8);
       __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     }
+    if (j == 0) {
+      pin(rpre.x);
+      pin(rpre.y);
+    }
 #pragma unroll
     for (int tb = 0; tb < TB; ++tb) {
 #pragma unroll
@@ -1100,7 +1116,11 @@ __device__ __forceinline__ void gemm_os_body(const GemmArgs& a, const OsShape& s
     float v[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) v[e] = SWIGLU ? swiglu_bf(sum[0][e], sum[R - 1][e]) : acc_out(a, sum[0][e]);
-    gemm_store4(a, g, start + tb * 16 + li, (rblk * sh.rbw + urb) * 16 + 4 * kg, v);
+    const int slot = start + tb * 16 + li, n = (rblk * sh.rbw + urb) * 16 + 4 * kg;
+    if (u == wv)
+      gemm_store4r(a, g, slot, n, v, rpre);
+    else
+      gemm_store4(a, g, slot, n, v);
   }
 }
 
