@@ -171,9 +171,23 @@ __global__ __launch_bounds__(256, 2) void mla_decode_kernel(const bf16_t* __rest
   __shared__ __attribute__((aligned(16))) bf16_t lds[2][kTile * kLdsRow];
   __shared__ floatx4_t spart[4][64];  // per-wave partial S^T (one 16-token block, half of K)
   const int s = blockIdx.x, b = blockIdx.y;
-  const int len = min(pos[b] + 1, cap[b]);  // never past the row's own slots
-  const int t_begin = s * split_tokens;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, li = lane & 15, kg = lane >> 4;
+  // S^T = K Q^T is split over the waves: wave w scores 16-token block w >> 1 of every tile
+  // over k steps [9*(w & 1), 9*(w & 1) + 9) of the 18; the pair's partials meet in LDS.
+  // Q^T fragments (B operand) of those steps: head li, dims kk*32 + kg*8 .. +8.  They depend
+  // on the row only and are requested first; the row's position, capacity and cache base
+  // then come in one round trip, ahead of the split's range check.
+  const int sblk = wv >> 1, k0 = (wv & 1) * 9;
+  bf16x8_t qf[9];
+  {
+    const bf16_t* qh = q + ((int64_t)b * kHeads + li) * kRow + kg * 8 + k0 * 32;
+#pragma unroll
+    for (int kk = 0; kk < 9; ++kk) qf[kk] = as_bf16x8(ldg16(qh + kk * 32));
+  }
+  const int pb = pos[b], cb = cap[b];
+  const int64_t bb = base[b];
+  const int len = min(pb + 1, cb);  // never past the row's own slots
+  const int t_begin = s * split_tokens;
   if (t_begin >= len) {
     if (DIRECT) {  // a row with no cached token (capacity 0): zeros, as the combine writes
 #pragma unroll
@@ -183,18 +197,7 @@ __global__ __launch_bounds__(256, 2) void mla_decode_kernel(const bf16_t* __rest
   }
   const int t_end = min(len, t_begin + split_tokens);
   const int ntiles = (t_end - t_begin + kTile - 1) / kTile;
-  const bf16_t* crow = cache + base[b] * kRow;
-
-  // S^T = K Q^T is split over the waves: wave w scores 16-token block w >> 1 of every tile
-  // over k steps [9*(w & 1), 9*(w & 1) + 9) of the 18; the pair's partials meet in LDS.
-  // Q^T fragments (B operand) of those steps: head li, dims kk*32 + kg*8 .. +8
-  const int sblk = wv >> 1, k0 = (wv & 1) * 9;
-  bf16x8_t qf[9];
-  {
-    const bf16_t* qh = q + ((int64_t)b * kHeads + li) * kRow + kg * 8 + k0 * 32;
-#pragma unroll
-    for (int kk = 0; kk < 9; ++kk) qf[kk] = as_bf16x8(ldg16(qh + kk * 32));
-  }
+  const bf16_t* crow = cache + bb * kRow;
 
   // Two register stages: tile it + 2 is requested while tile it + 1 is still in flight
   // (cache rows are read once per step: non-temporal loads, which stream ~15% faster here).
@@ -390,7 +393,8 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(const float* __restric
   __shared__ float olat[kLat];
   __shared__ float wsp[64];
   const int b = blockIdx.x, h = blockIdx.y, part = blockIdx.z, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int len = min(pos[b] + 1, cap[b]);  // the tokens dsv2_mla_decode attended
+  const int pb = pos[b], cb = cap[b];  // one round trip for both
+  const int len = min(pb + 1, cb);     // the tokens dsv2_mla_decode attended
   const int ns = min((len + split_tokens - 1) / split_tokens, max_splits);
   // W_UV rows of this workgroup (part*32 + wv*8 .. +8) are requested before the merge
   uint4 wr[8];

@@ -449,6 +449,9 @@ __global__ __launch_bounds__(512) void qkva_absorb_kernel(const bf16_t* __restri
   const int h = w / 12, blk = w % 12;
   const bool absorb = w < kQWgs && blk < kAbsBlocks;  // uniform over the workgroup
   const bf16_t* xr = x + b * xs;
+  // the row's position, capacity and cache base (for the prefetch below), in one round trip
+  const int pb = pos[b], cb = cap[b];
+  const int64_t bb = base[b];
   // entry loads, in the order they are consumed: x and the norm weights (waves 4..7 repeat
   // waves 0..3's chunks), W_UK (absorbing workgroups; the others re-read head 0's first rows,
   // an L2 hit), then the weight rows
@@ -474,9 +477,9 @@ __global__ __launch_bounds__(512) void qkva_absorb_kernel(const bf16_t* __restri
   uint4 pf[kPf];
   {
     const int slot = w >> 3;
-    const int n = min(min(max(pos[b], 0), cap[b]), 256);
+    const int n = min(min(max(pb, 0), cb), 256);
     const int nt = n > slot ? (n - 1 - slot) / kSlots + 1 : 0;
-    const bf16_t* crow0 = cache + base[b] * kRow;
+    const bf16_t* crow0 = cache + bb * kRow;
 #pragma unroll
     for (int i = 0; i < kPf; ++i) {
       const int c = tid + 512 * i;

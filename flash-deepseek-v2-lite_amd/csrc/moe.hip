@@ -759,9 +759,7 @@ constexpr int kMaxChunks = kMaxRoutes / 64;
 
 // expert of route r (kE when r is past the routes), and its rank among the lanes of its
 // 64-route chunk that hold the same expert; `last` is set on the chunk's last such lane
-__device__ __forceinline__ int route_rank(const int32_t* __restrict__ ids, int r, int R, int lane, int& e,
-                                          bool& last) {
-  e = r < R ? min(max(ids[r], 0), kE - 1) : kE;
+__device__ __forceinline__ int chunk_rank(int e, int lane, bool& last) {
   // lanes holding the same expert: intersect, over the 7 bits of e, the ballots that agree
   unsigned long long same = ~0ull;
 #pragma unroll
@@ -773,6 +771,11 @@ __device__ __forceinline__ int route_rank(const int32_t* __restrict__ ids, int r
   last = __popcll(same & ~below) == 1;
   return __popcll(same & below);
 }
+__device__ __forceinline__ int route_rank(const int32_t* __restrict__ ids, int r, int R, int lane, int& e,
+                                          bool& last) {
+  e = r < R ? min(max(ids[r], 0), kE - 1) : kE;
+  return chunk_rank(e, lane, last);
+}
 
 __global__ __launch_bounds__(1024) void bucket_kernel(const int32_t* __restrict__ ids, int R, int tile_tokens,
                                                       int32_t* __restrict__ sorted_routes,
@@ -782,12 +785,33 @@ __global__ __launch_bounds__(1024) void bucket_kernel(const int32_t* __restrict_
   __shared__ int start[kE], tstart[kE], total[kE];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int nchunks = (R + 63) / 64;
+  // a wave's chunks wv and wv + 16 (every chunk up to 2,048 routes): their ids are requested
+  // before the histogram is cleared (clamped indices; no routes: num_tiles' word, unused) and
+  // their (expert, rank) kept for the placement pass instead of being read and ranked again
+  const int32_t* idp = R > 0 ? ids : num_tiles;
+  int ek[2], bk[2] = {0, 0};
+#pragma unroll
+  for (int k = 0; k < 2; ++k) ek[k] = idp[max(min((wv + 16 * k) * 64 + lane, R - 1), 0)];
   for (int i = tid; i < nchunks * kE; i += 1024) hist[i / kE][i % kE] = 0;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    pin(ek[k]);
+    ek[k] = (wv + 16 * k) * 64 + lane < R ? min(max(ek[k], 0), kE - 1) : kE;
+  }
   __syncthreads();
   for (int c = wv; c < nchunks; c += 16) {
     int e;
     bool last;
-    const int before = route_rank(ids, c * 64 + lane, R, lane, e, last);
+    int before;
+    if (c == wv) {
+      e = ek[0];
+      before = bk[0] = chunk_rank(e, lane, last);
+    } else if (c == wv + 16) {
+      e = ek[1];
+      before = bk[1] = chunk_rank(e, lane, last);
+    } else {
+      before = route_rank(ids, c * 64 + lane, R, lane, e, last);
+    }
     if (c * 64 + lane < R && last) hist[c][e] = (uint16_t)(before + 1);
   }
   __syncthreads();
@@ -820,9 +844,17 @@ __global__ __launch_bounds__(1024) void bucket_kernel(const int32_t* __restrict_
   __syncthreads();
   for (int c = wv; c < nchunks; c += 16) {
     const int r = c * 64 + lane;
-    int e;
-    bool last;
-    const int before = route_rank(ids, r, R, lane, e, last);
+    int e, before;
+    if (c == wv) {
+      e = ek[0];
+      before = bk[0];
+    } else if (c == wv + 16) {
+      e = ek[1];
+      before = bk[1];
+    } else {
+      bool last;
+      before = route_rank(ids, r, R, lane, e, last);
+    }
     if (r < R) {
       const int p = start[e] + hist[c][e] + before;
       sorted_routes[p] = r;
