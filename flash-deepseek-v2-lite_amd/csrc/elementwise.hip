@@ -254,15 +254,26 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
   float best = -INFINITY;
   int bi = 0x7fffffff;
   const int nch = vocab >> 2;
-  for (int c = threadIdx.x; c < nch; c += 1024) {
-    const float4 v = reinterpret_cast<const float4*>(lr)[c];
-    const float vv[4] = {v.x, v.y, v.z, v.w};
+  // kU of the thread's 16-byte chunks requested together (clamped, masked where compared),
+  // then compared in index order: one load round trip per kU chunks instead of per chunk
+  constexpr int kU = 16;
+  for (int c0 = threadIdx.x; c0 < nch; c0 += 1024 * kU) {
+    float4 v[kU];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (vv[i] > best) {
-        best = vv[i];
-        bi = c * 4 + i;
-      }
+    for (int u = 0; u < kU; ++u) v[u] = reinterpret_cast<const float4*>(lr)[min(c0 + 1024 * u, nch - 1)];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) pin(__float_as_uint(v[u].x));  // all issued before the first wait
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int c = c0 + 1024 * u;
+      const float vv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (c < nch && vv[i] > best) {
+          best = vv[i];
+          bi = c * 4 + i;
+        }
+    }
   }
   for (int j = nch * 4 + threadIdx.x; j < vocab; j += 1024)
     if (lr[j] > best) {
