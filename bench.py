@@ -520,10 +520,12 @@ def bench_mla_micro(args) -> dict:
     pos = torch.tensor([n - 1 for n in lens], dtype=torch.int32, device=dev)
     cap = torch.tensor(lens, dtype=torch.int32, device=dev)
     base_d = base.to(dev)
-    # the planner with 512 workgroups, which suits these very unequal lengths (the engine's
-    # 256 suits its equal-length batches); measured on MI355X, decode kernel: split 2048 (4
-    # splits) 132 us, 4064 171 us, 1536 154 us, 1120 155 us, 1024 148 us, 768 137 us
-    split, ns = plan_splits(B, max(lens), target_wgs=512)
+    # the planner with 640 workgroups (5 splits of the longest row), which suits these very
+    # unequal lengths (the engine's 256 suits its batches: 320 and 384 made the bsz=64 step
+    # 1.5% / 0.7% slower); measured on MI355X, decode kernel: split 1664 (5 splits) 120.3 us,
+    # 1728 117.5, 1792 119.6, 1920 121.5, 2048 (4 splits) 126.5, 2304 140.5, 1536 (6 splits)
+    # 147.6, 1280 130.3, 3072 169.3
+    split, ns = plan_splits(B, max(lens), target_wgs=640)
     if args.mla_split:
         split, ns = args.mla_split, math.ceil(max(lens) / args.mla_split)
     po = torch.empty(B, ns, 16, 512, device=dev)

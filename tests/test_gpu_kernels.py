@@ -609,7 +609,7 @@ def _mla_reference(q, cache_rows, lens, scale):
                                                 (128, 256, 8192, 3, None), (128, 256, 8192, 3, "bench"),
                                                 (2, 500, 1300, 52, 1056), (3, 40, 200, 53, 128), (4, 1, 97, 54, 96)])
 def test_mla_decode_combine_vs_fp32(B, lo, hi, seed, split):
-    """Split plan of the engine, the one bench.py's config 4 times ("bench": 512 target
+    """Split plan of the engine, the one bench.py's config 4 times ("bench": 640 target
     workgroups), or a fixed one: 33 tiles (odd) / 4 tiles (even, last one partial) / 3 tiles
     per split, so both register stages and the loop exits are covered."""
     from triton_kernels.attention_decode_batch import plan_splits
@@ -626,7 +626,7 @@ def test_mla_decode_combine_vs_fp32(B, lo, hi, seed, split):
     if split is None:
         split, ns = plan_splits(B, maxL)
     elif split == "bench":  # bench.py sizes the plan by the longest row itself
-        split, _ = plan_splits(B, max(lens), target_wgs=512)
+        split, _ = plan_splits(B, max(lens), target_wgs=640)
         ns = math.ceil(maxL / split)
     else:
         ns = math.ceil(maxL / split)
